@@ -1,0 +1,204 @@
+/*
+ * tinyllm_kv.h -- C ABI of libtinyllm_kv.so, the MI355X (gfx950) KV-cache
+ * decode path of tiny-llm: per-step K/V append, block/slot gather and GQA
+ * decode attention over the cache.
+ *
+ * Plain pointers and sizes only.  fp16 tensors are passed as `void *` device
+ * pointers holding IEEE binary16 values; streams are `void *` holding a
+ * hipStream_t (NULL = the default stream).  Every `int` result is TL_OK (0) or
+ * a negative status; tl_last_error() returns the message of the last failing
+ * call on the calling thread.  Every entry point is asynchronous with respect
+ * to the host exactly where its reference counterpart is (stream-ordered
+ * device work, synchronous host bookkeeping).
+ *
+ * Reference = AICL-Lab/tiny-llm v2.0.2.  Each declaration names the reference
+ * interface it replaces (file:line).  The C++ mirror of the same API
+ * (tiny_llm::KVCacheManager, tiny_llm::kernels::attention_decode) lives in
+ * tiny-llm_amd/include/tiny_llm/ and is exported from the same library.
+ */
+#ifndef TINYLLM_KV_H
+#define TINYLLM_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TL_OK 0
+#define TL_ERR_INVALID (-1) /* host validation failed: Result::err(...) in the reference */
+#define TL_ERR_HIP (-2)     /* HIP runtime failure: CudaException via CUDA_CHECK */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *tl_last_error(void);
+
+/* Library version string, e.g. "tinyllm_kv 0.1.0 gfx950". */
+const char *tl_version(void);
+
+/* ------------------------------------------------------------------------
+ * KVCacheManager (include/tiny_llm/kv_cache.h:24-111, src/kv_cache.cpp)
+ * Same semantics and the same pool layout:
+ *   pool = [slot][layer][K|V][max_seq_len][num_heads][head_dim] fp16.
+ * ---------------------------------------------------------------------- */
+
+/* KVCacheConfig (include/tiny_llm/types.h:122-128); num_heads = KV heads. */
+typedef struct tl_kv_config {
+    int num_layers;
+    int num_heads;
+    int head_dim;
+    int max_seq_len;
+    int max_batch_size;
+} tl_kv_config;
+
+typedef struct tl_kv_manager tl_kv_manager;
+
+/* KVCacheManager::create (kv_cache.cpp:8-60): validates, hipMalloc + zero. */
+int tl_kv_create(const tl_kv_config *cfg, tl_kv_manager **out);
+/* ~KVCacheManager (kv_cache.cpp:62-67). NULL is accepted. */
+void tl_kv_destroy(tl_kv_manager *mgr);
+/* allocateSequence (kv_cache.cpp:91-119): lowest free slot, monotonically
+ * increasing ids; error text contains "exhausted" when no slot is free. */
+int tl_kv_allocate_sequence(tl_kv_manager *mgr, int max_len, int *seq_id);
+/* releaseSequence (kv_cache.cpp:121-137): device bytes are not cleared. */
+int tl_kv_release_sequence(tl_kv_manager *mgr, int seq_id);
+/* getCacheChecked (kv_cache.cpp:139-157): device pointers of the (seq,
+ * layer) K and V regions ([max_seq_len][num_heads][head_dim] each).  Fails
+ * for paged pools (tl_kv_set_block_map), which have no contiguous region. */
+int tl_kv_get_cache(tl_kv_manager *mgr, int seq_id, int layer, void **k_cache, void **v_cache);
+/* appendKV (kv_cache.cpp:168-238): copies num_tokens tokens of
+ * [num_tokens][num_heads][head_dim] fp16 K and V to the sequence tail
+ * (current_len) on `stream`; does NOT advance the visible length. */
+int tl_kv_append(tl_kv_manager *mgr, int seq_id, int layer, const void *new_k, const void *new_v,
+                 int num_tokens, void *stream);
+/* advanceSeqLen (kv_cache.cpp:240-259): clamps to the sequence's max_len. */
+int tl_kv_advance(tl_kv_manager *mgr, int seq_id, int num_tokens);
+/* getSeqLen (kv_cache.cpp:261-267): 0 for an unknown sequence. */
+int tl_kv_seq_len(const tl_kv_manager *mgr, int seq_id);
+/* hasSequence (kv_cache.cpp:269-271). */
+int tl_kv_has_sequence(const tl_kv_manager *mgr, int seq_id);
+/* getUsedMemory / getTotalMemory / getFreeMemory (kv_cache.cpp:273-286). */
+size_t tl_kv_used_memory(const tl_kv_manager *mgr);
+size_t tl_kv_total_memory(const tl_kv_manager *mgr);
+size_t tl_kv_free_memory(const tl_kv_manager *mgr);
+/* getActiveSequenceCount (kv_cache.cpp:288-295). */
+int tl_kv_active_count(const tl_kv_manager *mgr);
+/* getConfig (kv_cache.h:83). */
+int tl_kv_get_config(const tl_kv_manager *mgr, tl_kv_config *out);
+/* Device base of the pool and the per-slot byte size (slot_size_,
+ * kv_cache.cpp:28); no reference accessor exists, these expose the private
+ * memory_pool_ / slot_size_ for parity checks of the whole pool. */
+void  *tl_kv_pool(const tl_kv_manager *mgr);
+size_t tl_kv_slot_bytes(const tl_kv_manager *mgr);
+/* Slot index of a live sequence (seq_to_slot_, kv_cache.h:104), -1 if absent. */
+int tl_kv_slot_of(const tl_kv_manager *mgr, int seq_id);
+
+/* Paged addressing over the same pool (build addition; the reference layout
+ * is the identity map).  Logical block x = slot*(max_seq_len/block_tokens)+j
+ * (token block j of that slot) is stored at physical block perm[x] of the
+ * same geometry; every layer's K and V region uses the same map.  perm must
+ * be a permutation of [0, max_batch_size*max_seq_len/block_tokens); it is
+ * copied.  block_tokens must be a power of two dividing max_seq_len.
+ * perm == NULL restores the reference layout. */
+int tl_kv_set_block_map(tl_kv_manager *mgr, int block_tokens, const int32_t *perm, size_t n);
+
+/* ------------------------------------------------------------------------
+ * Batched decode surface (build addition layered on the manager).  The
+ * reference decodes one sequence per call: TransformerLayer::attention
+ * (src/transformer.cpp:222-237) does getCache -> appendKV(n=1) ->
+ * attention_decode(q, K*, V*, out, 1/sqrt(D), 1, Hq, getSeqLen+1, D) per
+ * layer, and InferenceEngine::decodeStep commits with advanceSeqLen(seq, 1)
+ * after all layers (src/inference_engine.cpp:287-291).  A batch snapshots
+ * that state for n sequences once per step; every layer then appends and
+ * attends through it.  Query head h reads KV head h / (num_q_heads/num_heads).
+ * ---------------------------------------------------------------------- */
+typedef struct tl_kv_batch tl_kv_batch;
+
+/* A batch of at most max_seqs sequences with num_q_heads query heads. */
+int tl_kv_batch_create(tl_kv_manager *mgr, int max_seqs, int num_q_heads, tl_kv_batch **out);
+void tl_kv_batch_destroy(tl_kv_batch *batch);
+/* Snapshot for a decode step: for each seq_ids[i] (distinct, live),
+ * write position = getSeqLen (kv_cache.cpp:208), attended length = write
+ * position + 1 (transformer.cpp:230-235).  Fails like appendKV(n=1) when a
+ * sequence is full.  Uploads the step's metadata on `stream`. */
+int tl_kv_batch_prepare(tl_kv_batch *batch, const int *seq_ids, int n, void *stream);
+/* Like prepare, but with explicit attended lengths and no append slot:
+ * attended[i] tokens of seq_ids[i] (1 <= attended[i] <= its max_len) are
+ * read by attention/gather; append is rejected for such a batch. */
+int tl_kv_batch_prepare_lengths(tl_kv_batch *batch, const int *seq_ids, const int *attended, int n,
+                                void *stream);
+/* Size, split-K chunk length (tokens per work item) and work-item count of
+ * the last prepare; any pointer may be NULL.  No reference counterpart. */
+int tl_kv_batch_info(const tl_kv_batch *batch, int *n, int *chunk_tokens, int *work_items);
+/* Fused append of one token per (sequence, layer) for layers
+ * [layer_begin, layer_begin + num_layers): new_k/new_v are
+ * [num_layers][n][num_heads][head_dim] fp16.  Byte-identical to n*num_layers
+ * appendKV(seq, layer, k_row, v_row, 1) calls (kv_cache.cpp:226-233). */
+int tl_kv_batch_append(tl_kv_batch *batch, int layer_begin, int num_layers, const void *new_k,
+                       const void *new_v, void *stream);
+/* GQA decode attention of every batch entry at `layer`: q and out are
+ * [n][num_q_heads][head_dim] fp16; replaces the per-sequence
+ * attention_decode call of transformer.cpp:236-237 (math of
+ * kernels/attention.cu:11-112). */
+int tl_kv_batch_attention(tl_kv_batch *batch, int layer, const void *q, void *out, float scale,
+                          void *stream);
+/* The whole decode branch of TransformerLayer::attention for one layer
+ * (transformer.cpp:222-237): append the new token, then attend over
+ * attended = write position + 1, in one stream-ordered call. */
+int tl_kv_batch_decode(tl_kv_batch *batch, int layer, const void *q, const void *new_k,
+                       const void *new_v, void *out, float scale, void *stream);
+/* Gather of the attended tokens into compact head-major layout (the K/V
+ * layout attention_decode reads, kernels/attention.cuh:10-13):
+ * k_out/v_out are [n][num_heads][s_max][head_dim]; tokens at or beyond a
+ * sequence's attended length are written as +0.0.  Either output may be NULL. */
+int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, int s_max,
+                       void *stream);
+
+/* ------------------------------------------------------------------------
+ * Stateless kernels over an explicit cache view (no manager).
+ * ---------------------------------------------------------------------- */
+
+/* Element offset of (sequence b, kv head g, token t) relative to k_base or
+ * v_base:  blk(b, t >> log2_blk) * blk_stride + (t & (2^log2_blk - 1)) *
+ * tok_stride + g * head_stride, with blk(b, j) = block_table[b*bt_stride+j]
+ * (device int32) or b when block_table is NULL.  Strides are in elements. */
+typedef struct tl_kv_view {
+    const void    *k_base;
+    const void    *v_base;
+    const int32_t *block_table;
+    int            bt_stride;
+    int            log2_blk;
+    int64_t        blk_stride;
+    int64_t        tok_stride;
+    int64_t        head_stride;
+} tl_kv_view;
+
+/* GQA decode attention over a view.  seq_lens_host[b] (host memory) is the
+ * attended length of entry b (0 gives a zero output row).  q/out:
+ * [B][Hq][D] fp16 device.  head_dim in {32, 64, 128, 256}, Hq/Hkv in
+ * {1, 2, 4, 8}.  Uses library-owned device workspace. */
+int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_lens_host, int B,
+                       int Hq, int Hkv, int D, float scale, void *out, void *stream);
+
+/* attention_decode (kernels/attention.cuh:15-18, attention.cu:114-128):
+ * q [B][H][D], k/v [B][H][S][D], out [B][H][D] fp16 device pointers.
+ * Silently returns on non-positive dimensions, like the reference. */
+void tl_attention_decode(const void *q, const void *k, const void *v, void *out, float scale,
+                         int batch, int num_heads, int seq_len, int head_dim, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Kernel timing (the reference has only an unused CudaEvent wrapper,
+ * include/tiny_llm/cuda_streams.h:67-99).  When enabled, every launch of the
+ * named kernels is bracketed by hipEvents on its own stream.
+ * Names: "attn_chunk", "attn_merge", "kv_append", "kv_gather".
+ * ---------------------------------------------------------------------- */
+void tl_profile_enable(int on);
+void tl_profile_reset(void);
+/* Synchronises the recorded events; total device milliseconds and launch
+ * count of `kernel`.  Returns TL_ERR_INVALID for an unknown name. */
+int tl_profile_query(const char *kernel, double *total_ms, long long *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,526 @@
+/*
+ * kv_oracle.c -- CPU restatement of tiny-llm's KV-cache decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product; see kv_oracle.h).
+ *
+ * Pinning of each part (what independent check would fail on a plausible
+ * mistake -- a dropped term, a wrong sign or index, a transposed operand):
+ *   orc_h2f / orc_f2h      exhaustive over all 65536 binary16 patterns and
+ *                          every midpoint between neighbours, against numpy's
+ *                          float16 conversion (tests/test_oracle_fp16.py).
+ *   orc_fill_normal_f16    moments / determinism only (input generator; its
+ *                          exact values are not a parity claim).
+ *   orc_kv_* bookkeeping   the reference's own live tests
+ *                          (tests/test_kv_cache.cpp:43-287) and its disabled
+ *                          invariants (:298-443), ported one for one
+ *                          (tests/test_oracle_kv.py).
+ *   orc_kv_append / layout the documented layout comment of the reference
+ *                          ("[Layer 0 K][Layer 0 V][Layer 1 K]...",
+ *                          kv_cache.cpp:70-71, kv_cache.h:16) checked by
+ *                          tagging every (slot, layer, K|V, token) region
+ *                          with a distinct value and reading the raw pool in
+ *                          order; round trips of test_transformer.cu:141-194,
+ *                          :302-381 (KVCachePreservesData) and :383-446
+ *                          (SequentialAppendEquivalence).
+ *   orc_attn_decode_gqa    float64 matrix-form softmax(q K^T s) V computed by
+ *                          numpy on small cases; closed forms S=1, q=0,
+ *                          identical keys, dominant score; permutation
+ *                          invariance; GQA sharing; decode == last row of
+ *                          causal full attention (test_transformer.cu:222-300)
+ *                          (tests/test_oracle_attention.py).
+ *   orc_kv_gather          brute-force element loop in numpy over the same
+ *                          view parameters plus the identity
+ *                          gather(cache layout) == reshaped reference pool.
+ * No function is left "parity unpinned" at the 1e-3 / bit-exact bars.  The
+ * exact output BITS of the CUDA kernel (warp-tree reduction order, CUDA's expf
+ * ULP behaviour) cannot be pinned without running it, which is impossible
+ * here (no nvcc, no NVIDIA GPU); the gate for attention is 1e-3 relative.
+ */
+#include "kv_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* binary16 <-> binary32                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* Exact widening; IEEE 754-2008 binary16 layout: 1 sign, 5 exponent (bias
+ * 15), 10 fraction bits.  Stands in for __half2float (attention.cu:37-38). */
+float orc_h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t ex = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    uint32_t bits;
+    if (ex == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            float f = (float)man * 5.9604644775390625e-08f; /* man * 2^-24, exact */
+            memcpy(&bits, &f, 4);
+            bits |= sign;
+        }
+    } else if (ex == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((ex + 112u) << 23) | (man << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* Round to nearest, ties to even.  Stands in for __float2half
+ * (attention.cu:110), whose default rounding is RNE. */
+uint16_t orc_f2h(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) { /* Inf or NaN (NaN stays quiet NaN) */
+        if (ax == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+        return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    }
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: overflow */
+    if (ax < 0x38800000u) {                                    /* below 2^-14 */
+        if (ax <= 0x33000000u) return (uint16_t)sign;          /* <= 2^-25: ties to 0 */
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e; /* value in units of 2^-24 is m >> shift */
+        uint32_t qv = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (qv & 1u))) qv++;
+        return (uint16_t)(sign | qv);
+    }
+    uint32_t r = ax + 0xfffu + ((ax >> 13) & 1u);
+    r -= 0x38000000u; /* rebias exponent 127 -> 15 */
+    return (uint16_t)(sign | (r >> 13));
+}
+
+void orc_h2f_n(const uint16_t *src, float *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_h2f(src[i]);
+}
+
+void orc_f2h_n(const float *src, uint16_t *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f2h(src[i]);
+}
+
+static float g_h2f_table[65536];
+static int   g_h2f_ready = 0;
+
+static void h2f_table_init(void) {
+    if (g_h2f_ready) return;
+#ifdef _OPENMP
+#pragma omp critical(orc_h2f_table)
+#endif
+    {
+        if (!g_h2f_ready) {
+            for (uint32_t i = 0; i < 65536u; ++i) g_h2f_table[i] = orc_h2f((uint16_t)i);
+            g_h2f_ready = 1;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* splitmix64 -> Box-Muller normal generator                                 */
+/* ------------------------------------------------------------------------ */
+
+static uint64_t splitmix64(uint64_t *state) {
+    uint64_t z = (*state += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+void orc_fill_normal_f16(uint64_t seed, float stddev, uint16_t *out, size_t n) {
+    uint64_t st = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        double u1 = 1.0 - (double)(splitmix64(&st) >> 11) * (1.0 / 9007199254740992.0);
+        double u2 = (double)(splitmix64(&st) >> 11) * (1.0 / 9007199254740992.0);
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = orc_f2h((float)(r * cos(two_pi * u2) * stddev));
+        if (i + 1 < n) out[i + 1] = orc_f2h((float)(r * sin(two_pi * u2) * stddev));
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* KVCacheManager restatement (kv_cache.cpp)                                 */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    int seq_id;      /* SequenceCache::seq_id      (kv_cache.h:16) */
+    int current_len; /* SequenceCache::current_len (kv_cache.h:17) */
+    int max_len;     /* SequenceCache::max_len     (kv_cache.h:18) */
+    int active;      /* SequenceCache::active      (kv_cache.h:19) */
+} orc_slot;
+
+struct orc_kv {
+    orc_kv_config cfg;
+    uint16_t     *pool;
+    size_t        pool_size; /* bytes */
+    size_t        slot_size; /* bytes */
+    orc_slot     *slots;
+    int           next_seq_id;
+};
+
+static void set_err(char *err, int errlen, const char *fmt, ...) {
+    if (!err || errlen <= 0) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, (size_t)errlen, fmt, ap);
+    va_end(ap);
+}
+
+/* KVCacheManager::create (kv_cache.cpp:8-60): validate, size with overflow
+ * checks, allocate the pool, zero it (cudaMemset, :43), slots inactive with
+ * max_len = config.max_seq_len (:51-57). */
+int orc_kv_create(const orc_kv_config *cfg, orc_kv **out, char *err, int errlen) {
+    *out = NULL;
+    if (cfg->num_layers <= 0 || cfg->num_heads <= 0 || cfg->head_dim <= 0 ||
+        cfg->max_seq_len <= 0 || cfg->max_batch_size <= 0) {
+        set_err(err, errlen, "KVCacheManager: invalid configuration parameters");
+        return -1;
+    }
+    size_t kv_per_layer = (size_t)cfg->num_heads * (size_t)cfg->max_seq_len * (size_t)cfg->head_dim;
+    size_t kv_total = kv_per_layer * (size_t)cfg->num_layers * 2u;
+    if (kv_total > SIZE_MAX / 2u) {
+        set_err(err, errlen, "KVCacheManager: memory size overflow");
+        return -1;
+    }
+    size_t slot_size = kv_total * 2u;
+    if (slot_size > SIZE_MAX / (size_t)cfg->max_batch_size) {
+        set_err(err, errlen, "KVCacheManager: pool size overflow");
+        return -1;
+    }
+    orc_kv *kv = (orc_kv *)calloc(1, sizeof(orc_kv));
+    if (!kv) {
+        set_err(err, errlen, "KVCacheManager: host allocation failed");
+        return -1;
+    }
+    kv->cfg = *cfg;
+    kv->slot_size = slot_size;
+    kv->pool_size = slot_size * (size_t)cfg->max_batch_size;
+    kv->pool = (uint16_t *)calloc(kv->pool_size / 2u, 2u); /* zeroed like cudaMemset(0) */
+    kv->slots = (orc_slot *)calloc((size_t)cfg->max_batch_size, sizeof(orc_slot));
+    if (!kv->pool || !kv->slots) {
+        free(kv->pool);
+        free(kv->slots);
+        free(kv);
+        set_err(err, errlen, "KVCacheManager: host allocation failed");
+        return -1;
+    }
+    for (int i = 0; i < cfg->max_batch_size; ++i) {
+        kv->slots[i].active = 0;
+        kv->slots[i].seq_id = -1;
+        kv->slots[i].current_len = 0;
+        kv->slots[i].max_len = cfg->max_seq_len;
+    }
+    kv->next_seq_id = 0;
+    *out = kv;
+    return 0;
+}
+
+void orc_kv_destroy(orc_kv *kv) {
+    if (!kv) return;
+    free(kv->pool);
+    free(kv->slots);
+    free(kv);
+}
+
+/* calculateOffset (kv_cache.cpp:69-80), in elements. */
+static size_t calc_offset(const orc_kv *kv, int slot_idx, int layer_idx, int is_value) {
+    size_t kv_per_layer =
+        (size_t)kv->cfg.num_heads * (size_t)kv->cfg.max_seq_len * (size_t)kv->cfg.head_dim;
+    size_t slot_offset = (size_t)slot_idx * kv->slot_size / 2u;
+    size_t layer_offset = (size_t)layer_idx * kv_per_layer * 2u;
+    size_t kv_offset = is_value ? kv_per_layer : 0u;
+    return slot_offset + layer_offset + kv_offset;
+}
+
+/* seq_to_slot_ lookup.  The reference keeps an unordered_map whose entries
+ * exist exactly for active slots (allocate inserts :116, release erases :133),
+ * and seq ids are never reused (:111), so a scan over active slots returns
+ * the same slot. */
+int orc_kv_slot_of(const orc_kv *kv, int seq_id) {
+    for (int i = 0; i < kv->cfg.max_batch_size; ++i)
+        if (kv->slots[i].active && kv->slots[i].seq_id == seq_id) return i;
+    return -1;
+}
+
+/* findFreeSlot (kv_cache.cpp:82-89): lowest inactive slot. */
+static int find_free_slot(const orc_kv *kv) {
+    for (int i = 0; i < kv->cfg.max_batch_size; ++i)
+        if (!kv->slots[i].active) return i;
+    return -1;
+}
+
+size_t orc_kv_used(const orc_kv *kv) {
+    int active = 0;
+    for (int i = 0; i < kv->cfg.max_batch_size; ++i) active += kv->slots[i].active ? 1 : 0;
+    return (size_t)active * kv->slot_size; /* kv_cache.cpp:273-282 */
+}
+size_t orc_kv_total(const orc_kv *kv) { return kv->pool_size; }
+size_t orc_kv_free(const orc_kv *kv) { return orc_kv_total(kv) - orc_kv_used(kv); }
+int    orc_kv_active(const orc_kv *kv) {
+    int active = 0;
+    for (int i = 0; i < kv->cfg.max_batch_size; ++i) active += kv->slots[i].active ? 1 : 0;
+    return active;
+}
+size_t    orc_kv_slot_bytes(const orc_kv *kv) { return kv->slot_size; }
+uint16_t *orc_kv_pool(orc_kv *kv) { return kv->pool; }
+size_t    orc_kv_pool_elems(const orc_kv *kv) { return kv->pool_size / 2u; }
+
+/* allocateSequence (kv_cache.cpp:91-119). */
+int orc_kv_allocate(orc_kv *kv, int max_len, int *seq_id, char *err, int errlen) {
+    if (max_len <= 0 || max_len > kv->cfg.max_seq_len) {
+        set_err(err, errlen, "Invalid max_len: %d (must be 1-%d)", max_len, kv->cfg.max_seq_len);
+        return -1;
+    }
+    int slot_idx = find_free_slot(kv);
+    if (slot_idx < 0) {
+        set_err(err, errlen,
+                "KV cache exhausted: no free slots available. Used: %zu bytes, Total: %zu bytes",
+                orc_kv_used(kv), orc_kv_total(kv));
+        return -1;
+    }
+    int id = kv->next_seq_id++;
+    kv->slots[slot_idx].seq_id = id;
+    kv->slots[slot_idx].current_len = 0;
+    kv->slots[slot_idx].max_len = max_len;
+    kv->slots[slot_idx].active = 1;
+    *seq_id = id;
+    return 0;
+}
+
+/* releaseSequence (kv_cache.cpp:121-137): device bytes are left as they are. */
+int orc_kv_release(orc_kv *kv, int seq_id, char *err, int errlen) {
+    int s = orc_kv_slot_of(kv, seq_id);
+    if (s < 0) {
+        set_err(err, errlen, "Sequence not found: %d", seq_id);
+        return -1;
+    }
+    kv->slots[s].active = 0;
+    kv->slots[s].seq_id = -1;
+    kv->slots[s].current_len = 0;
+    return 0;
+}
+
+/* getCacheChecked (kv_cache.cpp:139-157). */
+int orc_kv_get_cache(const orc_kv *kv, int seq_id, int layer, size_t *k_off, size_t *v_off,
+                     char *err, int errlen) {
+    int s = orc_kv_slot_of(kv, seq_id);
+    if (s < 0) {
+        set_err(err, errlen, "Sequence not found: %d", seq_id);
+        return -1;
+    }
+    if (layer < 0 || layer >= kv->cfg.num_layers) {
+        set_err(err, errlen, "getCache: Invalid layer_idx: %d (valid range: 0-%d)", layer,
+                kv->cfg.num_layers - 1);
+        return -1;
+    }
+    *k_off = calc_offset(kv, s, layer, 0);
+    *v_off = calc_offset(kv, s, layer, 1);
+    return 0;
+}
+
+/* appendKV (kv_cache.cpp:168-238): validation order null k, null v,
+ * num_tokens, layer, sequence, overflow; then two byte copies of
+ * num_tokens*Hkv*D halves to offset write_pos*Hkv*D (:226-233).  The visible
+ * length is not advanced. */
+int orc_kv_append(orc_kv *kv, int seq_id, int layer, const uint16_t *new_k,
+                  const uint16_t *new_v, int num_tokens, char *err, int errlen) {
+    if (!new_k) {
+        set_err(err, errlen, "new_k is null");
+        return -1;
+    }
+    if (!new_v) {
+        set_err(err, errlen, "new_v is null");
+        return -1;
+    }
+    if (num_tokens <= 0) {
+        set_err(err, errlen, "appendKV: num_tokens must be positive: %d", num_tokens);
+        return -1;
+    }
+    if (layer < 0 || layer >= kv->cfg.num_layers) {
+        set_err(err, errlen, "appendKV: Invalid layer_idx: %d (valid range: 0-%d)", layer,
+                kv->cfg.num_layers - 1);
+        return -1;
+    }
+    int s = orc_kv_slot_of(kv, seq_id);
+    if (s < 0) {
+        set_err(err, errlen, "appendKV: sequence not found: %d", seq_id);
+        return -1;
+    }
+    int write_pos = kv->slots[s].current_len;
+    if (write_pos + num_tokens > kv->slots[s].max_len) {
+        set_err(err, errlen, "appendKV: cache overflow. Current: %d, appending: %d, max: %d",
+                write_pos, num_tokens, kv->slots[s].max_len);
+        return -1;
+    }
+    size_t k_off = calc_offset(kv, s, layer, 0);
+    size_t v_off = calc_offset(kv, s, layer, 1);
+    size_t pos_offset = (size_t)write_pos * (size_t)kv->cfg.num_heads * (size_t)kv->cfg.head_dim;
+    size_t n = (size_t)num_tokens * (size_t)kv->cfg.num_heads * (size_t)kv->cfg.head_dim;
+    memcpy(kv->pool + k_off + pos_offset, new_k, n * 2u);
+    memcpy(kv->pool + v_off + pos_offset, new_v, n * 2u);
+    return 0;
+}
+
+/* advanceSeqLen (kv_cache.cpp:240-259): clamps at max_len. */
+int orc_kv_advance(orc_kv *kv, int seq_id, int num_tokens, char *err, int errlen) {
+    if (num_tokens <= 0) {
+        set_err(err, errlen, "advanceSeqLen: num_tokens must be positive: %d", num_tokens);
+        return -1;
+    }
+    int s = orc_kv_slot_of(kv, seq_id);
+    if (s < 0) {
+        set_err(err, errlen, "advanceSeqLen: sequence not found: %d", seq_id);
+        return -1;
+    }
+    int nl = kv->slots[s].current_len + num_tokens;
+    kv->slots[s].current_len = nl < kv->slots[s].max_len ? nl : kv->slots[s].max_len;
+    return 0;
+}
+
+/* getSeqLen / hasSequence (kv_cache.cpp:261-271). */
+int orc_kv_seq_len(const orc_kv *kv, int seq_id) {
+    int s = orc_kv_slot_of(kv, seq_id);
+    return s < 0 ? 0 : kv->slots[s].current_len;
+}
+int orc_kv_has(const orc_kv *kv, int seq_id) { return orc_kv_slot_of(kv, seq_id) >= 0; }
+
+/* ------------------------------------------------------------------------ */
+/* views                                                                     */
+/* ------------------------------------------------------------------------ */
+
+static inline int64_t view_elem(const orc_kv_view *kv, int b, int g, int t) {
+    int64_t j = (int64_t)t >> kv->log2_blk;
+    int64_t r = (int64_t)t & ((((int64_t)1) << kv->log2_blk) - 1);
+    int64_t blk = kv->block_table ? (int64_t)kv->block_table[(int64_t)b * kv->bt_stride + j] : b;
+    return blk * kv->blk_stride + r * kv->tok_stride + (int64_t)g * kv->head_stride;
+}
+
+/* ------------------------------------------------------------------------ */
+/* decode attention (attention.cu:11-112)                                    */
+/* ------------------------------------------------------------------------ */
+
+/* One (b, h) row.  Arithmetic, in order:
+ *   s_p   = (sum_{d=0}^{D-1} q_d * k_{p,d}) * scale   sequential in d (:34-42);
+ *           nvcc contracts `score += q*k` to an FMA by default (--fmad=true),
+ *           so each step is fmaf(q_d, k_pd, acc)
+ *   m     = max_p s_p                                 (:46-69)
+ *   e_p   = expf(s_p - m), sum = sum_p e_p            (:72-94)
+ *   w_p   = e_p * (1 / (sum + 1e-6f))                 (:97-101)
+ *   o_d   = sum_p w_p * v_{p,d}, sequential in p, FMA-contracted (:104-109)
+ *   out_d = half_rn(o_d)                              (:110)
+ * The reference reduces max and sum with warp trees; the sequential order here
+ * differs from it only in the rounding of the sum, far below the 1e-3 gate. */
+static void decode_row(const float *qf, const uint16_t *kbase, const uint16_t *vbase,
+                       const orc_kv_view *kv, int b, int g, int S, int D, float scale,
+                       float *scores, float *acc, float *out_f32, uint16_t *out_f16) {
+    for (int p = 0; p < S; ++p) {
+        const uint16_t *krow = kbase + view_elem(kv, b, g, p);
+        float           score = 0.0f;
+        for (int d = 0; d < D; ++d) score = fmaf(qf[d], g_h2f_table[krow[d]], score);
+        scores[p] = score * scale;
+    }
+    float max_score = -FLT_MAX;
+    for (int p = 0; p < S; ++p) max_score = fmaxf(max_score, scores[p]);
+    float sum_exp = 0.0f;
+    for (int p = 0; p < S; ++p) {
+        float e = expf(scores[p] - max_score);
+        scores[p] = e;
+        sum_exp += e;
+    }
+    float inv_sum = 1.0f / (sum_exp + 1e-6f);
+    for (int p = 0; p < S; ++p) scores[p] *= inv_sum;
+    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+    /* p outer, d inner: each acc[d] still sees p = 0, 1, ... in order. */
+    for (int p = 0; p < S; ++p) {
+        const uint16_t *vrow = vbase + view_elem(kv, b, g, p);
+        float           w = scores[p];
+        for (int d = 0; d < D; ++d) acc[d] = fmaf(w, g_h2f_table[vrow[d]], acc[d]);
+    }
+    for (int d = 0; d < D; ++d) {
+        if (out_f32) out_f32[d] = S > 0 ? acc[d] : 0.0f;
+        if (out_f16) out_f16[d] = orc_f2h(S > 0 ? acc[d] : 0.0f);
+    }
+}
+
+void orc_attn_decode_gqa(const uint16_t *q, const orc_kv_view *kv, const int32_t *seq_lens,
+                         int B, int Hq, int Hkv, int D, float scale, float *out_f32,
+                         uint16_t *out_f16, int nthreads) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0) return;
+    h2f_table_init();
+    const int G = Hq / Hkv;
+    int       smax = 0;
+    for (int b = 0; b < B; ++b) smax = seq_lens[b] > smax ? seq_lens[b] : smax;
+    const long rows = (long)B * Hq;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = 1;
+#pragma omp parallel num_threads(nthreads)
+#endif
+    {
+        float *scores = (float *)malloc(sizeof(float) * (size_t)(smax > 0 ? smax : 1));
+        float *acc = (float *)malloc(sizeof(float) * (size_t)D);
+        float *qf = (float *)malloc(sizeof(float) * (size_t)D);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (long r = 0; r < rows; ++r) {
+            int b = (int)(r / Hq), h = (int)(r % Hq);
+            int g = h / G;
+            for (int d = 0; d < D; ++d) qf[d] = g_h2f_table[q[r * D + d]];
+            decode_row(qf, kv->k_base, kv->v_base, kv, b, g, seq_lens[b], D, scale, scores, acc,
+                       out_f32 ? out_f32 + r * D : NULL, out_f16 ? out_f16 + r * D : NULL);
+        }
+        free(scores);
+        free(acc);
+        free(qf);
+    }
+}
+
+/* attention_decode (attention.cu:114-128): silent no-op on non-positive dims
+ * (:117-119); compact head-major K/V. */
+void orc_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out_f32,
+                          uint16_t *out_f16, float scale, int B, int H, int S, int D) {
+    if (B <= 0 || H <= 0 || S <= 0 || D <= 0) return;
+    orc_kv_view view;
+    view.k_base = k;
+    view.v_base = v;
+    view.block_table = NULL;
+    view.bt_stride = 0;
+    view.log2_blk = 30;
+    view.blk_stride = (int64_t)H * S * D;
+    view.tok_stride = D;
+    view.head_stride = (int64_t)S * D;
+    int32_t *lens = (int32_t *)malloc(sizeof(int32_t) * (size_t)B);
+    for (int b = 0; b < B; ++b) lens[b] = S;
+    orc_attn_decode_gqa(q, &view, lens, B, H, H, D, scale, out_f32, out_f16, 1);
+    free(lens);
+}
+
+void orc_kv_gather(const orc_kv_view *kv, int which, const int32_t *seq_lens, int B, int Hkv,
+                   int D, int S_max, uint16_t *out) {
+    const uint16_t *base = which ? kv->v_base : kv->k_base;
+    for (int b = 0; b < B; ++b)
+        for (int g = 0; g < Hkv; ++g)
+            for (int t = 0; t < S_max; ++t) {
+                uint16_t *dst = out + (((size_t)b * Hkv + g) * S_max + t) * D;
+                if (t < seq_lens[b]) {
+                    memcpy(dst, base + view_elem(kv, b, g, t), (size_t)D * 2u);
+                } else {
+                    memset(dst, 0, (size_t)D * 2u);
+                }
+            }
+}

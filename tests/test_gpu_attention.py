@@ -1,0 +1,199 @@
+"""GPU: decode attention and gather vs the oracle.
+
+Tolerance: the reference's normwise metric max|a-b|/max(|a|,|b|)
+(test_transformer.cu:80-92) between the GPU fp16 output and the oracle's fp32
+output must be <= 1e-3 (the stated gate; fp16 output rounding alone is
+<= 2^-11 ~ 4.9e-4).  Gather outputs must be bit-exact."""
+import zlib
+
+import numpy as np
+import pytest
+
+from devutil import empty_dev, read_dev, rel_err, stream, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def f16bits(rng, shape, std=1.0):
+    return (rng.standard_normal(shape) * std).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+# ------------------------------------------------------ legacy attention_decode
+@pytest.mark.parametrize("B,H,S,D", [(1, 2, 8, 32), (1, 4, 8, 32), (2, 8, 129, 64),
+                                     (1, 32, 128, 128), (1, 32, 512, 128), (1, 32, 2048, 128),
+                                     (3, 4, 13000, 128), (2, 2, 700, 256), (1, 1, 1, 64)])
+def test_attention_decode_legacy_vs_oracle(tl, orc, B, H, S, D):
+    rng = np.random.default_rng(B * 7 + S)
+    q = f16bits(rng, (B, H, D))
+    k = f16bits(rng, (B, H, S, D))
+    v = f16bits(rng, (B, H, S, D))
+    dq, dk, dv = to_dev(q), to_dev(k), to_dev(v)
+    out = empty_dev((B, H, D))
+    scale = 1.0 / np.sqrt(D)
+    tl.attention_decode(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), scale, B, H,
+                        S, D, stream())
+    got = to_host(out).view(np.float16).astype(np.float32)
+    ref32, _ = orc.attn_decode_gqa(q, orc.compact_view(k, v, B, H, S, D), np.full(B, S), H, H, D,
+                                   scale, nthreads=8)
+    assert rel_err(got, ref32) <= TOL, rel_err(got, ref32)
+
+
+def test_attention_decode_nonpositive_dims_is_noop(tl):
+    out = to_dev(np.full((1, 2, 32), 0x3C00, np.uint16))
+    tl.attention_decode(0, 0, 0, out.data_ptr(), 1.0, 1, 2, 0, 32, stream())
+    assert np.all(to_host(out) == 0x3C00)
+
+
+def test_attention_decode_unsupported_dim_reports_error(tl):
+    out = to_dev(np.full((1, 1, 48), 0x3C00, np.uint16))
+    q = to_dev(np.zeros((1, 1, 48), np.uint16))
+    tl.attention_decode(q.data_ptr(), q.data_ptr(), q.data_ptr(), out.data_ptr(), 1.0, 1, 1, 1, 48,
+                        stream())
+    assert "unsupported head_dim" in tl.last_error()
+    assert np.all(to_host(out) == 0x3C00)
+
+
+# ---------------------------------------------------- batched decode over cache
+def _filled_cache(tl, orc, rng, L, Hkv, D, M, slots, ctx, kv_std=1.0, block_perm=None):
+    """Product manager + oracle pool with identical prompt appends."""
+    g = tl.KVCacheManager(L, Hkv, D, M, slots)
+    o = orc.KVCacheOracle(L, Hkv, D, M, slots)
+    if block_perm is not None:
+        assert g.setBlockMap(16, block_perm) is None
+    ids = []
+    keep = []
+    for S in ctx:
+        sid, err = g.allocateSequence(M)
+        assert err is None
+        o.allocate(M)
+        for layer in range(L):
+            if S == 0:
+                continue
+            k = f16bits(rng, S * Hkv * D, kv_std)
+            v = f16bits(rng, S * Hkv * D, kv_std)
+            dk, dv = to_dev(k), to_dev(v)
+            keep += [dk, dv]
+            assert g.appendKV(sid, layer, dk.data_ptr(), dv.data_ptr(), S, stream()) is None
+            assert o.append(sid, layer, k, v, S) is None
+        if S:
+            g.advanceSeqLen(sid, S)
+            o.advance(sid, S)
+        ids.append(sid)
+    return g, o, ids
+
+
+CASES = {
+    # name: (L, Hkv, G, D, ctx, kv_std)
+    "cfg1_exact": (1, 8, 1, 64, [128, 256, 384, 512], 1.0),
+    "cfg2_like": (2, 32, 1, 128, [512, 1000, 2047, 4096], 0.5),
+    "cfg3_like": (1, 8, 4, 128, [8192, 8192], 1.0),
+    "cfg5_group8": (1, 8, 8, 128, [256, 1500, 4096, 3], 1.0),
+    "ragged_small": (1, 2, 2, 32, [1, 2, 63, 64, 65, 511, 512, 513, 1025], 1.0),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_batch_decode_step_vs_oracle(tl, orc, name):
+    """One decode step of TransformerLayer::attention for a batch: append the
+    new token (bit-exact pool), attend over ctx+1 (<= 1e-3)."""
+    L, Hkv, G, D, ctx, std = CASES[name]
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    M = int(np.ceil((max(ctx) + 2) / 16) * 16)
+    g, o, ids = _filled_cache(tl, orc, rng, L, Hkv, D, M, len(ctx) + 1, ctx, std)
+    Hq = Hkv * G
+    B = len(ids)
+    batch = tl.DecodeBatch(g, B, Hq)
+    order = ids[::-1]
+    batch.prepare(order, stream())
+    scale = 1.0 / np.sqrt(D)
+    layer = L - 1
+    q = f16bits(rng, (B, Hq, D))
+    nk = f16bits(rng, (B, Hkv * D), std)
+    nv = f16bits(rng, (B, Hkv * D), std)
+    dq, dk, dv = to_dev(q), to_dev(nk), to_dev(nv)
+    out = empty_dev((B, Hq, D))
+    batch.decode(layer, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), scale, stream())
+    for i, sid in enumerate(order):
+        assert o.append(sid, layer, nk[i], nv[i], 1) is None
+    assert np.array_equal(read_dev(g.pool(), o.pool().size), o.pool())
+    lens = np.array([o.seq_len(s) + 1 for s in order])
+    view = orc.cache_view(o.pool(), L, Hkv, D, M, layer, [o.slot_of(s) for s in order])
+    ref32, _ = orc.attn_decode_gqa(q, view, lens, Hq, Hkv, D, scale, nthreads=8)
+    got = to_host(out).view(np.float16).astype(np.float32)
+    for i in range(B):
+        assert rel_err(got[i], ref32[i]) <= TOL, (i, rel_err(got[i], ref32[i]))
+
+
+def test_paged_ragged_attention_and_gather(tl, orc):
+    """Config-4 shape at reduced batch: 16-token blocks through a seeded random
+    permutation, lognormal lengths; attention <= 1e-3, gather bit-exact."""
+    import workloads
+    rng = np.random.default_rng(4)
+    Hkv, G, D = 8, 4, 128
+    ctx = workloads.lognormal_lengths(12, 2048, 1.0, 1, 32768, workloads.seed(4, 3))
+    ctx[0], ctx[1] = 1, 15
+    M = int(np.ceil((ctx.max() + 1) / 64) * 64)
+    slots = len(ctx) + 2
+    perm = workloads.block_permutation(slots * (M // 16), workloads.seed(4, 4))
+    g, o, ids = _filled_cache(tl, orc, rng, 1, Hkv, D, M, slots, list(ctx), 1.0, block_perm=perm)
+    Hq = Hkv * G
+    B = len(ids)
+    batch = tl.DecodeBatch(g, B, Hq)
+    batch.prepare(ids, stream())
+    q = f16bits(rng, (B, Hq, D))
+    nk, nv = f16bits(rng, (B, Hkv * D)), f16bits(rng, (B, Hkv * D))
+    dq, dk, dv = to_dev(q), to_dev(nk), to_dev(nv)
+    out = empty_dev((B, Hq, D))
+    batch.decode(0, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), 0.088, stream())
+    for i, sid in enumerate(ids):
+        o.append(sid, 0, nk[i], nv[i], 1)
+    lens = np.array([o.seq_len(s) + 1 for s in ids])
+    view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(s) for s in ids])
+    ref32, _ = orc.attn_decode_gqa(q, view, lens, Hq, Hkv, D, 0.088, nthreads=8)
+    got = to_host(out).view(np.float16).astype(np.float32)
+    for i in range(B):
+        assert rel_err(got[i], ref32[i]) <= TOL
+    smax = int(lens.max()) + 3
+    gk, gv = empty_dev((B, Hkv, smax, D)), empty_dev((B, Hkv, smax, D))
+    batch.gather(0, gk.data_ptr(), gv.data_ptr(), smax, stream())
+    assert np.array_equal(to_host(gk), orc.gather(view, 0, lens, Hkv, D, smax))
+    assert np.array_equal(to_host(gv), orc.gather(view, 1, lens, Hkv, D, smax))
+
+
+def test_prepare_lengths_zero_and_partial(tl, orc):
+    rng = np.random.default_rng(8)
+    Hkv, G, D, M = 2, 4, 64, 1024
+    g, o, ids = _filled_cache(tl, orc, rng, 1, Hkv, D, M, 4, [700, 900, 1000], 1.0)
+    batch = tl.DecodeBatch(g, 3, Hkv * G)
+    att = [0, 513, 1000]
+    batch.prepare_lengths(ids, att, stream())
+    q = f16bits(rng, (3, Hkv * G, D))
+    dq = to_dev(q)
+    out = to_dev(np.full((3, Hkv * G, D), 0x3C00, np.uint16))
+    batch.attention(0, dq.data_ptr(), out.data_ptr(), 0.125, stream())
+    view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(s) for s in ids])
+    ref32, _ = orc.attn_decode_gqa(q, view, np.array(att), Hkv * G, Hkv, D, 0.125, nthreads=8)
+    got = to_host(out).view(np.float16).astype(np.float32)
+    assert not got[0].any()
+    for i in (1, 2):
+        assert rel_err(got[i], ref32[i]) <= TOL
+    with pytest.raises(tl.TinyLLMError, match="prepare"):
+        batch.append(0, 1, dq.data_ptr(), dq.data_ptr())
+
+
+def test_stateless_view_gqa(tl, orc):
+    rng = np.random.default_rng(21)
+    B, Hkv, G, S, D = 3, 4, 2, 300, 64
+    k, v = f16bits(rng, (B, Hkv, S, D)), f16bits(rng, (B, Hkv, S, D))
+    q = f16bits(rng, (B, Hkv * G, D))
+    dk, dv, dq = to_dev(k), to_dev(v), to_dev(q)
+    out = empty_dev((B, Hkv * G, D))
+    view = tl.KVView(dk.data_ptr(), dv.data_ptr(), None, 0, 30, Hkv * S * D, D, S * D)
+    lens = np.array([300, 1, 129])
+    tl.attn_decode_gqa(dq.data_ptr(), view, lens, Hkv * G, Hkv, D, 0.1, out.data_ptr(), stream())
+    ref32, _ = orc.attn_decode_gqa(q, orc.compact_view(k, v, B, Hkv, S, D), lens, Hkv * G, Hkv, D, 0.1)
+    got = to_host(out).view(np.float16).astype(np.float32)
+    for i in range(B):
+        assert rel_err(got[i], ref32[i]) <= TOL

@@ -1,0 +1,54 @@
+"""Pins the oracle's binary16 conversions against numpy's independent
+float16 implementation (round-to-nearest-even), exhaustively."""
+import numpy as np
+
+
+def test_h2f_all_65536_patterns(orc):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = orc.h2f(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def _f2h_ref(x):
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_f2h_representables_midpoints_and_neighbours(orc):
+    pos = np.arange(0, 0x7C00, dtype=np.uint16)            # every finite non-negative half
+    f = pos.view(np.float16).astype(np.float64)
+    mids = ((f[:-1] + f[1:]) / 2).astype(np.float32)      # exact: 12 significant bits
+    cases = [f.astype(np.float32), mids,
+             np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf)),
+             np.array([65504, 65519.99, 65520, 65536, 1e30, np.inf, 2.0 ** -25,
+                       2.0 ** -25 * 1.0000001, 2.0 ** -24 * 1.5, 2.0 ** -26, 1e-30, 0.0],
+                      dtype=np.float32)]
+    x = np.concatenate(cases)
+    x = np.concatenate([x, -x])
+    assert np.array_equal(orc.f2h(x), _f2h_ref(x))
+
+
+def test_f2h_random_float32(orc):
+    rng = np.random.default_rng(7)
+    u = rng.integers(0, 2 ** 32, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = u.view(np.float32)
+    x = x[~np.isnan(x)]
+    assert np.array_equal(orc.f2h(x), _f2h_ref(x))
+
+
+def test_f2h_nan_stays_nan(orc):
+    x = np.array([np.nan, -np.nan], dtype=np.float32)
+    h = orc.f2h(x)
+    assert np.all(np.isnan(h.view(np.float16)))
+
+
+def test_normal_generator_moments_and_determinism(orc):
+    a = orc.normal_f16(123, (200_000,), 0.5)
+    b = orc.normal_f16(123, (200_000,), 0.5)
+    assert np.array_equal(a, b)
+    v = a.view(np.float16).astype(np.float64)
+    assert abs(v.mean()) < 0.01 and abs(v.std() - 0.5) < 0.01
+    assert not np.array_equal(a, orc.normal_f16(124, (200_000,), 0.5))

@@ -1,0 +1,130 @@
+// Stateless decode-attention entry points: the reference's
+// tiny_llm::kernels::attention_decode (kernels/attention.cu:114-128) and the
+// view-based GQA call.  Both run the split-K kernels of
+// kernels/attention_decode.hip with the per-device workspace.
+#include "tiny_llm/kernels/attention.h"
+
+#include "kernels/kv_kernels.h"
+#include "runtime.h"
+#include "tiny_llm/hip_utils.h"
+#include "tiny_llm/logger.h"
+
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace tiny_llm {
+namespace detail {
+
+namespace {
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+} // namespace
+
+// Returns "" on success, else the reason the call was rejected.
+std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *seq_lens_host, int B,
+                             int Hq, int Hkv, int D, float scale, __half *out, hipStream_t stream) {
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0) return "tl_attn_decode_gqa: invalid dimensions";
+    if (B == 0) return "";
+    if (Hq % Hkv != 0) return "tl_attn_decode_gqa: Hq must be a multiple of Hkv";
+    if (!attn_shape_supported(D, Hq / Hkv))
+        return "tl_attn_decode_gqa: unsupported head_dim/group (head_dim in {32,64,128,256}, "
+               "Hq/Hkv in {1,2,4,8})";
+    if (!q || !out || !kv.k_base || !kv.v_base || !seq_lens_host)
+        return "tl_attn_decode_gqa: null pointer argument";
+    if (!aligned16(q) || !aligned16(kv.k_base) || !aligned16(kv.v_base))
+        return "tl_attn_decode_gqa: q, k_base and v_base must be 16-byte aligned";
+    if (kv.tok_stride % 8 != 0 || kv.head_stride % 8 != 0 || kv.blk_stride % 8 != 0)
+        return "tl_attn_decode_gqa: strides must be multiples of 8 elements";
+    if (kv.log2_blk < 4 || kv.log2_blk > 30) return "tl_attn_decode_gqa: log2_blk must be in [4, 30]";
+    for (int b = 0; b < B; ++b)
+        if (seq_lens_host[b] < 0) return "tl_attn_decode_gqa: negative sequence length";
+
+    const int            chunk = choose_chunk(seq_lens_host, B, Hkv, 0);
+    std::vector<int32_t> part_base(static_cast<size_t>(B) + 1, 0);
+    bool                 any_multi = false, any_empty = false;
+    for (int b = 0; b < B; ++b) {
+        const int c = (seq_lens_host[b] + chunk - 1) / chunk;
+        any_multi |= c > 1;
+        any_empty |= c == 0;
+        part_base[static_cast<size_t>(b) + 1] = part_base[static_cast<size_t>(b)] + c;
+    }
+    const int     n_work = part_base[static_cast<size_t>(B)];
+    const size_t  nb = static_cast<size_t>(B);
+    DeviceContext &ctx = DeviceContext::get(current_device());
+    std::lock_guard<std::mutex> lk(ctx.mu);
+    ctx.claim(stream);
+    const size_t words = nb + (nb + 1) + 2 * static_cast<size_t>(n_work);
+    int32_t     *h = static_cast<int32_t *>(ctx.ring.begin(words * 4));
+    std::memcpy(h, seq_lens_host, nb * 4);
+    std::memcpy(h + nb, part_base.data(), (nb + 1) * 4);
+    int32_t *w = h + 2 * nb + 1;
+    for (int b = 0; b < B; ++b)
+        for (int c = part_base[static_cast<size_t>(b)]; c < part_base[static_cast<size_t>(b) + 1]; ++c) {
+            *w++ = b;
+            *w++ = c - part_base[static_cast<size_t>(b)];
+        }
+    const int32_t *d = static_cast<const int32_t *>(ctx.ring.commit(stream));
+    AttnPlan       plan;
+    plan.seq_lens = d;
+    plan.part_base = d + nb;
+    plan.work = d + 2 * nb + 1;
+    plan.n_work = n_work;
+    plan.chunk = chunk;
+    plan.any_multi = any_multi;
+    plan.any_empty = any_empty;
+    float *part = any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
+    launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, stream);
+    return "";
+}
+
+std::string attn_decode_compact(const __half *q, const __half *k, const __half *v, __half *out,
+                                float scale, int B, int H, int S, int D, hipStream_t stream) {
+    if (!attn_shape_supported(D, 1))
+        return "attention_decode: unsupported head_dim " + std::to_string(D) +
+               " (supported: 32, 64, 128, 256)";
+    if (!q || !k || !v || !out) return "attention_decode: null pointer argument";
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v))
+        return "attention_decode: query, k_cache and v_cache must be 16-byte aligned";
+    KvView kv;
+    kv.k_base = k;
+    kv.v_base = v;
+    kv.log2_blk = 30;
+    kv.blk_stride = static_cast<int64_t>(H) * S * D;
+    kv.tok_stride = D;
+    kv.head_stride = static_cast<int64_t>(S) * D;
+    AttnPlan plan;
+    plan.uniform_len = S;
+    plan.chunk = choose_chunk(nullptr, B, H, S);
+    plan.nchunk = (S + plan.chunk - 1) / plan.chunk;
+    plan.n_work = B * plan.nchunk;
+    plan.any_multi = plan.nchunk > 1;
+    DeviceContext &ctx = DeviceContext::get(current_device());
+    std::lock_guard<std::mutex> lk(ctx.mu);
+    ctx.claim(stream);
+    float *part = plan.any_multi ? ctx.ws.get(attn_workspace_floats(plan.n_work, H, D)) : nullptr;
+    launch_attn_decode(q, kv, plan, B, H, H, D, scale, out, part, stream);
+    return "";
+}
+
+} // namespace detail
+
+namespace kernels {
+
+void attention_decode(const half *query, const half *k_cache, const half *v_cache, half *output,
+                      float scale, int batch_size, int num_heads, int seq_len, int head_dim,
+                      hipStream_t stream) {
+    if (batch_size <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return;
+    std::string err;
+    try {
+        err = detail::attn_decode_compact(query, k_cache, v_cache, output, scale, batch_size,
+                                          num_heads, seq_len, head_dim, stream);
+    } catch (const HipException &e) {
+        err = e.what();
+    }
+    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+}
+
+} // namespace kernels
+} // namespace tiny_llm

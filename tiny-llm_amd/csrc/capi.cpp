@@ -1,0 +1,284 @@
+// extern "C" surface of libtinyllm_kv.so (declared in include/tinyllm_kv.h).
+// Thin: argument marshalling, Result -> status code, exceptions -> TL_ERR_HIP.
+#include "tinyllm_kv.h"
+
+#include "kernels/kv_kernels.h"
+#include "runtime.h"
+#include "tiny_llm/kernels/attention.h"
+#include "tiny_llm/kv_cache.h"
+#include "tiny_llm/logger.h"
+
+#include <cstring>
+#include <memory>
+#include <string>
+
+namespace tiny_llm {
+namespace detail {
+std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *seq_lens_host, int B,
+                             int Hq, int Hkv, int D, float scale, __half *out, hipStream_t stream);
+std::string attn_decode_compact(const __half *q, const __half *k, const __half *v, __half *out,
+                                float scale, int B, int H, int S, int D, hipStream_t stream);
+} // namespace detail
+} // namespace tiny_llm
+
+using tiny_llm::DecodeBatch;
+using tiny_llm::KVCacheManager;
+using tiny_llm::Result;
+
+struct tl_kv_manager {
+    std::unique_ptr<KVCacheManager> m;
+};
+struct tl_kv_batch {
+    std::unique_ptr<DecodeBatch> b;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+template <typename T>
+int status(const Result<T> &r) {
+    if (r.isOk()) {
+        g_last_error.clear();
+        return TL_OK;
+    }
+    return fail(TL_ERR_INVALID, r.error());
+}
+
+// Runs f(); maps exceptions to status codes.
+template <typename F>
+int guarded(F &&f) {
+    try {
+        return f();
+    } catch (const tiny_llm::HipException &e) {
+        return fail(TL_ERR_HIP, e.what());
+    } catch (const std::exception &e) {
+        return fail(TL_ERR_INVALID, e.what());
+    }
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+const half *as_half(const void *p) { return static_cast<const half *>(p); }
+half       *as_half(void *p) { return static_cast<half *>(p); }
+
+} // namespace
+
+extern "C" {
+
+const char *tl_last_error(void) { return g_last_error.c_str(); }
+
+const char *tl_version(void) { return "tinyllm_kv 0.1.0 gfx950"; }
+
+int tl_kv_create(const tl_kv_config *cfg, tl_kv_manager **out) {
+    if (!out) return fail(TL_ERR_INVALID, "tl_kv_create: out is null");
+    *out = nullptr;
+    if (!cfg) return fail(TL_ERR_INVALID, "tl_kv_create: cfg is null");
+    return guarded([&] {
+        tiny_llm::KVCacheConfig c;
+        c.num_layers = cfg->num_layers;
+        c.num_heads = cfg->num_heads;
+        c.head_dim = cfg->head_dim;
+        c.max_seq_len = cfg->max_seq_len;
+        c.max_batch_size = cfg->max_batch_size;
+        auto r = KVCacheManager::create(c);
+        if (r.isErr()) return fail(TL_ERR_INVALID, r.error());
+        *out = new tl_kv_manager{std::move(r.value())};
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+void tl_kv_destroy(tl_kv_manager *mgr) { delete mgr; }
+
+int tl_kv_allocate_sequence(tl_kv_manager *mgr, int max_len, int *seq_id) {
+    if (!mgr || !seq_id) return fail(TL_ERR_INVALID, "tl_kv_allocate_sequence: null argument");
+    auto r = mgr->m->allocateSequence(max_len);
+    if (r.isOk()) *seq_id = r.value();
+    return status(r);
+}
+
+int tl_kv_release_sequence(tl_kv_manager *mgr, int seq_id) {
+    if (!mgr) return fail(TL_ERR_INVALID, "tl_kv_release_sequence: null manager");
+    return status(mgr->m->releaseSequence(seq_id));
+}
+
+int tl_kv_get_cache(tl_kv_manager *mgr, int seq_id, int layer, void **k_cache, void **v_cache) {
+    if (!mgr) return fail(TL_ERR_INVALID, "tl_kv_get_cache: null manager");
+    auto r = mgr->m->getCacheChecked(seq_id, layer);
+    if (k_cache) *k_cache = r.isOk() ? r.value().first : nullptr;
+    if (v_cache) *v_cache = r.isOk() ? r.value().second : nullptr;
+    return status(r);
+}
+
+int tl_kv_append(tl_kv_manager *mgr, int seq_id, int layer, const void *new_k, const void *new_v,
+                 int num_tokens, void *stream) {
+    if (!mgr) return fail(TL_ERR_INVALID, "tl_kv_append: null manager");
+    return guarded([&] {
+        return status(mgr->m->appendKV(seq_id, layer, as_half(new_k), as_half(new_v), num_tokens,
+                                       as_stream(stream)));
+    });
+}
+
+int tl_kv_advance(tl_kv_manager *mgr, int seq_id, int num_tokens) {
+    if (!mgr) return fail(TL_ERR_INVALID, "tl_kv_advance: null manager");
+    return status(mgr->m->advanceSeqLen(seq_id, num_tokens));
+}
+
+int tl_kv_seq_len(const tl_kv_manager *mgr, int seq_id) { return mgr ? mgr->m->getSeqLen(seq_id) : 0; }
+int tl_kv_has_sequence(const tl_kv_manager *mgr, int seq_id) {
+    return mgr && mgr->m->hasSequence(seq_id) ? 1 : 0;
+}
+size_t tl_kv_used_memory(const tl_kv_manager *mgr) { return mgr ? mgr->m->getUsedMemory() : 0; }
+size_t tl_kv_total_memory(const tl_kv_manager *mgr) { return mgr ? mgr->m->getTotalMemory() : 0; }
+size_t tl_kv_free_memory(const tl_kv_manager *mgr) { return mgr ? mgr->m->getFreeMemory() : 0; }
+int    tl_kv_active_count(const tl_kv_manager *mgr) {
+    return mgr ? mgr->m->getActiveSequenceCount() : 0;
+}
+
+int tl_kv_get_config(const tl_kv_manager *mgr, tl_kv_config *out) {
+    if (!mgr || !out) return fail(TL_ERR_INVALID, "tl_kv_get_config: null argument");
+    const auto &c = mgr->m->getConfig();
+    out->num_layers = c.num_layers;
+    out->num_heads = c.num_heads;
+    out->head_dim = c.head_dim;
+    out->max_seq_len = c.max_seq_len;
+    out->max_batch_size = c.max_batch_size;
+    return TL_OK;
+}
+
+void  *tl_kv_pool(const tl_kv_manager *mgr) { return mgr ? mgr->m->pool() : nullptr; }
+size_t tl_kv_slot_bytes(const tl_kv_manager *mgr) { return mgr ? mgr->m->slotBytes() : 0; }
+int    tl_kv_slot_of(const tl_kv_manager *mgr, int seq_id) { return mgr ? mgr->m->slotOf(seq_id) : -1; }
+
+int tl_kv_set_block_map(tl_kv_manager *mgr, int block_tokens, const int32_t *perm, size_t n) {
+    if (!mgr) return fail(TL_ERR_INVALID, "tl_kv_set_block_map: null manager");
+    return guarded([&] { return status(mgr->m->setBlockMap(block_tokens, perm, n)); });
+}
+
+int tl_kv_batch_create(tl_kv_manager *mgr, int max_seqs, int num_q_heads, tl_kv_batch **out) {
+    if (!mgr || !out) return fail(TL_ERR_INVALID, "tl_kv_batch_create: null argument");
+    *out = nullptr;
+    return guarded([&] {
+        auto r = DecodeBatch::create(*mgr->m, max_seqs, num_q_heads);
+        if (r.isErr()) return fail(TL_ERR_INVALID, r.error());
+        *out = new tl_kv_batch{std::move(r.value())};
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+void tl_kv_batch_destroy(tl_kv_batch *batch) { delete batch; }
+
+int tl_kv_batch_prepare(tl_kv_batch *batch, const int *seq_ids, int n, void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_prepare: null batch");
+    return guarded([&] { return status(batch->b->prepare(seq_ids, n, as_stream(stream))); });
+}
+
+int tl_kv_batch_prepare_lengths(tl_kv_batch *batch, const int *seq_ids, const int *attended, int n,
+                                void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_prepare_lengths: null batch");
+    return guarded(
+        [&] { return status(batch->b->prepareLengths(seq_ids, attended, n, as_stream(stream))); });
+}
+
+int tl_kv_batch_info(const tl_kv_batch *batch, int *n, int *chunk_tokens, int *work_items) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_info: null batch");
+    if (n) *n = batch->b->size();
+    if (chunk_tokens) *chunk_tokens = batch->b->chunkTokens();
+    if (work_items) *work_items = batch->b->workItems();
+    return TL_OK;
+}
+
+int tl_kv_batch_append(tl_kv_batch *batch, int layer_begin, int num_layers, const void *new_k,
+                       const void *new_v, void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_append: null batch");
+    return guarded([&] {
+        return status(batch->b->append(layer_begin, num_layers, as_half(new_k), as_half(new_v),
+                                       as_stream(stream)));
+    });
+}
+
+int tl_kv_batch_attention(tl_kv_batch *batch, int layer, const void *q, void *out, float scale,
+                          void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_attention: null batch");
+    return guarded([&] {
+        return status(batch->b->attention(layer, as_half(q), as_half(out), scale, as_stream(stream)));
+    });
+}
+
+int tl_kv_batch_decode(tl_kv_batch *batch, int layer, const void *q, const void *new_k,
+                       const void *new_v, void *out, float scale, void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_decode: null batch");
+    return guarded([&] {
+        return status(batch->b->decode(layer, as_half(q), as_half(new_k), as_half(new_v),
+                                       as_half(out), scale, as_stream(stream)));
+    });
+}
+
+int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, int s_max,
+                       void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_gather: null batch");
+    return guarded([&] {
+        return status(batch->b->gather(layer, as_half(k_out), as_half(v_out), s_max, as_stream(stream)));
+    });
+}
+
+int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_lens_host, int B,
+                       int Hq, int Hkv, int D, float scale, void *out, void *stream) {
+    if (!kv) return fail(TL_ERR_INVALID, "tl_attn_decode_gqa: kv is null");
+    return guarded([&] {
+        tiny_llm::detail::KvView v;
+        v.k_base = as_half(kv->k_base);
+        v.v_base = as_half(kv->v_base);
+        v.block_table = kv->block_table;
+        v.seq_row = nullptr;
+        v.bt_stride = kv->bt_stride;
+        v.log2_blk = kv->log2_blk;
+        v.blk_stride = kv->blk_stride;
+        v.tok_stride = kv->tok_stride;
+        v.head_stride = kv->head_stride;
+        const std::string err = tiny_llm::detail::attn_decode_view(
+            as_half(q), v, seq_lens_host, B, Hq, Hkv, D, scale, as_half(out), as_stream(stream));
+        if (!err.empty()) return fail(TL_ERR_INVALID, err);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+void tl_attention_decode(const void *q, const void *k, const void *v, void *out, float scale,
+                         int batch, int num_heads, int seq_len, int head_dim, void *stream) {
+    if (batch <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return;
+    (void)guarded([&] {
+        const std::string err = tiny_llm::detail::attn_decode_compact(
+            as_half(q), as_half(k), as_half(v), as_half(out), scale, batch, num_heads, seq_len,
+            head_dim, as_stream(stream));
+        if (!err.empty()) {
+            TLLM_ERROR("%s", err.c_str());
+            return fail(TL_ERR_INVALID, err);
+        }
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+void tl_profile_enable(int on) { tiny_llm::detail::profile_set(on != 0); }
+void tl_profile_reset(void) { tiny_llm::detail::profile_reset(); }
+
+int tl_profile_query(const char *kernel, double *total_ms, long long *launches) {
+    static const char *names[] = {"attn_chunk", "attn_merge", "kv_append", "kv_gather"};
+    if (!kernel || !total_ms || !launches) return fail(TL_ERR_INVALID, "tl_profile_query: null argument");
+    for (int i = 0; i < 4; ++i)
+        if (std::strcmp(kernel, names[i]) == 0)
+            return guarded([&] {
+                tiny_llm::detail::profile_query(i, total_ms, launches);
+                return TL_OK;
+            });
+    return fail(TL_ERR_INVALID, std::string("tl_profile_query: unknown kernel ") + kernel);
+}
+
+} // extern "C"

@@ -1,0 +1,84 @@
+// Launch interface of the HIP kernels of the KV decode path (gfx950).
+// Host code (kv_cache.cpp, capi.cpp) calls only these launchers.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+namespace tiny_llm {
+namespace detail {
+
+// Addressing of (batch entry b, kv head g, token t), in fp16 elements from
+// k_base / v_base:
+//   row(b)  = seq_row ? seq_row[b] : b
+//   blk     = block_table ? block_table[row(b) * bt_stride + (t >> log2_blk)] : row(b)
+//   offset  = blk * blk_stride + (t & (2^log2_blk - 1)) * tok_stride + g * head_stride
+// The reference pool (kv_cache.cpp:69-80, 226-233) is block_table = NULL,
+// seq_row = slot of each entry, blk_stride = slot size, log2_blk = 30.
+struct KvView {
+    const __half  *k_base = nullptr;
+    const __half  *v_base = nullptr;
+    const int32_t *block_table = nullptr;
+    const int32_t *seq_row = nullptr;
+    int            bt_stride = 0;
+    int            log2_blk = 30;
+    int64_t        blk_stride = 0;
+    int64_t        tok_stride = 0;
+    int64_t        head_stride = 0;
+};
+
+// How the split-K work of one attention call is laid out.
+//  - uniform: every entry has uniform_len tokens and nchunk chunks; work item
+//    w = b * nchunk + c (work, seq_lens and part_base are NULL).
+//  - ragged:  seq_lens[b] tokens; work[2w], work[2w+1] = (b, c); the items of
+//    entry b are part_base[b] .. part_base[b+1]-1 in chunk order.
+struct AttnPlan {
+    const int32_t *seq_lens = nullptr;
+    const int32_t *work = nullptr;
+    const int32_t *part_base = nullptr;
+    int            uniform_len = 0;
+    int            nchunk = 1;
+    int            n_work = 0;
+    int            chunk = 512;  // tokens per work item, multiple of 64, <= kChunkMax
+    bool           any_multi = false;  // some entry spans more than one chunk
+    bool           any_empty = false;  // some entry attends to zero tokens
+};
+
+constexpr int kChunkMax = 512;
+
+// Work-list chunk size for a set of lengths (tokens per work item).
+int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len);
+
+// Partials workspace (floats) needed by launch_attn_decode for n_work items.
+size_t attn_workspace_floats(int n_work, int Hq, int D);
+
+// True when (D, Hq/Hkv) has a kernel instantiation.
+bool attn_shape_supported(int D, int G);
+
+// q, out: [B][Hq][D]; part: workspace of attn_workspace_floats() floats.
+void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
+                        int Hkv, int D, float scale, __half *out, float *part, hipStream_t stream);
+
+// One token row ([Hkv][D] contiguous: tok_stride == Hkv*D, head_stride == D)
+// per (entry i, layer l) for n entries and num_layers layers.
+//   position  = wpos ? wpos[i] : first_pos + i
+//   src_k/v   = new_k/new_v + ((l * n) + i) * Hkv*D
+//   dst       = view (shifted by l * layer_stride elements) at (i, position)
+void launch_kv_append(const KvView &view, int64_t layer_stride, const int32_t *wpos, int first_pos,
+                      int n, int num_layers, int row_elems, const __half *new_k,
+                      const __half *new_v, hipStream_t stream);
+
+// out[b][g][t][:] = cache(b, g, t) for t < lens[b] (lens NULL: uniform_len),
+// +0.0 for lens[b] <= t < s_max.  which: 0 = K, 1 = V.
+void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int uniform_len, int n,
+                      int Hkv, int D, int s_max, __half *out, hipStream_t stream);
+
+// Per-kernel event timing (tl_profile_*).
+enum class KernelId { AttnChunk = 0, AttnMerge = 1, KvAppend = 2, KvGather = 3, Count = 4 };
+void profile_begin(KernelId id, hipStream_t stream);
+void profile_end(KernelId id, hipStream_t stream);
+
+} // namespace detail
+} // namespace tiny_llm

@@ -1,0 +1,515 @@
+// KVCacheManager and DecodeBatch for MI355X.
+//
+// Bookkeeping follows src/kv_cache.cpp of the reference (cited per function):
+// the same validation order, error texts, slot policy, id policy, layout and
+// "append does not advance" contract.  Device work is HIP: the pool is one
+// hipMalloc'd block zeroed at create; appendKV keeps the reference's two
+// stream-ordered D2D copies; the batched surface launches the fused kernels
+// of csrc/kernels/.
+#include "tiny_llm/kv_cache.h"
+
+#include "kernels/kv_kernels.h"
+#include "runtime.h"
+#include "tiny_llm/logger.h"
+
+#include <algorithm>
+#include <climits>
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace tiny_llm {
+
+using detail::KvView;
+
+// KVCacheManager::create (kv_cache.cpp:8-60).
+Result<std::unique_ptr<KVCacheManager>> KVCacheManager::create(const KVCacheConfig &config) {
+    using R = Result<std::unique_ptr<KVCacheManager>>;
+    if (config.num_layers <= 0 || config.num_heads <= 0 || config.head_dim <= 0 ||
+        config.max_seq_len <= 0 || config.max_batch_size <= 0) {
+        return R::err("KVCacheManager: invalid configuration parameters");
+    }
+    auto manager = std::unique_ptr<KVCacheManager>(new KVCacheManager(config));
+
+    const size_t kv_per_layer =
+        static_cast<size_t>(config.num_heads) * config.max_seq_len * config.head_dim;
+    const size_t kv_total = kv_per_layer * static_cast<size_t>(config.num_layers) * 2;
+    if (kv_total > SIZE_MAX / sizeof(half)) return R::err("KVCacheManager: memory size overflow");
+    manager->slot_size_ = kv_total * sizeof(half);
+    if (manager->slot_size_ > SIZE_MAX / static_cast<size_t>(config.max_batch_size))
+        return R::err("KVCacheManager: pool size overflow");
+    manager->pool_size_ = manager->slot_size_ * static_cast<size_t>(config.max_batch_size);
+
+    hipError_t err = hipGetDevice(&manager->device_);
+    if (err != hipSuccess)
+        return R::err(std::string("KVCacheManager: hipGetDevice failed: ") + hipGetErrorString(err));
+    err = hipMalloc(reinterpret_cast<void **>(&manager->memory_pool_), manager->pool_size_);
+    if (err != hipSuccess) {
+        manager->memory_pool_ = nullptr;
+        return R::err(std::string("KVCacheManager: hipMalloc failed: ") + hipGetErrorString(err));
+    }
+    err = hipMemset(manager->memory_pool_, 0, manager->pool_size_);
+    if (err != hipSuccess) {
+        (void)hipFree(manager->memory_pool_);
+        manager->memory_pool_ = nullptr;
+        return R::err(std::string("KVCacheManager: hipMemset failed: ") + hipGetErrorString(err));
+    }
+
+    manager->slots_.resize(static_cast<size_t>(config.max_batch_size));
+    for (auto &slot : manager->slots_) {
+        slot.active = false;
+        slot.seq_id = -1;
+        slot.current_len = 0;
+        slot.max_len = config.max_seq_len;
+    }
+    return R::ok(std::move(manager));
+}
+
+// ~KVCacheManager (kv_cache.cpp:62-67).
+KVCacheManager::~KVCacheManager() {
+    if (block_map_dev_) (void)hipFree(block_map_dev_);
+    if (memory_pool_) {
+        (void)hipFree(memory_pool_);
+        memory_pool_ = nullptr;
+    }
+}
+
+// calculateOffset (kv_cache.cpp:69-80): [Layer 0 K][Layer 0 V][Layer 1 K]...
+size_t KVCacheManager::calculateOffset(int slot_idx, int layer_idx, bool is_value) const {
+    const size_t kv_per_layer =
+        static_cast<size_t>(config_.num_heads) * config_.max_seq_len * config_.head_dim;
+    const size_t slot_offset = static_cast<size_t>(slot_idx) * slot_size_ / sizeof(half);
+    const size_t layer_offset = static_cast<size_t>(layer_idx) * kv_per_layer * 2;
+    const size_t kv_offset = is_value ? kv_per_layer : 0;
+    return slot_offset + layer_offset + kv_offset;
+}
+
+// findFreeSlot (kv_cache.cpp:82-89): lowest inactive slot.
+int KVCacheManager::findFreeSlot() const {
+    for (int i = 0; i < static_cast<int>(slots_.size()); ++i)
+        if (!slots_[static_cast<size_t>(i)].active) return i;
+    return -1;
+}
+
+// allocateSequence (kv_cache.cpp:91-119).
+Result<int> KVCacheManager::allocateSequence(int max_len) {
+    if (max_len <= 0 || max_len > config_.max_seq_len) {
+        return Result<int>::err("Invalid max_len: " + std::to_string(max_len) + " (must be 1-" +
+                                std::to_string(config_.max_seq_len) + ")");
+    }
+    const int slot_idx = findFreeSlot();
+    if (slot_idx < 0) {
+        return Result<int>::err("KV cache exhausted: no free slots available. Used: " +
+                                std::to_string(getUsedMemory()) +
+                                " bytes, Total: " + std::to_string(getTotalMemory()) + " bytes");
+    }
+    const int seq_id = next_seq_id_++;
+    auto     &slot = slots_[static_cast<size_t>(slot_idx)];
+    slot.seq_id = seq_id;
+    slot.current_len = 0;
+    slot.max_len = max_len;
+    slot.active = true;
+    seq_to_slot_[seq_id] = slot_idx;
+    return Result<int>::ok(seq_id);
+}
+
+// releaseSequence (kv_cache.cpp:121-137).  Device bytes are not cleared.
+Result<void> KVCacheManager::releaseSequence(int seq_id) {
+    auto it = seq_to_slot_.find(seq_id);
+    if (it == seq_to_slot_.end()) {
+        TLLM_WARN("releaseSequence: sequence not found: %d", seq_id);
+        return Result<void>::err("Sequence not found: " + std::to_string(seq_id));
+    }
+    auto &slot = slots_[static_cast<size_t>(it->second)];
+    slot.active = false;
+    slot.seq_id = -1;
+    slot.current_len = 0;
+    TLLM_DEBUG("KVCache: released sequence %d (slot %d)", seq_id, it->second);
+    seq_to_slot_.erase(it);
+    return Result<void>::ok();
+}
+
+// getCacheChecked (kv_cache.cpp:139-157).
+Result<std::pair<half *, half *>> KVCacheManager::getCacheChecked(int seq_id, int layer_idx) {
+    using R = Result<std::pair<half *, half *>>;
+    auto it = seq_to_slot_.find(seq_id);
+    if (it == seq_to_slot_.end()) return R::err("Sequence not found: " + std::to_string(seq_id));
+    if (layer_idx < 0 || layer_idx >= config_.num_layers) {
+        return R::err("getCache: Invalid layer_idx: " + std::to_string(layer_idx) +
+                      " (valid range: 0-" + std::to_string(config_.num_layers - 1) + ")");
+    }
+    if (isPaged()) {
+        return R::err("getCache: paged layout (block_tokens=" + std::to_string(block_tokens_) +
+                      ") has no contiguous per-sequence region");
+    }
+    const size_t k_offset = calculateOffset(it->second, layer_idx, false);
+    const size_t v_offset = calculateOffset(it->second, layer_idx, true);
+    return R::ok({memory_pool_ + k_offset, memory_pool_ + v_offset});
+}
+
+// getCache (kv_cache.cpp:159-166).
+std::pair<half *, half *> KVCacheManager::getCache(int seq_id, int layer_idx) {
+    auto result = getCacheChecked(seq_id, layer_idx);
+    if (result.isErr()) {
+        TLLM_WARN("getCache: %s", result.error().c_str());
+        return {nullptr, nullptr};
+    }
+    return result.value();
+}
+
+// appendKV (kv_cache.cpp:168-238).
+Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new_k,
+                                      const half *new_v, int num_tokens, hipStream_t stream) {
+    if (new_k == nullptr) {
+        TLLM_ERROR("appendKV: new_k is null");
+        return Result<void>::err("new_k is null");
+    }
+    if (new_v == nullptr) {
+        TLLM_ERROR("appendKV: new_v is null");
+        return Result<void>::err("new_v is null");
+    }
+    if (num_tokens <= 0) {
+        TLLM_ERROR("appendKV: invalid num_tokens: %d", num_tokens);
+        return Result<void>::err("appendKV: num_tokens must be positive: " +
+                                 std::to_string(num_tokens));
+    }
+    if (layer_idx < 0 || layer_idx >= config_.num_layers) {
+        std::string msg = "appendKV: Invalid layer_idx: " + std::to_string(layer_idx) +
+                          " (valid range: 0-" + std::to_string(config_.num_layers - 1) + ")";
+        TLLM_ERROR("%s", msg.c_str());
+        return Result<void>::err(msg);
+    }
+    auto it = seq_to_slot_.find(seq_id);
+    if (it == seq_to_slot_.end()) {
+        TLLM_ERROR("appendKV: sequence not found: %d", seq_id);
+        return Result<void>::err("appendKV: sequence not found: " + std::to_string(seq_id));
+    }
+    const int slot_idx = it->second;
+    auto     &slot = slots_[static_cast<size_t>(slot_idx)];
+    // All layers of a step see the same write position: the length is
+    // advanced once after the last layer (kv_cache.cpp:204-208).
+    const int write_pos = slot.current_len;
+    if (write_pos + num_tokens > slot.max_len) {
+        TLLM_ERROR("appendKV: cache overflow. seq_id=%d, write_pos=%d, num_tokens=%d, max_len=%d",
+                   seq_id, write_pos, num_tokens, slot.max_len);
+        return Result<void>::err("appendKV: cache overflow. Current: " + std::to_string(write_pos) +
+                                 ", appending: " + std::to_string(num_tokens) +
+                                 ", max: " + std::to_string(slot.max_len));
+    }
+    const int row = config_.num_heads * config_.head_dim;
+    if (!isPaged()) {
+        half        *k_cache = memory_pool_ + calculateOffset(slot_idx, layer_idx, false);
+        half        *v_cache = memory_pool_ + calculateOffset(slot_idx, layer_idx, true);
+        const size_t pos_offset = static_cast<size_t>(write_pos) * row;
+        const size_t copy_size = static_cast<size_t>(num_tokens) * row * sizeof(half);
+        HIP_CHECK(hipMemcpyAsync(k_cache + pos_offset, new_k, copy_size, hipMemcpyDeviceToDevice, stream));
+        HIP_CHECK(hipMemcpyAsync(v_cache + pos_offset, new_v, copy_size, hipMemcpyDeviceToDevice, stream));
+    } else {
+        // Paged pool: the tokens cross 16-token blocks, so scatter them with
+        // the append kernel through this slot's row of the block map.
+        KvView v = layerView(layer_idx, nullptr);
+        v.block_table = block_map_dev_ + static_cast<size_t>(slot_idx) * v.bt_stride;
+        v.bt_stride = 0;
+        detail::launch_kv_append(v, 0, nullptr, write_pos, num_tokens, 1, row, new_k, new_v, stream);
+    }
+    TLLM_TRACE("appendKV: seq_id=%d, layer=%d, num_tokens=%d, write_pos=%d", seq_id, layer_idx,
+               num_tokens, write_pos);
+    return Result<void>::ok();
+}
+
+// advanceSeqLen (kv_cache.cpp:240-259).
+Result<void> KVCacheManager::advanceSeqLen(int seq_id, int num_tokens) {
+    if (num_tokens <= 0) {
+        TLLM_ERROR("advanceSeqLen: invalid num_tokens: %d", num_tokens);
+        return Result<void>::err("advanceSeqLen: num_tokens must be positive: " +
+                                 std::to_string(num_tokens));
+    }
+    auto it = seq_to_slot_.find(seq_id);
+    if (it == seq_to_slot_.end()) {
+        TLLM_ERROR("advanceSeqLen: sequence not found: %d", seq_id);
+        return Result<void>::err("advanceSeqLen: sequence not found: " + std::to_string(seq_id));
+    }
+    auto     &slot = slots_[static_cast<size_t>(it->second)];
+    const int old_len = slot.current_len;
+    slot.current_len = std::min(slot.current_len + num_tokens, slot.max_len);
+    TLLM_TRACE("advanceSeqLen: seq_id=%d, %d -> %d", seq_id, old_len, slot.current_len);
+    (void)old_len;
+    return Result<void>::ok();
+}
+
+// getSeqLen / hasSequence / memory statistics (kv_cache.cpp:261-295).
+int KVCacheManager::getSeqLen(int seq_id) const noexcept {
+    auto it = seq_to_slot_.find(seq_id);
+    return it == seq_to_slot_.end() ? 0 : slots_[static_cast<size_t>(it->second)].current_len;
+}
+bool KVCacheManager::hasSequence(int seq_id) const noexcept {
+    return seq_to_slot_.find(seq_id) != seq_to_slot_.end();
+}
+size_t KVCacheManager::getUsedMemory() const noexcept {
+    return static_cast<size_t>(getActiveSequenceCount()) * slot_size_;
+}
+size_t KVCacheManager::getTotalMemory() const noexcept { return pool_size_; }
+size_t KVCacheManager::getFreeMemory() const noexcept { return getTotalMemory() - getUsedMemory(); }
+int    KVCacheManager::getActiveSequenceCount() const noexcept {
+    int count = 0;
+    for (const auto &slot : slots_) count += slot.active ? 1 : 0;
+    return count;
+}
+
+int KVCacheManager::slotOf(int seq_id) const noexcept {
+    auto it = seq_to_slot_.find(seq_id);
+    return it == seq_to_slot_.end() ? -1 : it->second;
+}
+
+const SequenceCache *KVCacheManager::sequence(int seq_id) const noexcept {
+    const int s = slotOf(seq_id);
+    return s < 0 ? nullptr : &slots_[static_cast<size_t>(s)];
+}
+
+Result<void> KVCacheManager::setBlockMap(int block_tokens, const int32_t *perm, size_t n) {
+    if (getActiveSequenceCount() != 0)
+        return Result<void>::err("setBlockMap: the block map can only change with no live sequences");
+    if (perm == nullptr) {
+        if (block_map_dev_) HIP_CHECK(hipFree(block_map_dev_));
+        block_map_dev_ = nullptr;
+        block_map_host_.clear();
+        block_tokens_ = 0;
+        return Result<void>::ok();
+    }
+    if (block_tokens < 16 || (block_tokens & (block_tokens - 1)) != 0 ||
+        config_.max_seq_len % block_tokens != 0) {
+        return Result<void>::err("setBlockMap: block_tokens must be a power of two >= 16 dividing "
+                                 "max_seq_len (got " + std::to_string(block_tokens) + ")");
+    }
+    const size_t per_slot = static_cast<size_t>(config_.max_seq_len / block_tokens);
+    const size_t total = per_slot * static_cast<size_t>(config_.max_batch_size);
+    if (n != total) {
+        return Result<void>::err("setBlockMap: expected " + std::to_string(total) +
+                                 " entries, got " + std::to_string(n));
+    }
+    // Physical block ids in units of block_tokens*num_heads*head_dim elements
+    // from a layer's K base: slot s' block j' -> s' * (2*L*M/bt) + j'.
+    const size_t slot_blocks = 2 * static_cast<size_t>(config_.num_layers) * per_slot;
+    if ((static_cast<size_t>(config_.max_batch_size) - 1) * slot_blocks + per_slot > INT32_MAX)
+        return Result<void>::err("setBlockMap: pool too large for 32-bit block ids");
+    std::vector<char>    seen(total, 0);
+    std::vector<int32_t> phys(total);
+    for (size_t x = 0; x < total; ++x) {
+        const int32_t y = perm[x];
+        if (y < 0 || static_cast<size_t>(y) >= total || seen[static_cast<size_t>(y)])
+            return Result<void>::err("setBlockMap: perm is not a permutation (entry " +
+                                     std::to_string(x) + ")");
+        seen[static_cast<size_t>(y)] = 1;
+        const size_t s = static_cast<size_t>(y) / per_slot, j = static_cast<size_t>(y) % per_slot;
+        phys[x] = static_cast<int32_t>(s * slot_blocks + j);
+    }
+    if (block_map_dev_) HIP_CHECK(hipFree(block_map_dev_));
+    block_map_dev_ = nullptr;
+    HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&block_map_dev_), total * sizeof(int32_t)));
+    HIP_CHECK(hipMemcpy(block_map_dev_, phys.data(), total * sizeof(int32_t), hipMemcpyHostToDevice));
+    block_map_host_ = std::move(phys);
+    block_tokens_ = block_tokens;
+    return Result<void>::ok();
+}
+
+KvView KVCacheManager::layerView(int layer_idx, const int32_t *seq_row_dev) const {
+    const int64_t kv_per_layer =
+        static_cast<int64_t>(config_.num_heads) * config_.max_seq_len * config_.head_dim;
+    KvView v;
+    v.k_base = memory_pool_ + static_cast<int64_t>(layer_idx) * 2 * kv_per_layer;
+    v.v_base = v.k_base + kv_per_layer;
+    v.seq_row = seq_row_dev;
+    v.tok_stride = static_cast<int64_t>(config_.num_heads) * config_.head_dim;
+    v.head_stride = config_.head_dim;
+    if (isPaged()) {
+        int lg = 0;
+        while ((1 << lg) < block_tokens_) ++lg;
+        v.block_table = block_map_dev_;
+        v.bt_stride = config_.max_seq_len / block_tokens_;
+        v.log2_blk = lg;
+        v.blk_stride = static_cast<int64_t>(block_tokens_) * v.tok_stride;
+    } else {
+        v.block_table = nullptr;
+        v.bt_stride = 0;
+        v.log2_blk = 30;
+        v.blk_stride = static_cast<int64_t>(slot_size_ / sizeof(half));
+    }
+    return v;
+}
+
+// ======================================================================
+// DecodeBatch
+// ======================================================================
+
+DecodeBatch::DecodeBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads)
+    : mgr_(mgr), max_seqs_(max_seqs), num_q_heads_(num_q_heads), meta_(new detail::MetaRing(4)),
+      work_(new detail::Workspace()) {}
+
+DecodeBatch::~DecodeBatch() = default;
+
+Result<std::unique_ptr<DecodeBatch>> DecodeBatch::create(KVCacheManager &mgr, int max_seqs,
+                                                         int num_q_heads) {
+    using R = Result<std::unique_ptr<DecodeBatch>>;
+    const KVCacheConfig &cfg = mgr.getConfig();
+    if (max_seqs <= 0) return R::err("DecodeBatch: max_seqs must be positive");
+    if (num_q_heads <= 0 || num_q_heads % cfg.num_heads != 0)
+        return R::err("DecodeBatch: num_q_heads (" + std::to_string(num_q_heads) +
+                      ") must be a positive multiple of num_heads (" +
+                      std::to_string(cfg.num_heads) + ")");
+    if (!detail::attn_shape_supported(cfg.head_dim, num_q_heads / cfg.num_heads))
+        return R::err("DecodeBatch: unsupported head_dim/group (head_dim in {32,64,128,256}, "
+                      "num_q_heads/num_heads in {1,2,4,8})");
+    return R::ok(std::unique_ptr<DecodeBatch>(new DecodeBatch(mgr, max_seqs, num_q_heads)));
+}
+
+Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n, bool appendable,
+                                 hipStream_t stream) {
+    if (n < 0 || n > max_seqs_)
+        return Result<void>::err("DecodeBatch: n=" + std::to_string(n) + " outside [0, " +
+                                 std::to_string(max_seqs_) + "]");
+    if (n > 0 && seq_ids == nullptr) return Result<void>::err("DecodeBatch: seq_ids is null");
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    std::vector<char>    taken(static_cast<size_t>(cfg.max_batch_size), 0);
+    lens_.assign(static_cast<size_t>(n), 0);
+    wpos_.assign(static_cast<size_t>(n), 0);
+    slot_.assign(static_cast<size_t>(n), 0);
+    for (int i = 0; i < n; ++i) {
+        const int            id = seq_ids[i];
+        const SequenceCache *sc = mgr_.sequence(id);
+        if (!sc) return Result<void>::err("DecodeBatch: sequence not found: " + std::to_string(id));
+        const int slot = mgr_.slotOf(id);
+        if (taken[static_cast<size_t>(slot)])
+            return Result<void>::err("DecodeBatch: duplicate sequence in batch: " + std::to_string(id));
+        taken[static_cast<size_t>(slot)] = 1;
+        slot_[static_cast<size_t>(i)] = slot;
+        wpos_[static_cast<size_t>(i)] = sc->current_len;
+        if (appendable) {
+            if (sc->current_len + 1 > sc->max_len) {
+                return Result<void>::err("appendKV: cache overflow. Current: " +
+                                         std::to_string(sc->current_len) +
+                                         ", appending: 1, max: " + std::to_string(sc->max_len));
+            }
+            lens_[static_cast<size_t>(i)] = sc->current_len + 1;
+        } else {
+            const int a = attended[i];
+            if (a < 0 || a > sc->max_len)
+                return Result<void>::err("DecodeBatch: attended length " + std::to_string(a) +
+                                         " of sequence " + std::to_string(id) + " outside [0, " +
+                                         std::to_string(sc->max_len) + "]");
+            lens_[static_cast<size_t>(i)] = a;
+        }
+    }
+    // Split-K plan: work items (entry, chunk) in entry order.
+    chunk_ = detail::choose_chunk(lens_.data(), n, cfg.num_heads, 0);
+    std::vector<int32_t> part_base(static_cast<size_t>(n) + 1, 0);
+    any_multi_ = false;
+    any_empty_ = false;
+    for (int i = 0; i < n; ++i) {
+        const int c = (lens_[static_cast<size_t>(i)] + chunk_ - 1) / chunk_;
+        any_multi_ |= c > 1;
+        any_empty_ |= c == 0;
+        part_base[static_cast<size_t>(i) + 1] = part_base[static_cast<size_t>(i)] + c;
+    }
+    n_work_ = part_base[static_cast<size_t>(n)];
+
+    const size_t n1 = static_cast<size_t>(n);
+    const size_t words = 3 * n1 + (n1 + 1) + 2 * static_cast<size_t>(n_work_);
+    int32_t     *h = static_cast<int32_t *>(meta_->begin(words * sizeof(int32_t)));
+    std::memcpy(h, lens_.data(), n1 * 4);
+    std::memcpy(h + n1, wpos_.data(), n1 * 4);
+    std::memcpy(h + 2 * n1, slot_.data(), n1 * 4);
+    std::memcpy(h + 3 * n1, part_base.data(), (n1 + 1) * 4);
+    int32_t *w = h + 4 * n1 + 1;
+    for (int i = 0; i < n; ++i)
+        for (int c = part_base[static_cast<size_t>(i)]; c < part_base[static_cast<size_t>(i) + 1]; ++c) {
+            *w++ = i;
+            *w++ = c - part_base[static_cast<size_t>(i)];
+        }
+    const int32_t *d = static_cast<const int32_t *>(meta_->commit(stream));
+    d_lens_ = d;
+    d_wpos_ = d + n1;
+    d_slot_ = d + 2 * n1;
+    d_part_base_ = d + 3 * n1;
+    d_work_ = d + 4 * n1 + 1;
+    n_ = n;
+    appendable_ = appendable;
+    return Result<void>::ok();
+}
+
+Result<void> DecodeBatch::prepare(const int *seq_ids, int n, hipStream_t stream) {
+    return upload(seq_ids, nullptr, n, true, stream);
+}
+
+Result<void> DecodeBatch::prepareLengths(const int *seq_ids, const int *attended, int n,
+                                         hipStream_t stream) {
+    if (n > 0 && attended == nullptr) return Result<void>::err("DecodeBatch: attended is null");
+    return upload(seq_ids, attended, n, false, stream);
+}
+
+Result<void> DecodeBatch::append(int layer_begin, int num_layers, const half *new_k,
+                                 const half *new_v, hipStream_t stream) {
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    if (!appendable_)
+        return Result<void>::err("DecodeBatch: append needs a batch made by prepare()");
+    if (new_k == nullptr) return Result<void>::err("new_k is null");
+    if (new_v == nullptr) return Result<void>::err("new_v is null");
+    if (num_layers <= 0 || layer_begin < 0 || layer_begin + num_layers > cfg.num_layers)
+        return Result<void>::err("DecodeBatch: layers [" + std::to_string(layer_begin) + ", " +
+                                 std::to_string(layer_begin + num_layers) + ") outside [0, " +
+                                 std::to_string(cfg.num_layers) + ")");
+    if (n_ == 0) return Result<void>::ok();
+    const KvView  v = mgr_.layerView(layer_begin, d_slot_);
+    const int64_t layer_stride =
+        2 * static_cast<int64_t>(cfg.num_heads) * cfg.max_seq_len * cfg.head_dim;
+    detail::launch_kv_append(v, layer_stride, d_wpos_, 0, n_, num_layers,
+                             cfg.num_heads * cfg.head_dim, new_k, new_v, stream);
+    return Result<void>::ok();
+}
+
+Result<void> DecodeBatch::attention(int layer_idx, const half *q, half *out, float scale,
+                                    hipStream_t stream) {
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    if (q == nullptr || out == nullptr) return Result<void>::err("DecodeBatch: q/out is null");
+    if (layer_idx < 0 || layer_idx >= cfg.num_layers)
+        return Result<void>::err("DecodeBatch: Invalid layer_idx: " + std::to_string(layer_idx));
+    if (n_ == 0) return Result<void>::ok();
+    detail::AttnPlan plan;
+    plan.seq_lens = d_lens_;
+    plan.work = d_work_;
+    plan.part_base = d_part_base_;
+    plan.n_work = n_work_;
+    plan.chunk = chunk_;
+    plan.any_multi = any_multi_;
+    plan.any_empty = any_empty_;
+    float *part = nullptr;
+    if (any_multi_)
+        part = work_->get(detail::attn_workspace_floats(n_work_, num_q_heads_, cfg.head_dim));
+    detail::launch_attn_decode(q, mgr_.layerView(layer_idx, d_slot_), plan, n_, num_q_heads_,
+                               cfg.num_heads, cfg.head_dim, scale, out, part, stream);
+    return Result<void>::ok();
+}
+
+Result<void> DecodeBatch::decode(int layer_idx, const half *q, const half *new_k,
+                                 const half *new_v, half *out, float scale, hipStream_t stream) {
+    auto r = append(layer_idx, 1, new_k, new_v, stream);
+    if (r.isErr()) return r;
+    return attention(layer_idx, q, out, scale, stream);
+}
+
+Result<void> DecodeBatch::gather(int layer_idx, half *k_out, half *v_out, int s_max,
+                                 hipStream_t stream) {
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    if (layer_idx < 0 || layer_idx >= cfg.num_layers)
+        return Result<void>::err("DecodeBatch: Invalid layer_idx: " + std::to_string(layer_idx));
+    if (s_max < 0) return Result<void>::err("DecodeBatch: s_max must be >= 0");
+    if (n_ == 0 || s_max == 0) return Result<void>::ok();
+    const KvView v = mgr_.layerView(layer_idx, d_slot_);
+    if (k_out)
+        detail::launch_kv_gather(v, 0, d_lens_, 0, n_, cfg.num_heads, cfg.head_dim, s_max, k_out, stream);
+    if (v_out)
+        detail::launch_kv_gather(v, 1, d_lens_, 0, n_, cfg.num_heads, cfg.head_dim, s_max, v_out, stream);
+    return Result<void>::ok();
+}
+
+} // namespace tiny_llm

@@ -1,0 +1,229 @@
+#include "runtime.h"
+
+#include "kernels/kv_kernels.h"
+#include "tiny_llm/hip_utils.h"
+#include "tiny_llm/logger.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <array>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <utility>
+
+namespace tiny_llm {
+
+// ------------------------------------------------------------------ logger
+namespace {
+LogLevel level_from_env() {
+    const char *s = std::getenv("TLLM_LOG_LEVEL");
+    if (!s) return LogLevel::WARN;
+    const std::pair<const char *, LogLevel> names[] = {
+        {"trace", LogLevel::TRACE}, {"debug", LogLevel::DEBUG}, {"info", LogLevel::INFO},
+        {"warn", LogLevel::WARN},   {"error", LogLevel::ERROR}, {"critical", LogLevel::CRITICAL},
+        {"off", LogLevel::OFF}};
+    for (const auto &n : names)
+        if (std::strcmp(s, n.first) == 0) return n.second;
+    return LogLevel::WARN;
+}
+std::atomic<int> g_level{-1};
+const char      *level_name(LogLevel l) {
+    static const char *n[] = {"trace", "debug", "info", "warn", "error", "critical", "off"};
+    return n[static_cast<int>(l)];
+}
+} // namespace
+
+void Logger::setLevel(LogLevel level) { g_level.store(static_cast<int>(level)); }
+
+LogLevel Logger::level() {
+    int l = g_level.load(std::memory_order_relaxed);
+    if (l < 0) {
+        l = static_cast<int>(level_from_env());
+        g_level.store(l);
+    }
+    return static_cast<LogLevel>(l);
+}
+
+void Logger::log(LogLevel level, const char *fmt, ...) {
+    char    buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    std::fprintf(stderr, "[tiny_llm] [%s] %s\n", level_name(level), buf);
+}
+
+namespace detail {
+
+int current_device() {
+    int d = 0;
+    HIP_CHECK(hipGetDevice(&d));
+    return d;
+}
+
+// ---------------------------------------------------------------- MetaRing
+MetaRing::MetaRing(int slots) : slots_(static_cast<size_t>(slots)) {}
+
+MetaRing::~MetaRing() {
+    for (auto &s : slots_) {
+        if (s.ev) {
+            (void)hipEventSynchronize(s.ev);
+            (void)hipEventDestroy(s.ev);
+        }
+        if (s.host) (void)hipHostFree(s.host);
+        if (s.dev) (void)hipFree(s.dev);
+    }
+}
+
+void *MetaRing::begin(size_t bytes) {
+    cur_ = (cur_ + 1) % static_cast<int>(slots_.size());
+    Slot &s = slots_[static_cast<size_t>(cur_)];
+    if (s.pending) {
+        HIP_CHECK(hipEventSynchronize(s.ev));
+        s.pending = false;
+    }
+    if (bytes == 0) bytes = 16;
+    if (s.cap < bytes) {
+        size_t cap = 4096;
+        while (cap < bytes) cap <<= 1;
+        if (s.host) HIP_CHECK(hipHostFree(s.host));
+        if (s.dev) {
+            HIP_CHECK(hipDeviceSynchronize()); // kernels may still read the old slot
+            HIP_CHECK(hipFree(s.dev));
+        }
+        s.host = nullptr;
+        s.dev = nullptr;
+        HIP_CHECK(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
+        HIP_CHECK(hipMalloc(&s.dev, cap));
+        s.cap = cap;
+    }
+    if (!s.ev) HIP_CHECK(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
+    bytes_ = bytes;
+    return s.host;
+}
+
+void *MetaRing::commit(hipStream_t stream) {
+    Slot &s = slots_[static_cast<size_t>(cur_)];
+    HIP_CHECK(hipMemcpyAsync(s.dev, s.host, bytes_, hipMemcpyHostToDevice, stream));
+    HIP_CHECK(hipEventRecord(s.ev, stream));
+    s.pending = true;
+    return s.dev;
+}
+
+// --------------------------------------------------------------- Workspace
+Workspace::~Workspace() {
+    if (ptr_) (void)hipFree(ptr_);
+}
+
+float *Workspace::get(size_t floats) {
+    if (floats == 0) return ptr_;
+    if (floats > cap_) {
+        if (ptr_) {
+            HIP_CHECK(hipDeviceSynchronize());
+            HIP_CHECK(hipFree(ptr_));
+            ptr_ = nullptr;
+            cap_ = 0;
+        }
+        size_t cap = 1 << 16;
+        while (cap < floats) cap <<= 1;
+        HIP_CHECK(hipMalloc(&ptr_, cap * sizeof(float)));
+        cap_ = cap;
+    }
+    return ptr_;
+}
+
+// ----------------------------------------------------------- DeviceContext
+void DeviceContext::claim(hipStream_t stream) {
+    if (used && last_stream != stream) HIP_CHECK(hipStreamSynchronize(last_stream));
+    last_stream = stream;
+    used = true;
+}
+
+DeviceContext &DeviceContext::get(int device) {
+    static std::mutex                                 mu;
+    static std::map<int, std::unique_ptr<DeviceContext>> ctxs;
+    std::lock_guard<std::mutex>                       lk(mu);
+    auto                                             &p = ctxs[device];
+    if (!p) p.reset(new DeviceContext());
+    return *p;
+}
+
+// ---------------------------------------------------------------- profiling
+namespace {
+struct ProfState {
+    std::mutex                                          mu;
+    std::atomic<bool>                                   on{false};
+    std::array<std::vector<std::pair<hipEvent_t, hipEvent_t>>, 4> done;
+    std::array<hipEvent_t, 4>                           open{};
+};
+ProfState &prof() {
+    static ProfState p;
+    return p;
+}
+} // namespace
+
+void profile_begin(KernelId id, hipStream_t stream) {
+    ProfState &p = prof();
+    if (!p.on.load(std::memory_order_relaxed)) return;
+    std::lock_guard<std::mutex> lk(p.mu);
+    hipEvent_t                  e;
+    HIP_CHECK(hipEventCreate(&e));
+    HIP_CHECK(hipEventRecord(e, stream));
+    p.open[static_cast<size_t>(id)] = e;
+}
+
+void profile_end(KernelId id, hipStream_t stream) {
+    ProfState &p = prof();
+    if (!p.on.load(std::memory_order_relaxed)) return;
+    std::lock_guard<std::mutex> lk(p.mu);
+    hipEvent_t                  start = p.open[static_cast<size_t>(id)];
+    if (!start) return;
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreate(&e));
+    HIP_CHECK(hipEventRecord(e, stream));
+    p.done[static_cast<size_t>(id)].emplace_back(start, e);
+    p.open[static_cast<size_t>(id)] = nullptr;
+}
+
+void profile_set(bool on) { prof().on.store(on); }
+
+void profile_reset() {
+    ProfState                  &p = prof();
+    std::lock_guard<std::mutex> lk(p.mu);
+    for (auto &v : p.done) {
+        for (auto &pr : v) {
+            (void)hipEventSynchronize(pr.second);
+            (void)hipEventDestroy(pr.first);
+            (void)hipEventDestroy(pr.second);
+        }
+        v.clear();
+    }
+    for (auto &o : p.open) {
+        if (o) (void)hipEventDestroy(o);
+        o = nullptr;
+    }
+}
+
+bool profile_query(int id, double *total_ms, long long *launches) {
+    if (id < 0 || id >= 4) return false;
+    ProfState                  &p = prof();
+    std::lock_guard<std::mutex> lk(p.mu);
+    double                      tot = 0.0;
+    for (auto &pr : p.done[static_cast<size_t>(id)]) {
+        HIP_CHECK(hipEventSynchronize(pr.second));
+        float ms = 0.0f;
+        HIP_CHECK(hipEventElapsedTime(&ms, pr.first, pr.second));
+        tot += ms;
+    }
+    *total_ms = tot;
+    *launches = static_cast<long long>(p.done[static_cast<size_t>(id)].size());
+    return true;
+}
+
+} // namespace detail
+} // namespace tiny_llm

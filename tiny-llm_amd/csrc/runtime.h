@@ -1,0 +1,77 @@
+// Host runtime pieces of the KV path: metadata staging, device workspace,
+// the per-device context of the stateless entry points.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <mutex>
+#include <vector>
+
+namespace tiny_llm {
+namespace detail {
+
+// Ring of (pinned host, device) buffer pairs for per-step metadata.  begin()
+// returns host memory to fill; commit() queues one async H2D copy on the
+// stream and returns the device copy.  A slot is rewritten only after its
+// previous copy has completed (event), so the host never overwrites bytes a
+// pending copy still reads; kernels that read a device slot are ordered
+// before its next copy by the stream.
+class MetaRing {
+  public:
+    explicit MetaRing(int slots = 4);
+    ~MetaRing();
+    MetaRing(const MetaRing &) = delete;
+    MetaRing &operator=(const MetaRing &) = delete;
+
+    void *begin(size_t bytes);
+    void *commit(hipStream_t stream);
+
+  private:
+    struct Slot {
+        void      *host = nullptr;
+        void      *dev = nullptr;
+        size_t     cap = 0;
+        hipEvent_t ev = nullptr;
+        bool       pending = false;
+    };
+    std::vector<Slot> slots_;
+    int               cur_ = -1;
+    size_t            bytes_ = 0;
+};
+
+// Grow-only device buffer (split-K partials).
+class Workspace {
+  public:
+    Workspace() = default;
+    ~Workspace();
+    Workspace(const Workspace &) = delete;
+    Workspace &operator=(const Workspace &) = delete;
+    float *get(size_t floats);
+
+  private:
+    float *ptr_ = nullptr;
+    size_t cap_ = 0;
+};
+
+// Staging + workspace of the stateless entry points, one per device.
+struct DeviceContext {
+    std::mutex  mu;
+    MetaRing    ring;
+    Workspace   ws;
+    hipStream_t last_stream = nullptr;
+    bool        used = false;
+    // Orders this call after the previous user of the shared workspace.
+    void claim(hipStream_t stream);
+    static DeviceContext &get(int device);
+};
+
+int current_device();
+
+// Event timing of the launchers (tl_profile_*); ids are KernelId values.
+void profile_set(bool on);
+void profile_reset();
+bool profile_query(int id, double *total_ms, long long *launches);
+
+} // namespace detail
+} // namespace tiny_llm

@@ -1,0 +1,152 @@
+// KVCacheManager for MI355X: the reference API (include/tiny_llm/kv_cache.h:
+// 15-111) with its semantics and pool layout unchanged, plus the batched
+// decode surface (DecodeBatch) that drives the fused HIP kernels.
+//
+// Pool layout (kv_cache.cpp:69-80, 226-233), one hipMalloc'd block:
+//   [slot][layer][K|V][max_seq_len][num_heads][head_dim]  fp16
+// so a token's K (or V) row of num_heads*head_dim halves is contiguous.
+#pragma once
+
+#include "tiny_llm/hip_utils.h"
+#include "tiny_llm/result.h"
+#include "tiny_llm/types.h"
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <memory>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+namespace tiny_llm {
+
+namespace detail {
+struct KvView;
+class MetaRing;
+class Workspace;
+} // namespace detail
+
+// Per-sequence cache state (kv_cache.h:15-20).
+struct SequenceCache {
+    int  seq_id = -1;
+    int  current_len = 0;
+    int  max_len = 0;
+    bool active = false;
+};
+
+class KVCacheManager {
+  public:
+    static Result<std::unique_ptr<KVCacheManager>> create(const KVCacheConfig &config);
+
+    ~KVCacheManager();
+    KVCacheManager(const KVCacheManager &) = delete;
+    KVCacheManager &operator=(const KVCacheManager &) = delete;
+    KVCacheManager(KVCacheManager &&) = delete;
+    KVCacheManager &operator=(KVCacheManager &&) = delete;
+
+    Result<int>  allocateSequence(int max_len);
+    Result<void> releaseSequence(int seq_id);
+
+    std::pair<half *, half *>         getCache(int seq_id, int layer_idx);
+    Result<std::pair<half *, half *>> getCacheChecked(int seq_id, int layer_idx);
+
+    // Copies num_tokens tokens to the sequence tail; does NOT advance the
+    // visible length (the caller advances once after all layers).
+    Result<void> appendKV(int seq_id, int layer_idx, const half *new_k, const half *new_v,
+                          int num_tokens, hipStream_t stream = 0);
+    Result<void> advanceSeqLen(int seq_id, int num_tokens);
+
+    int    getSeqLen(int seq_id) const noexcept;
+    bool   hasSequence(int seq_id) const noexcept;
+    size_t getUsedMemory() const noexcept;
+    size_t getTotalMemory() const noexcept;
+    size_t getFreeMemory() const noexcept;
+    int    getActiveSequenceCount() const noexcept;
+
+    const KVCacheConfig &getConfig() const noexcept { return config_; }
+
+    // ---- additions of the batched path ----
+    // Paged addressing over the same pool (see tl_kv_set_block_map).
+    Result<void>         setBlockMap(int block_tokens, const int32_t *perm, size_t n);
+    bool                 isPaged() const noexcept { return block_tokens_ > 0; }
+    int                  blockTokens() const noexcept { return block_tokens_; }
+    int                  slotOf(int seq_id) const noexcept;
+    const SequenceCache *sequence(int seq_id) const noexcept;
+    half                *pool() const noexcept { return memory_pool_; }
+    size_t               slotBytes() const noexcept { return slot_size_; }
+    int                  device() const noexcept { return device_; }
+    // Layer view for batch kernels; seq_row_dev holds the slot of each entry.
+    detail::KvView layerView(int layer_idx, const int32_t *seq_row_dev) const;
+
+  private:
+    explicit KVCacheManager(const KVCacheConfig &config) : config_(config) {}
+
+    size_t calculateOffset(int slot_idx, int layer_idx, bool is_value) const;
+    int    findFreeSlot() const;
+
+    KVCacheConfig config_;
+    half         *memory_pool_ = nullptr;
+    size_t        pool_size_ = 0;
+    std::vector<SequenceCache>   slots_;
+    std::unordered_map<int, int> seq_to_slot_;
+    int                          next_seq_id_ = 0;
+    size_t                       slot_size_ = 0;
+    int                          device_ = 0;
+
+    int      block_tokens_ = 0;          // 0: reference layout
+    int32_t *block_map_dev_ = nullptr;   // [max_batch][max_seq_len/bt] physical block ids
+    std::vector<int32_t> block_map_host_;
+};
+
+// A decode step over n sequences of one manager.  prepare() snapshots the
+// write position (getSeqLen) and attended length (getSeqLen + 1) of each
+// sequence and uploads them once; every layer's append / attention / gather
+// then reads that snapshot.  One batch is used from one stream (or the caller
+// orders streams); entries must be distinct live sequences.
+class DecodeBatch {
+  public:
+    static Result<std::unique_ptr<DecodeBatch>> create(KVCacheManager &mgr, int max_seqs,
+                                                       int num_q_heads);
+    ~DecodeBatch();
+    DecodeBatch(const DecodeBatch &) = delete;
+    DecodeBatch &operator=(const DecodeBatch &) = delete;
+
+    Result<void> prepare(const int *seq_ids, int n, hipStream_t stream);
+    Result<void> prepareLengths(const int *seq_ids, const int *attended, int n, hipStream_t stream);
+
+    Result<void> append(int layer_begin, int num_layers, const half *new_k, const half *new_v,
+                        hipStream_t stream);
+    Result<void> attention(int layer_idx, const half *q, half *out, float scale, hipStream_t stream);
+    Result<void> decode(int layer_idx, const half *q, const half *new_k, const half *new_v, half *out,
+                        float scale, hipStream_t stream);
+    Result<void> gather(int layer_idx, half *k_out, half *v_out, int s_max, hipStream_t stream);
+
+    int size() const noexcept { return n_; }
+    int chunkTokens() const noexcept { return chunk_; }
+    int workItems() const noexcept { return n_work_; }
+    const std::vector<int32_t> &attendedLengths() const noexcept { return lens_; }
+
+  private:
+    DecodeBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads);
+    Result<void> upload(const int *seq_ids, const int *attended, int n, bool appendable,
+                        hipStream_t stream);
+
+    KVCacheManager &mgr_;
+    int             max_seqs_;
+    int             num_q_heads_;
+    int             n_ = 0;
+    bool            appendable_ = false;
+    int             chunk_ = 0;
+    int             n_work_ = 0;
+    bool            any_multi_ = false;
+    bool            any_empty_ = false;
+    std::vector<int32_t> lens_, wpos_, slot_;
+    std::unique_ptr<detail::MetaRing>  meta_;
+    std::unique_ptr<detail::Workspace> work_;
+    const int32_t  *d_lens_ = nullptr, *d_wpos_ = nullptr, *d_slot_ = nullptr;
+    const int32_t  *d_part_base_ = nullptr, *d_work_ = nullptr;
+};
+
+} // namespace tiny_llm

@@ -1,0 +1,298 @@
+"""ctypes binding of libtinyllm_kv.so (the C ABI of include/tinyllm_kv.h).
+
+This is the host-side mirror used by tests/, bench.py and __graft_entry__:
+the same names and argument meaning as the reference's KVCacheManager
+(include/tiny_llm/kv_cache.h) and attention_decode (kernels/attention.cuh),
+plus the batched decode surface.  Device memory is passed as integer device
+addresses (e.g. torch tensor .data_ptr()); streams as integer hipStream_t
+handles (0 = default stream).
+
+There is no fallback: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_REPO = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(_HERE, "_build", "libtinyllm_kv.so")
+HEADER_PATH = os.path.join(_REPO, "include", "tinyllm_kv.h")
+
+TL_OK = 0
+TL_ERR_INVALID = -1
+TL_ERR_HIP = -2
+
+_lib = None
+
+
+class TinyLLMError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+        self.msg = msg
+
+
+def build(jobs: int = 8) -> str:
+    """Compile the HIP library for gfx950 (always runs make; make skips
+    up-to-date objects)."""
+    subprocess.run(["make", "-s", "-C", _HERE, f"-j{jobs}"], check=True)
+    return LIB_PATH
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is not built; run __graft_entry__.build() (or make -C tiny-llm_amd)")
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class KVConfig(C.Structure):
+    _fields_ = [("num_layers", C.c_int), ("num_heads", C.c_int), ("head_dim", C.c_int),
+                ("max_seq_len", C.c_int), ("max_batch_size", C.c_int)]
+
+
+class KVView(C.Structure):
+    _fields_ = [("k_base", C.c_void_p), ("v_base", C.c_void_p), ("block_table", C.c_void_p),
+                ("bt_stride", C.c_int), ("log2_blk", C.c_int), ("blk_stride", C.c_int64),
+                ("tok_stride", C.c_int64), ("head_stride", C.c_int64)]
+
+
+def _declare(L: C.CDLL) -> None:
+    vp, i, sz, f = C.c_void_p, C.c_int, C.c_size_t, C.c_float
+    ip = C.POINTER(C.c_int)
+    sig = {
+        "tl_last_error": (C.c_char_p, []),
+        "tl_version": (C.c_char_p, []),
+        "tl_kv_create": (i, [C.POINTER(KVConfig), C.POINTER(vp)]),
+        "tl_kv_destroy": (None, [vp]),
+        "tl_kv_allocate_sequence": (i, [vp, i, ip]),
+        "tl_kv_release_sequence": (i, [vp, i]),
+        "tl_kv_get_cache": (i, [vp, i, i, C.POINTER(vp), C.POINTER(vp)]),
+        "tl_kv_append": (i, [vp, i, i, vp, vp, i, vp]),
+        "tl_kv_advance": (i, [vp, i, i]),
+        "tl_kv_seq_len": (i, [vp, i]),
+        "tl_kv_has_sequence": (i, [vp, i]),
+        "tl_kv_used_memory": (sz, [vp]),
+        "tl_kv_total_memory": (sz, [vp]),
+        "tl_kv_free_memory": (sz, [vp]),
+        "tl_kv_active_count": (i, [vp]),
+        "tl_kv_get_config": (i, [vp, C.POINTER(KVConfig)]),
+        "tl_kv_pool": (vp, [vp]),
+        "tl_kv_slot_bytes": (sz, [vp]),
+        "tl_kv_slot_of": (i, [vp, i]),
+        "tl_kv_set_block_map": (i, [vp, i, vp, sz]),
+        "tl_kv_batch_create": (i, [vp, i, i, C.POINTER(vp)]),
+        "tl_kv_batch_destroy": (None, [vp]),
+        "tl_kv_batch_prepare": (i, [vp, vp, i, vp]),
+        "tl_kv_batch_prepare_lengths": (i, [vp, vp, vp, i, vp]),
+        "tl_kv_batch_info": (i, [vp, ip, ip, ip]),
+        "tl_kv_batch_append": (i, [vp, i, i, vp, vp, vp]),
+        "tl_kv_batch_attention": (i, [vp, i, vp, vp, f, vp]),
+        "tl_kv_batch_decode": (i, [vp, i, vp, vp, vp, vp, f, vp]),
+        "tl_kv_batch_gather": (i, [vp, i, vp, vp, i, vp]),
+        "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
+        "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
+        "tl_profile_enable": (None, [i]),
+        "tl_profile_reset": (None, []),
+        "tl_profile_query": (i, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def header_symbols(path: str = HEADER_PATH) -> list[str]:
+    """Every function the public header declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tl_[a-z0-9_]+)\s*\(", text)))
+
+
+def last_error() -> str:
+    return load().tl_last_error().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != TL_OK:
+        raise TinyLLMError(rc, last_error())
+
+
+def _int_array(vals):
+    vals = list(vals)
+    return (C.c_int * max(1, len(vals)))(*vals), len(vals)
+
+
+class KVCacheManager:
+    """tiny_llm::KVCacheManager over HIP (same method names as the reference)."""
+
+    def __init__(self, num_layers=32, num_heads=32, head_dim=128, max_seq_len=2048,
+                 max_batch_size=1):
+        L = load()
+        self.config = KVConfig(num_layers, num_heads, head_dim, max_seq_len, max_batch_size)
+        self._h = C.c_void_p()
+        _check(L.tl_kv_create(C.byref(self.config), C.byref(self._h)))
+
+    @classmethod
+    def create(cls, **cfg):
+        """Result-style factory: (manager, None) or (None, error message)."""
+        try:
+            return cls(**cfg), None
+        except TinyLLMError as e:
+            return None, e.msg
+
+    def close(self):
+        if getattr(self, "_h", None):
+            load().tl_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    # Result<T>-like methods return (value, error) with error None on success.
+    def allocateSequence(self, max_len):
+        out = C.c_int(-1)
+        rc = load().tl_kv_allocate_sequence(self._h, max_len, C.byref(out))
+        return (out.value, None) if rc == TL_OK else (None, last_error())
+
+    def releaseSequence(self, seq_id):
+        rc = load().tl_kv_release_sequence(self._h, seq_id)
+        return None if rc == TL_OK else last_error()
+
+    def getCacheChecked(self, seq_id, layer_idx):
+        k, v = C.c_void_p(), C.c_void_p()
+        rc = load().tl_kv_get_cache(self._h, seq_id, layer_idx, C.byref(k), C.byref(v))
+        return ((k.value or 0, v.value or 0), None) if rc == TL_OK else (None, last_error())
+
+    def getCache(self, seq_id, layer_idx):
+        r, _ = self.getCacheChecked(seq_id, layer_idx)
+        return r if r is not None else (0, 0)
+
+    def appendKV(self, seq_id, layer_idx, new_k, new_v, num_tokens, stream=0):
+        rc = load().tl_kv_append(self._h, seq_id, layer_idx, new_k, new_v, num_tokens, stream)
+        if rc == TL_ERR_HIP:
+            raise TinyLLMError(rc, last_error())
+        return None if rc == TL_OK else last_error()
+
+    def advanceSeqLen(self, seq_id, num_tokens):
+        rc = load().tl_kv_advance(self._h, seq_id, num_tokens)
+        return None if rc == TL_OK else last_error()
+
+    def getSeqLen(self, seq_id):
+        return load().tl_kv_seq_len(self._h, seq_id)
+
+    def hasSequence(self, seq_id):
+        return bool(load().tl_kv_has_sequence(self._h, seq_id))
+
+    def getUsedMemory(self):
+        return load().tl_kv_used_memory(self._h)
+
+    def getTotalMemory(self):
+        return load().tl_kv_total_memory(self._h)
+
+    def getFreeMemory(self):
+        return load().tl_kv_free_memory(self._h)
+
+    def getActiveSequenceCount(self):
+        return load().tl_kv_active_count(self._h)
+
+    def getConfig(self):
+        c = KVConfig()
+        _check(load().tl_kv_get_config(self._h, C.byref(c)))
+        return c
+
+    def pool(self) -> int:
+        return load().tl_kv_pool(self._h) or 0
+
+    def slot_bytes(self) -> int:
+        return load().tl_kv_slot_bytes(self._h)
+
+    def slot_of(self, seq_id) -> int:
+        return load().tl_kv_slot_of(self._h, seq_id)
+
+    def setBlockMap(self, block_tokens, perm):
+        if perm is None:
+            rc = load().tl_kv_set_block_map(self._h, block_tokens, None, 0)
+        else:
+            import numpy as np
+            p = np.ascontiguousarray(perm, dtype=np.int32)
+            rc = load().tl_kv_set_block_map(self._h, block_tokens, p.ctypes.data, p.size)
+        return None if rc == TL_OK else last_error()
+
+
+class DecodeBatch:
+    """Batched decode step over a KVCacheManager (tl_kv_batch_*)."""
+
+    def __init__(self, mgr: KVCacheManager, max_seqs: int, num_q_heads: int):
+        self._mgr = mgr
+        self._h = C.c_void_p()
+        _check(load().tl_kv_batch_create(mgr._h, max_seqs, num_q_heads, C.byref(self._h)))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            load().tl_kv_batch_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def prepare(self, seq_ids, stream=0):
+        arr, n = _int_array(seq_ids)
+        _check(load().tl_kv_batch_prepare(self._h, arr, n, stream))
+
+    def prepare_lengths(self, seq_ids, attended, stream=0):
+        ids, n = _int_array(seq_ids)
+        att, m = _int_array(attended)
+        assert n == m
+        _check(load().tl_kv_batch_prepare_lengths(self._h, ids, att, n, stream))
+
+    def info(self):
+        n, chunk, work = C.c_int(), C.c_int(), C.c_int()
+        _check(load().tl_kv_batch_info(self._h, C.byref(n), C.byref(chunk), C.byref(work)))
+        return {"n": n.value, "chunk_tokens": chunk.value, "work_items": work.value}
+
+    def append(self, layer_begin, num_layers, new_k, new_v, stream=0):
+        _check(load().tl_kv_batch_append(self._h, layer_begin, num_layers, new_k, new_v, stream))
+
+    def attention(self, layer, q, out, scale, stream=0):
+        _check(load().tl_kv_batch_attention(self._h, layer, q, out, scale, stream))
+
+    def decode(self, layer, q, new_k, new_v, out, scale, stream=0):
+        _check(load().tl_kv_batch_decode(self._h, layer, q, new_k, new_v, out, scale, stream))
+
+    def gather(self, layer, k_out, v_out, s_max, stream=0):
+        _check(load().tl_kv_batch_gather(self._h, layer, k_out or None, v_out or None, s_max, stream))
+
+
+def attn_decode_gqa(q, view: KVView, seq_lens, Hq, Hkv, D, scale, out, stream=0):
+    import numpy as np
+    lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    _check(load().tl_attn_decode_gqa(q, C.byref(view), lens.ctypes.data, lens.size, Hq, Hkv, D,
+                                     scale, out, stream))
+
+
+def attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, stream=0):
+    """tiny_llm::kernels::attention_decode (void; errors go to the log and
+    tl_last_error)."""
+    load().tl_attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, stream)
+
+
+def profile_enable(on: bool = True):
+    load().tl_profile_enable(1 if on else 0)
+
+
+def profile_reset():
+    load().tl_profile_reset()
+
+
+def profile_query(kernel: str):
+    ms, n = C.c_double(), C.c_longlong()
+    _check(load().tl_profile_query(kernel.encode(), C.byref(ms), C.byref(n)))
+    return ms.value, n.value
