@@ -9,6 +9,7 @@
 #include "tiny_llm/hip_utils.h"
 #include "tiny_llm/logger.h"
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <mutex>
@@ -41,7 +42,7 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
     for (int b = 0; b < B; ++b)
         if (seq_lens_host[b] < 0) return "tl_attn_decode_gqa: negative sequence length";
 
-    const int            chunk = choose_chunk(seq_lens_host, B, Hkv, 0);
+    const int            chunk = choose_chunk(seq_lens_host, B, Hkv, 0, D);
     std::vector<int32_t> part_base(static_cast<size_t>(B) + 1, 0);
     bool                 any_multi = false, any_empty = false;
     for (int b = 0; b < B; ++b) {
@@ -74,8 +75,9 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
     plan.chunk = chunk;
     plan.any_multi = any_multi;
     plan.any_empty = any_empty;
+    plan.max_len = *std::max_element(seq_lens_host, seq_lens_host + B);
     float *part = any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
-    launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, stream);
+    launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, nullptr, nullptr, stream);
     return "";
 }
 
@@ -96,15 +98,16 @@ std::string attn_decode_compact(const __half *q, const __half *k, const __half *
     kv.head_stride = static_cast<int64_t>(S) * D;
     AttnPlan plan;
     plan.uniform_len = S;
-    plan.chunk = choose_chunk(nullptr, B, H, S);
+    plan.chunk = choose_chunk(nullptr, B, H, S, D);
     plan.nchunk = (S + plan.chunk - 1) / plan.chunk;
     plan.n_work = B * plan.nchunk;
     plan.any_multi = plan.nchunk > 1;
+    plan.max_len = S;
     DeviceContext &ctx = DeviceContext::get(current_device());
     std::lock_guard<std::mutex> lk(ctx.mu);
     ctx.claim(stream);
     float *part = plan.any_multi ? ctx.ws.get(attn_workspace_floats(plan.n_work, H, D)) : nullptr;
-    launch_attn_decode(q, kv, plan, B, H, H, D, scale, out, part, stream);
+    launch_attn_decode(q, kv, plan, B, H, H, D, scale, out, part, nullptr, nullptr, stream);
     return "";
 }
 
@@ -120,7 +123,7 @@ void attention_decode(const half *query, const half *k_cache, const half *v_cach
     try {
         err = detail::attn_decode_compact(query, k_cache, v_cache, output, scale, batch_size,
                                           num_heads, seq_len, head_dim, stream);
-    } catch (const HipException &e) {
+    } catch (const std::exception &e) {
         err = e.what();
     }
     if (!err.empty()) TLLM_ERROR("%s", err.c_str());

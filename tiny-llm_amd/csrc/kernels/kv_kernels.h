@@ -44,12 +44,16 @@ struct AttnPlan {
     int            chunk = 512;  // tokens per work item, multiple of 64, <= kChunkMax
     bool           any_multi = false;  // some entry spans more than one chunk
     bool           any_empty = false;  // some entry attends to zero tokens
+    int            max_len = 0;        // longest attended length (offset-width check)
 };
 
 constexpr int kChunkMax = 512;
 
-// Work-list chunk size for a set of lengths (tokens per work item).
-int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len);
+// Work-list chunk size for a set of lengths (tokens per work item).  The
+// chunk is a multiple of 64 and of the smallest chunk the head size allows
+// (each wave's quarter must hold whole P.V pair blocks: 128 tokens for
+// head_dim 32, 64 otherwise).
+int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim);
 
 // Partials workspace (floats) needed by launch_attn_decode for n_work items.
 size_t attn_workspace_floats(int n_work, int Hq, int D);
@@ -58,8 +62,13 @@ size_t attn_workspace_floats(int n_work, int Hq, int D);
 bool attn_shape_supported(int D, int G);
 
 // q, out: [B][Hq][D]; part: workspace of attn_workspace_floats() floats.
+// new_k/new_v ([B][Hkv][D], or null): append that token at position
+// seq_lens[b]-1 before attending (the decode branch of a transformer layer).
+// Throws HipException on launch failure, std::invalid_argument when a token
+// offset of a non-paged view does not fit in 32 bits.
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
-                        int Hkv, int D, float scale, __half *out, float *part, hipStream_t stream);
+                        int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
+                        const __half *new_v, hipStream_t stream);
 
 // One token row ([Hkv][D] contiguous: tok_stride == Hkv*D, head_stride == D)
 // per (entry i, layer l) for n entries and num_layers layers.

@@ -401,7 +401,7 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
         }
     }
     // Split-K plan: work items (entry, chunk) in entry order.
-    chunk_ = detail::choose_chunk(lens_.data(), n, cfg.num_heads, 0);
+    chunk_ = detail::choose_chunk(lens_.data(), n, cfg.num_heads, 0, cfg.head_dim);
     std::vector<int32_t> part_base(static_cast<size_t>(n) + 1, 0);
     any_multi_ = false;
     any_empty_ = false;
@@ -469,6 +469,12 @@ Result<void> DecodeBatch::append(int layer_begin, int num_layers, const half *ne
 
 Result<void> DecodeBatch::attention(int layer_idx, const half *q, half *out, float scale,
                                     hipStream_t stream) {
+    return run_attention(layer_idx, q, nullptr, nullptr, out, scale, stream);
+}
+
+Result<void> DecodeBatch::run_attention(int layer_idx, const half *q, const half *new_k,
+                                        const half *new_v, half *out, float scale,
+                                        hipStream_t stream) {
     const KVCacheConfig &cfg = mgr_.getConfig();
     if (q == nullptr || out == nullptr) return Result<void>::err("DecodeBatch: q/out is null");
     if (layer_idx < 0 || layer_idx >= cfg.num_layers)
@@ -482,19 +488,24 @@ Result<void> DecodeBatch::attention(int layer_idx, const half *q, half *out, flo
     plan.chunk = chunk_;
     plan.any_multi = any_multi_;
     plan.any_empty = any_empty_;
+    plan.max_len = cfg.max_seq_len;
     float *part = nullptr;
     if (any_multi_)
         part = work_->get(detail::attn_workspace_floats(n_work_, num_q_heads_, cfg.head_dim));
     detail::launch_attn_decode(q, mgr_.layerView(layer_idx, d_slot_), plan, n_, num_q_heads_,
-                               cfg.num_heads, cfg.head_dim, scale, out, part, stream);
+                               cfg.num_heads, cfg.head_dim, scale, out, part, new_k, new_v, stream);
     return Result<void>::ok();
 }
 
+// Append and attention in one launch: the workgroup that owns the last chunk
+// of each (entry, kv head) writes the new token, then attends over it.
 Result<void> DecodeBatch::decode(int layer_idx, const half *q, const half *new_k,
                                  const half *new_v, half *out, float scale, hipStream_t stream) {
-    auto r = append(layer_idx, 1, new_k, new_v, stream);
-    if (r.isErr()) return r;
-    return attention(layer_idx, q, out, scale, stream);
+    if (!appendable_)
+        return Result<void>::err("DecodeBatch: append needs a batch made by prepare()");
+    if (new_k == nullptr) return Result<void>::err("new_k is null");
+    if (new_v == nullptr) return Result<void>::err("new_v is null");
+    return run_attention(layer_idx, q, new_k, new_v, out, scale, stream);
 }
 
 Result<void> DecodeBatch::gather(int layer_idx, half *k_out, half *v_out, int s_max,

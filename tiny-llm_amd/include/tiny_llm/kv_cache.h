@@ -132,6 +132,8 @@ class DecodeBatch {
     DecodeBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads);
     Result<void> upload(const int *seq_ids, const int *attended, int n, bool appendable,
                         hipStream_t stream);
+    Result<void> run_attention(int layer_idx, const half *q, const half *new_k, const half *new_v,
+                               half *out, float scale, hipStream_t stream);
 
     KVCacheManager &mgr_;
     int             max_seqs_;
