@@ -574,69 +574,93 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
 }
 
 struct MergeArgs {
-    const float *part_o;
-    const float *part_ml;
-    __half      *out;
-    AttnPlan     plan;
-    int          Hq;
-    int          D;
+    const float   *part_o;  // [n_work][Hq][D]
+    const float   *part_ml; // [n_work][Hq][2]
+    __half        *out;
+    const int32_t *part_base;
+    int            nchunk;
+    int            Hq;
+    int            Hkv;
 };
 
-// One wave per (entry b, query head h): log-sum-exp merge of the chunks.
-// Lane c holds chunk c's (m, l); the chunk weights are broadcast from LDS so
-// the o loads of consecutive chunks are independent.
-__global__ __launch_bounds__(64) void attn_merge_kernel(MergeArgs a) {
-    __shared__ float s_w[64];
-    const int        b = blockIdx.x;
-    const int        h = blockIdx.y;
-    const int        lane = threadIdx.x;
-    const AttnPlan  &pl = a.plan;
-    const int        nch = pl.part_base ? pl.part_base[b + 1] - pl.part_base[b] : pl.nchunk;
-    __half          *dst = a.out + ((int64_t)b * a.Hq + h) * a.D;
+constexpr int kMergeMaxChunks = 64;
+
+// One workgroup per (entry b, kv head g): log-sum-exp merge of the chunk
+// partials of the G query heads,
+//   m* = max m_c, l = sum l_c 2^(m_c-m*), o = sum o_c 2^(m_c-m*) / (l+1e-6).
+// The chunk weights go through LDS; every thread then issues the o loads of
+// all chunks back to back.  Entries with no tokens get a zero row.
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
+    __shared__ float s_w[kMergeMaxChunks][G];
+    __shared__ float s_m[G], s_l[G];
+    const int        b = blockIdx.x / a.Hkv;
+    const int        g = blockIdx.x - b * a.Hkv;
+    const int        nch = a.part_base ? a.part_base[b + 1] - a.part_base[b] : a.nchunk;
+    __half          *dst = a.out + ((int64_t)b * a.Hq + (int64_t)g * G) * D;
     if (nch == 1) return; // written by attn_chunk_kernel
-    if (nch == 0) {       // empty sequence: zero row
-        for (int d = lane; d < a.D; d += 64) dst[d] = __float2half(0.0f);
+    if (nch == 0) {
+        for (int i = threadIdx.x; i < G * D; i += 256) dst[i] = __float2half(0.0f);
         return;
     }
-    const int     w0 = pl.part_base ? pl.part_base[b] : b * pl.nchunk;
-    const int64_t rs = (int64_t)a.Hq; // rows between consecutive chunks
-    const float  *ml = a.part_ml + ((int64_t)w0 * a.Hq + h) * 2;
-    const float  *po = a.part_o + ((int64_t)w0 * a.Hq + h) * a.D;
-
-    float mx = -INFINITY;
-    for (int c = lane; c < nch; c += 64) mx = fmaxf(mx, ml[c * rs * 2]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-
-    constexpr int kMaxPer = 4; // D <= 256
-    float         o[kMaxPer] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float         l = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += 64) {
-        const int   c = c0 + lane;
-        const float wgt = c < nch ? __builtin_amdgcn_exp2f(ml[c * rs * 2] - mx) : 0.0f;
-        l += c < nch ? ml[c * rs * 2 + 1] * wgt : 0.0f;
-        __syncthreads();
-        s_w[lane] = wgt;
-        __syncthreads();
-        const int cn = min(64, nch - c0);
-#pragma unroll 8
-        for (int cc = 0; cc < cn; ++cc) {
-            const float  w = s_w[cc];
-            const float *src = po + (int64_t)(c0 + cc) * rs * a.D;
-#pragma unroll
-            for (int e = 0; e < kMaxPer; ++e) {
-                const int d = lane + 64 * e;
-                if (d < a.D) o[e] = fmaf(w, src[d], o[e]);
-            }
+    const int w0 = a.part_base ? a.part_base[b] : b * a.nchunk;
+    for (int c0 = 0; c0 < nch; c0 += kMergeMaxChunks) {
+        const int cn = min(kMergeMaxChunks, nch - c0);
+        for (int i = threadIdx.x; i < cn * G; i += 256) {
+            const int c = i / G, h = i - c * G;
+            s_w[c][h] = a.part_ml[((int64_t)(w0 + c0 + c) * a.Hq + (int64_t)g * G + h) * 2];
         }
+        __syncthreads();
+        if (threadIdx.x < G) { // running max and sum of head threadIdx.x
+            const int h = threadIdx.x;
+            float     mx = c0 ? s_m[h] : -INFINITY, mnew = mx;
+            for (int c = 0; c < cn; ++c) mnew = fmaxf(mnew, s_w[c][h]);
+            float l = c0 ? s_l[h] * __builtin_amdgcn_exp2f(mx - mnew) : 0.0f;
+            for (int c = 0; c < cn; ++c) {
+                const float wgt = __builtin_amdgcn_exp2f(s_w[c][h] - mnew);
+                l = fmaf(wgt, a.part_ml[((int64_t)(w0 + c0 + c) * a.Hq + (int64_t)g * G + h) * 2 + 1], l);
+                s_w[c][h] = wgt;
+            }
+            s_l[h] = l;
+            s_m[h] = mnew;
+        }
+        __syncthreads();
+        if (c0 == 0 && nch <= kMergeMaxChunks) {
+            for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+                const int     h = idx / D;
+                const float  *po = a.part_o + ((int64_t)w0 * a.Hq + (int64_t)g * G) * D + idx;
+                const int64_t rs = (int64_t)a.Hq * D;
+                float         o = 0.0f;
+#pragma unroll 16
+                for (int c = 0; c < cn; ++c) o = fmaf(s_w[c][h], po[c * rs], o);
+                dst[idx] = __float2half(o * (1.0f / (s_l[h] + 1e-6f)));
+            }
+            return;
+        }
+        __syncthreads();
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
-    const float inv = 1.0f / (l + 1e-6f);
-#pragma unroll
-    for (int e = 0; e < kMaxPer; ++e) {
-        const int d = lane + 64 * e;
-        if (d < a.D) dst[d] = __float2half(o[e] * inv);
+    // More than kMergeMaxChunks chunks: weights relative to the final max.
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        const int     h = idx / D;
+        const float  *ml = a.part_ml + ((int64_t)w0 * a.Hq + (int64_t)g * G + h) * 2;
+        const float  *po = a.part_o + ((int64_t)w0 * a.Hq + (int64_t)g * G) * D + idx;
+        const int64_t rs = (int64_t)a.Hq;
+        float         o = 0.0f;
+        for (int c = 0; c < nch; ++c)
+            o = fmaf(__builtin_amdgcn_exp2f(ml[c * rs * 2] - s_m[h]), po[c * rs * D], o);
+        dst[idx] = __float2half(o * (1.0f / (s_l[h] + 1e-6f)));
+    }
+}
+
+template <int D>
+void launch_merge_g(const MergeArgs &m, int B, int Hkv, int G, hipStream_t stream) {
+    const dim3 grid((unsigned)(B * Hkv));
+    switch (G) {
+    case 1: hipLaunchKernelGGL((attn_merge_kernel<D, 1>), grid, dim3(256), 0, stream, m); break;
+    case 2: hipLaunchKernelGGL((attn_merge_kernel<D, 2>), grid, dim3(256), 0, stream, m); break;
+    case 4: hipLaunchKernelGGL((attn_merge_kernel<D, 4>), grid, dim3(256), 0, stream, m); break;
+    case 8: hipLaunchKernelGGL((attn_merge_kernel<D, 8>), grid, dim3(256), 0, stream, m); break;
+    default: break;
     }
 }
 
@@ -719,6 +743,8 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     args.part_ml = part ? part + (size_t)plan.n_work * Hq * D : nullptr;
     args.new_k = new_k;
     args.new_v = new_v;
+    if (plan.any_multi && !part)
+        throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
     args.kv = kv;
     args.plan = plan;
     args.Hq = Hq;
@@ -749,11 +775,18 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         m.part_o = args.part_o;
         m.part_ml = args.part_ml;
         m.out = out;
-        m.plan = plan;
+        m.part_base = plan.part_base;
+        m.nchunk = plan.nchunk;
         m.Hq = Hq;
-        m.D = D;
+        m.Hkv = Hkv;
         profile_begin(KernelId::AttnMerge, stream);
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)B, (unsigned)Hq), dim3(64), 0, stream, m);
+        switch (D) {
+        case 32: launch_merge_g<32>(m, B, Hkv, G, stream); break;
+        case 64: launch_merge_g<64>(m, B, Hkv, G, stream); break;
+        case 128: launch_merge_g<128>(m, B, Hkv, G, stream); break;
+        case 256: launch_merge_g<256>(m, B, Hkv, G, stream); break;
+        default: break;
+        }
         HIP_CHECK(hipGetLastError());
         profile_end(KernelId::AttnMerge, stream);
     }

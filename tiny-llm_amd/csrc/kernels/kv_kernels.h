@@ -61,7 +61,8 @@ size_t attn_workspace_floats(int n_work, int Hq, int D);
 // True when (D, Hq/Hkv) has a kernel instantiation.
 bool attn_shape_supported(int D, int G);
 
-// q, out: [B][Hq][D]; part: workspace of attn_workspace_floats() floats.
+// q, out: [B][Hq][D]; part: workspace of attn_workspace_floats() floats
+// (needed only when plan.any_multi).
 // new_k/new_v ([B][Hkv][D], or null): append that token at position
 // seq_lens[b]-1 before attending (the decode branch of a transformer layer).
 // Throws HipException on launch failure, std::invalid_argument when a token
