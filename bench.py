@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU work of the cpu_baseline sample")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="only run one device-to-device copy of this many MiB (HBM counter "
+                         "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
@@ -131,6 +134,15 @@ def main():
         sys.exit(2)
     import numpy as np
     import torch  # HIP runtime first: one runtime in the process
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": n}))
+        return
     import tinyllm_kv as tl
     import workloads
 

@@ -186,6 +186,14 @@ int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_l
 void tl_attention_decode(const void *q, const void *k, const void *v, void *out, float scale,
                          int batch, int num_heads, int seq_len, int head_dim, void *stream);
 
+/* Score (q.K^T) path of the decode attention kernels, process-wide:
+ * 0 = VALU v_dot2 over the loaded K rows, 1 = MFMA v_mfma_f32_16x16x32_f16
+ * over an LDS-transposed K tile.  Both give results within the 1e-3 gate of
+ * the same oracle.  Initial value from the environment variable TL_ATTN_QK
+ * ("valu" / "mfma"), else 0.  No reference counterpart (tuning knob). */
+int tl_attn_set_score_path(int path);
+int tl_attn_get_score_path(void);
+
 /* ------------------------------------------------------------------------
  * Kernel timing (the reference has only an unused CudaEvent wrapper,
  * include/tiny_llm/cuda_streams.h:67-99).  When enabled, every launch of the

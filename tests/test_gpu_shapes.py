@@ -1,0 +1,81 @@
+"""GPU: every instantiated (head_dim, group) shape, both score paths (VALU and
+MFMA), contiguous and paged cache layouts, ragged lengths that span one and
+several split-K chunks -- one decode step (append + attention) each, against
+the oracle (attention <= 1e-3 normwise, cache bytes bit-exact)."""
+import numpy as np
+import pytest
+
+from devutil import empty_dev, read_dev, rel_err, stream, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+LENS = [1, 17, 67, 300, 700, 1100]
+
+
+@pytest.fixture
+def score_path(tl):
+    before = tl.get_score_path()
+    yield tl.set_score_path
+    tl.set_score_path(before)
+
+
+def f16bits(rng, shape):
+    return rng.standard_normal(shape).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("chunk", ["auto", "512"])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("path", [0, 1])
+def test_decode_step_all_shapes(tl, orc, score_path, monkeypatch, path, D, G, paged, chunk):
+    """chunk=512 forces full 512-token work items (the full-wave fast path);
+    "auto" lets the planner shrink chunks for this small batch."""
+    score_path(path)
+    if chunk != "auto":
+        monkeypatch.setenv("TL_ATTN_CHUNK", chunk)
+    rng = np.random.default_rng(path * 1000 + D * 10 + G + (500 if paged else 0))
+    Hkv, M = 2, 1152
+    slots = len(LENS) + 1
+    g = tl.KVCacheManager(1, Hkv, D, M, slots)
+    o = orc.KVCacheOracle(1, Hkv, D, M, slots)
+    if paged:
+        perm = rng.permutation(slots * (M // 16)).astype(np.int32)
+        assert g.setBlockMap(16, perm) is None
+    ids, keep = [], []
+    for S in LENS:
+        sid, _ = g.allocateSequence(M)
+        o.allocate(M)
+        k, v = f16bits(rng, S * Hkv * D), f16bits(rng, S * Hkv * D)
+        dk, dv = to_dev(k), to_dev(v)
+        keep += [dk, dv]
+        assert g.appendKV(sid, 0, dk.data_ptr(), dv.data_ptr(), S, stream()) is None
+        o.append(sid, 0, k, v, S)
+        g.advanceSeqLen(sid, S)
+        o.advance(sid, S)
+        ids.append(sid)
+    Hq = Hkv * G
+    B = len(ids)
+    batch = tl.DecodeBatch(g, B, Hq)
+    batch.prepare(ids, stream())
+    q = f16bits(rng, (B, Hq, D))
+    nk, nv = f16bits(rng, (B, Hkv * D)), f16bits(rng, (B, Hkv * D))
+    dq, dnk, dnv = to_dev(q), to_dev(nk), to_dev(nv)
+    out = empty_dev((B, Hq, D))
+    scale = 1.0 / np.sqrt(D)
+    batch.decode(0, dq.data_ptr(), dnk.data_ptr(), dnv.data_ptr(), out.data_ptr(), scale, stream())
+    for i, sid in enumerate(ids):
+        o.append(sid, 0, nk[i], nv[i], 1)
+    if not paged:
+        assert np.array_equal(read_dev(g.pool(), o.pool().size), o.pool())
+    lens = np.array([S + 1 for S in LENS])
+    view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(s) for s in ids])
+    ref32, _ = orc.attn_decode_gqa(q, view, lens, Hq, Hkv, D, scale, nthreads=8)
+    got = to_host(out).view(np.float16).astype(np.float32)
+    errs = [rel_err(got[i], ref32[i]) for i in range(B)]
+    assert max(errs) <= 1e-3, errs
+    if paged:  # the appended token landed where the block map says
+        smax = int(lens.max())
+        gk = empty_dev((B, Hkv, smax, D))
+        batch.gather(0, gk.data_ptr(), 0, smax, stream())
+        assert np.array_equal(to_host(gk), orc.gather(view, 0, lens, Hkv, D, smax))

@@ -266,6 +266,14 @@ void tl_attention_decode(const void *q, const void *k, const void *v, void *out,
     });
 }
 
+int tl_attn_set_score_path(int path) {
+    if (path != 0 && path != 1) return fail(TL_ERR_INVALID, "tl_attn_set_score_path: path must be 0 or 1");
+    tiny_llm::detail::set_score_path(path);
+    return TL_OK;
+}
+
+int tl_attn_get_score_path(void) { return tiny_llm::detail::score_path(); }
+
 void tl_profile_enable(int on) { tiny_llm::detail::profile_set(on != 0); }
 void tl_profile_reset(void) { tiny_llm::detail::profile_reset(); }
 

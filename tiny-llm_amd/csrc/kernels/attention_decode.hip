@@ -7,39 +7,47 @@
 // 11-112: scores, max, expf, 1/(sum+1e-6f), P.V, RNE fp16 output), extended to
 // GQA over the token-major cache of kv_cache.cpp:226-233.
 //
-// Work decomposition.  One workgroup (4 wave64) per (entry b, kv head g,
-// chunk of <= 512 tokens); each wave owns a contiguous quarter of the chunk
-// and runs its own two-pass softmax over it, so waves never wait for each
-// other until the final combine.  The G query heads of the group share every
-// K/V byte: K and V rows are loaded once from HBM into VGPRs and used for all
-// G heads.
-//   phase 1  scores.  Default: MFMA v_mfma_f32_16x16x32_f16 with q as the A
-//            operand (16 rows = query heads, G of them non-zero) and 16 cached
-//            K rows as B (each lane loads 16 contiguous bytes of one token
-//            row per k-step); the 16x16 fp32 result holds 16 tokens x G heads
-//            with no cross-lane reduction.  Alternative (TL_ATTN_QK=valu):
-//            v_dot2_f32_f16 over 8 lanes per token + DPP reduction.
+// Work decomposition.  One workgroup of 8 wave64 per work item (entry b, kv
+// head g, chunk of the sequence); the planner sizes chunks so that work items
+// roughly match the resident workgroup slots of the device, which for long
+// sequences usually means one chunk per sequence and no split-K partials at
+// all (partials are HBM writes interleaved with the read stream, which costs
+// far more than their byte count).  Inside a chunk the waves take interleaved
+// 64-token tiles (wave w: tiles w, w+8, ...) and keep a running softmax
+// (max m, sum l, o[G][D]) in registers, rescaling by 2^(m_old - m_new) from
+// tile to tile.  The G query heads of the group share every K/V byte: each
+// K/V row is loaded once into VGPRs and used for all G heads.
+//
+// Per tile:
+//   loads    K and V rows are read with LPR = D/8 lanes per token row, 16
+//            contiguous bytes per lane, TPI = 64/LPR rows per instruction,
+//            non-temporal (read once).  Batches are double-buffered: the next
+//            batch (and, at phase ends, the first batch of the next phase or
+//            tile) is in flight while the current one is consumed.
+//   scores   VALU path: v_dot2_f32_f16 of the lane's 8 dims with the G heads,
+//            DPP sum over the row's LPR lanes; lane p keeps heads h%LPR == p.
+//            MFMA path: the K rows of 16 tokens go through a padded LDS tile
+//            and are read back in the B layout of v_mfma_f32_16x16x32_f16
+//            with q as the A operand (G of its 16 rows non-zero).
 //            Scores are scaled by scale*log2(e) so exp(s - m) = exp2(s' - m')
 //            (v_exp_f32; the change of base, no CUDA math routine).
-//   softmax  per-wave max over its tokens (DPP row rotations), p = exp2(s-m)
-//            rounded to fp16 and stored in LDS pair-interleaved:
-//            (p[h][t], p[h][t+TPI]) as one half2 per head; l = sum of the
+//   softmax  tile max per head, new running max, alpha = 2^(m_old - m_new);
+//            p = exp2(s - m_new) rounded to fp16 into LDS, pair-interleaved:
+//            (p[h][t], p[h][t+TPI]) as one half2 per head; l accumulates the
 //            rounded p, so the normaliser matches the weights used.
-//   phase 2  P.V with v_dot2_f32_f16 on token pairs: a lane holds 8 dims of
-//            tokens t and t+TPI (two 16-byte loads), v_perm_b32 interleaves
-//            them into half2 (v[t][d], v[t+TPI][d]), one dot2 per (head, dim)
-//            consumes two tokens.
-//   combine  waves merged in LDS with 2^(m_w - m) weights; an entry whose
-//            sequence fits in one chunk is normalised and written as fp16,
-//            otherwise (m, l, o[D]) partials go to the workspace and
-//            attn_merge_kernel combines the chunks.
-//   append   (decode calls) the workgroup holding the last chunk of entry b
-//            first copies the new token's K/V row of head g into the cache at
-//            position S_b - 1 -- the bytes of appendKV(n=1) -- then reads it
-//            like any other token.
+//   P.V      v_dot2_f32_f16 on token pairs: a lane holds 8 dims of tokens t
+//            and t+TPI, v_perm_b32 interleaves them into half2
+//            (v[t][d], v[t+TPI][d]); one dot2 per (head, dim) takes two tokens.
+// End: per-wave (m, l, o) combined across the 8 waves in LDS; a work item that
+// covers its whole sequence is normalised and written as fp16, otherwise
+// (m, l, o[D]) partials go to the workspace and attn_merge_kernel combines
+// the chunks: m* = max m_c, l = sum l_c 2^(m_c-m*), o = sum o_c 2^(m_c-m*)/(l+1e-6).
+// Append (decode calls): the workgroup holding the last chunk of entry b first
+// copies the new token's K/V row of head g into the cache at position S_b - 1
+// -- the bytes of appendKV(n=1) -- then reads it like any other token.
 //
-// Every global load uses a token index clamped into [0, n) of its chunk, so
-// no load leaves the attended range; masked tokens get p = 0.
+// Every global load uses a token index clamped into its tile's valid range,
+// so no load leaves the attended range; masked tokens get p = 0.
 #include "kv_kernels.h"
 
 #include "tiny_llm/hip_utils.h"
@@ -47,23 +55,43 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
+#include <type_traits>
 
 namespace tiny_llm {
 namespace detail {
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int kTokPerWaveMax = kChunkMax / kWaves; // 128
+constexpr int kNW = 8;                // waves per workgroup
+constexpr int kThreads = kNW * 64;
+constexpr int kTile = 64;             // tokens per wave tile
+constexpr int kQuantum = kNW * kTile; // chunk lengths are multiples of this
+// Resident workgroups per CU the planner assumes; the kernel asks the
+// register allocator for 2 * kSlotsPerCU waves per SIMD to make it true.
+#ifndef TL_ATTN_SLOTS
+#define TL_ATTN_SLOTS 1
+#endif
+constexpr int kSlotsPerCU = TL_ATTN_SLOTS;
+
+// Tuning (compile-time): K load steps per batch, V pair blocks per batch.
+#ifndef TL_ATTN_KB
+#define TL_ATTN_KB 2
+#endif
+#ifndef TL_ATTN_VB
+#define TL_ATTN_VB 1
+#endif
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
     const __half *q;
@@ -107,11 +135,11 @@ struct RowAddr {
             vbase = reinterpret_cast<const char *>(v.v_base) + head + (int64_t)row * blk_bytes;
         }
     }
-    // Base of the block holding token t0 (t0 wave-uniform); tokens of one
-    // 16-aligned group share it.
-    __device__ __forceinline__ int64_t block_off(int t0) const {
+    // Base of the block holding token t (t wave-uniform); the <= 16 tokens of
+    // one aligned load step share it (blocks hold >= 16 tokens).
+    __device__ __forceinline__ int64_t block_off(int t) const {
         if constexpr (PAGED) {
-            const int j = __builtin_amdgcn_readfirstlane(t0 >> log2_blk);
+            const int j = __builtin_amdgcn_readfirstlane(t >> log2_blk);
             return (int64_t)bt_row[j] * blk_bytes;
         } else {
             return 0;
@@ -128,9 +156,6 @@ struct RowAddr {
     }
 };
 
-__device__ __forceinline__ uint4 ld16(const char *p) { return *reinterpret_cast<const uint4 *>(p); }
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Streaming load of cache bytes that are read once per call: the
 // non-temporal hint keeps them from displacing reusable lines in L2 / MALL.
 __device__ __forceinline__ uint4 ld16nt(const char *p) {
@@ -163,252 +188,261 @@ __device__ __forceinline__ float row_sum16(float v) {
     v += dpp_f<0x121>(v);
     return v;
 }
+// Sum over the LPR lanes that hold one token row (LPR = 4, 8, 16 or 32).
+template <int LPR>
+__device__ __forceinline__ float row_reduce_sum(float v) {
+    v += dpp_f<0xB1>(v);                           // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);                           // quad_perm [2,3,0,1]
+    if constexpr (LPR >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
+    if constexpr (LPR >= 16) v += dpp_f<0x140>(v); // row_mirror
+    if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
 __device__ __forceinline__ uint16_t f2h_bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 __device__ __forceinline__ float h_bits2f(uint16_t x) { return (float)__builtin_bit_cast(_Float16, x); }
-
-// Shared memory of one workgroup.
-template <int D, int G>
-struct Smem {
-    uint16_t pp[kWaves][kTokPerWaveMax * G]; // fp16 p, pair-interleaved per wave
-    float    o[kWaves][G * D];               // per-wave P.V partial
-    float    m[kWaves][G];
-    float    l[kWaves][G];
-};
-
-// Index (in halves) of p[h][t] in the pair-interleaved layout of a wave:
-// tokens t = 2*TPI*blk + hi*TPI + q pair up as (q, hi = 0/1).
-template <int G, int TPI>
-__device__ __forceinline__ int pp_index(int t, int h) {
-    const int blk = t / (2 * TPI);
-    const int r = t - blk * 2 * TPI;
-    const int q = r % TPI;
-    const int hi = r / TPI;
-    return ((blk * TPI + q) * G + h) * 2 + hi;
+__device__ __forceinline__ float bcast(float v, int src_lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src_lane));
+}
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// ---------------------------------------------------------------- phase 1
-// Both variants leave, for the wave: pp (fp16 p), s.m[wave][h], s.l[wave][h].
+// Dynamic shared memory of one workgroup.  Per wave one region that holds,
+// in turn, the K transpose tile of the MFMA path (16 rows of D halves, padded
+// by 8 halves so that column reads of 16 rows fall in distinct bank groups),
+// the tile's fp16 p, and at the end the wave's o[G][D] for the combine.
+template <int D, int G, bool MFMA>
+struct Smem {
+    static constexpr int kKt = MFMA ? 16 * (D + 8) * 2 : 0; // bytes
+    static constexpr int kPp = kTile * G * 2;
+    static constexpr int kO = G * D * 4;
+    static constexpr int kA = kKt > kPp ? kKt : kPp;
+    static constexpr int kWave = kA > kO ? kA : kO;
+    static constexpr int kBytes = kNW * kWave + 2 * kNW * G * 4;
+    __device__ static char  *wave(char *base, int w) { return base + w * kWave; }
+    __device__ static float *m(char *base) { return reinterpret_cast<float *>(base + kNW * kWave); }
+    __device__ static float *l(char *base) { return m(base) + kNW * G; }
+};
 
-template <int D, int G, bool PAGED>
-__device__ __forceinline__ void scores_mfma(const AttnArgs &a, const RowAddr<PAGED> &ra, Smem<D, G> &s,
-                                            int b, int g, int t0, int n, int wt0, int tpw, int lane,
-                                            int wave) {
-    constexpr int KS = D / 32;         // k-steps of 32 dims
-    constexpr int TPI = 64 / (D / 8);  // phase-2 tokens per step
-    constexpr int NG = kTokPerWaveMax / 16;
-    const int r16 = lane & 15;
-    const int kq = lane >> 4;
-    // A = q: row r16 = head, k = 32*s + 8*kq .. +8
+// ------------------------------------------------------------------ scorers
+// A scorer owns the q registers and the running softmax state of the heads a
+// lane is responsible for; it turns the K batches of a tile into fp16 p in
+// LDS and hands the per-head rescale factors to the P.V stage.
+
+// VALU: lane (r = lane / LPR, p = lane % LPR); owner of heads h % LPR == p.
+template <int D, int G>
+struct ValuScorer {
+    static constexpr int LPR = D / 8;
+    static constexpr int TPI = 64 / LPR;
+    static constexpr int NSTEP = kTile / TPI;
+    static constexpr int HPL = (G + LPR - 1) / LPR;
+    uint4 qv[G];
+    float sc[HPL][NSTEP];
+    float mrun[HPL], lrun[HPL], alpha[HPL];
+    int   r, p;
+
+    __device__ __forceinline__ void init(const __half *qrow, int lane) {
+        r = lane / LPR;
+        p = lane % LPR;
+#pragma unroll
+        for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const uint4 *>(qrow + h * D + 8 * p);
+#pragma unroll
+        for (int hh = 0; hh < HPL; ++hh) {
+            mrun[hh] = -INFINITY;
+            lrun[hh] = 0.0f;
+        }
+    }
+    // Scores of load step s (tokens s*TPI + r of the tile) from the lane's row piece.
+    __device__ __forceinline__ void step(int s, uint4 k, bool valid, float scale_log2) {
+        float mine[HPL];
+#pragma unroll
+        for (int hh = 0; hh < HPL; ++hh) mine[hh] = 0.0f;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float d = fdot2(qv[h].x, k.x, 0.0f);
+            d = fdot2(qv[h].y, k.y, d);
+            d = fdot2(qv[h].z, k.z, d);
+            d = fdot2(qv[h].w, k.w, d);
+            d = row_reduce_sum<LPR>(d);
+            if (h % LPR == p) mine[h / LPR] = d;
+        }
+#pragma unroll
+        for (int hh = 0; hh < HPL; ++hh) sc[hh][s] = valid ? mine[hh] * scale_log2 : -INFINITY;
+    }
+    // After all steps: running max/sum update, p -> LDS (pair layout).
+    __device__ __forceinline__ void softmax(uint16_t *pp) {
+#pragma unroll
+        for (int hh = 0; hh < HPL; ++hh) {
+            const int h = hh * LPR + p;
+            float     m = -INFINITY;
+#pragma unroll
+            for (int s = 0; s < NSTEP; ++s) m = fmaxf(m, sc[hh][s]);
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+            const float mnew = fmaxf(mrun[hh], m);
+            alpha[hh] = mrun[hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun[hh] - mnew);
+            mrun[hh] = mnew;
+            float l = 0.0f;
+            if (h < G) {
+#pragma unroll
+                for (int s = 0; s < NSTEP; ++s) {
+                    const float    pv = sc[hh][s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[hh][s] - mnew);
+                    const uint16_t ph = f2h_bits(pv);
+                    l += h_bits2f(ph);
+                    // token s*TPI + r: pair block s/2, half s%2, q = r
+                    pp[(((s >> 1) * TPI + r) * G + h) * 2 + (s & 1)] = ph;
+                }
+            }
+            lrun[hh] = lrun[hh] * alpha[hh] + l;
+        }
+    }
+    // Rescale factor of head h, broadcast to every lane.
+    __device__ __forceinline__ float head_alpha(int h) const { return bcast(alpha[h / LPR], h % LPR); }
+    // Final (m, l) of the lane's heads into LDS.
+    __device__ __forceinline__ void finish(float *sm, float *sl) {
+#pragma unroll
+        for (int hh = 0; hh < HPL; ++hh) {
+            float l = lrun[hh];
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) l += __shfl_xor(l, off);
+            const int h = hh * LPR + p;
+            if (r == 0 && h < G) {
+                sm[h] = mrun[hh];
+                sl[h] = l;
+            }
+        }
+    }
+};
+
+// MFMA: lane (kq = lane >> 4, r16 = lane & 15); lane holds heads 4*kq + i.
+template <int D, int G>
+struct MfmaScorer {
+    static constexpr int LPR = D / 8;
+    static constexpr int TPI = 64 / LPR;
+    static constexpr int SPG = 16 / TPI; // load steps per 16-token group
+    static constexpr int NG = kTile / 16;
+    static constexpr int KS = D / 32;
+    static constexpr int KR = D + 8; // padded tile row (halves)
     f16x8 qa[KS];
-    {
-        const __half *qp = a.q + ((int64_t)b * a.Hq + (int64_t)g * G + r16) * D + 8 * kq;
+    float sc[NG][4];
+    float mrun[4], lrun[4], alpha[4];
+    int   r, p, r16, kq;
+
+    __device__ __forceinline__ void init(const __half *qrow, int lane) {
+        r = lane / LPR;
+        p = lane % LPR;
+        r16 = lane & 15;
+        kq = lane >> 4;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (r16 < G) v = *reinterpret_cast<const uint4 *>(qp + 32 * ks);
+            if (r16 < G) v = *reinterpret_cast<const uint4 *>(qrow + r16 * D + 8 * kq + 32 * ks);
             qa[ks] = __builtin_bit_cast(f16x8, v);
         }
-    }
-    f32x4 sc[NG];
 #pragma unroll
-    for (int j = 0; j < NG; ++j) sc[j] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-
-    // Groups of 16 tokens; loads of 2 groups in flight per batch.
-#pragma unroll
-    for (int j0 = 0; j0 < NG; j0 += 2) {
-        if (j0 * 16 < tpw && wt0 + j0 * 16 < n) {
-            uint4 kr[2][KS];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int gs = wt0 + (j0 + u) * 16; // group start (chunk-local)
-                const int tl = gs + r16;
-                const int tc = tl < n ? tl : n - 1;
-                const int gsc = gs < n ? gs : n - 1;
-                const char *base = ra.kbase + ra.block_off(t0 + gsc);
-                const uint32_t off = ra.in_block(t0 + tc) + 16u * kq;
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) kr[u][ks] = ld16(base + off + 64u * ks);
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                if ((j0 + u) * 16 < tpw) {
-                    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], __builtin_bit_cast(f16x8, kr[u][ks]),
-                                                                     acc, 0, 0, 0);
-                    const int tl = wt0 + (j0 + u) * 16 + r16;
-                    const bool ok = tl < n;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) sc[j0 + u][i] = ok ? acc[i] * a.scale_log2 : -INFINITY;
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            mrun[i] = -INFINITY;
+            lrun[i] = 0.0f;
         }
     }
-    // acc[i] of lane (kq, r16) = score of head 4*kq + i for token r16 of the group.
-    float mh[4], lh[4];
+    // Group j (steps j*SPG .. +SPG) of the tile: kr holds those steps' rows.
+    __device__ __forceinline__ void group(int j, const uint4 *kr, uint16_t *kt, int nt,
+                                          float scale_log2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float m = -INFINITY;
+        for (int u = 0; u < SPG; ++u)
+            *reinterpret_cast<uint4 *>(kt + (r + TPI * u) * KR + 8 * p) = kr[u];
+        wave_sync_lds();
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < NG; ++j) m = fmaxf(m, sc[j][i]);
-        mh[i] = row_max16(m);
-        lh[i] = 0.0f;
-    }
-    uint16_t *pp = s.pp[wave];
-#pragma unroll
-    for (int j = 0; j < NG; ++j) {
-        if (j * 16 < tpw) {
-            const int tw = j * 16 + r16; // wave-local token
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int h = 4 * kq + i;
-                if (h < G) {
-                    const float    p = sc[j][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[j][i] - mh[i]);
-                    const uint16_t ph = f2h_bits(p);
-                    lh[i] += h_bits2f(ph);
-                    pp[pp_index<G, TPI>(tw, h)] = ph;
-                }
-            }
+        for (int ks = 0; ks < KS; ++ks) {
+            const uint4 kb = *reinterpret_cast<const uint4 *>(kt + r16 * KR + 8 * kq + 32 * ks);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[ks], __builtin_bit_cast(f16x8, kb), acc, 0,
+                                                         0, 0);
         }
+        wave_sync_lds();
+        const bool ok = j * 16 + r16 < nt;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[j][i] = ok ? acc[i] * scale_log2 : -INFINITY;
     }
+    __device__ __forceinline__ void softmax(uint16_t *pp) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float l = row_sum16(lh[i]);
-        const int   h = 4 * kq + i;
-        if (r16 == 0 && h < G) {
-            s.m[wave][h] = mh[i];
-            s.l[wave][h] = l;
-        }
-    }
-}
-
-// Sum over the LPR lanes that hold one token row (LPR = 4, 8, 16 or 32).
-template <int LPR>
-__device__ __forceinline__ float row_reduce_sum(float v) {
-    v += dpp_f<0xB1>(v);                              // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E>(v);                              // quad_perm [2,3,0,1]
-    if constexpr (LPR >= 8) v += dpp_f<0x141>(v);     // row_half_mirror
-    if constexpr (LPR >= 16) v += dpp_f<0x140>(v);    // row_mirror
-    if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
-    return v;
-}
-
-// Phase 1 on the VALU with the load pattern of phase 2: LPR = D/8 lanes per
-// token row, 16 contiguous bytes (8 dims) per lane, TPI = 64/LPR rows per
-// load instruction, non-temporal.  Each lane dots its 8 dims with the G
-// query heads (v_dot2_f32_f16), the row's LPR lanes are summed with DPP, and
-// lane p of the row keeps the score of heads h with h % LPR == p.
-template <int D, int G, bool PAGED>
-__device__ __forceinline__ void scores_rows(const AttnArgs &a, const RowAddr<PAGED> &ra, Smem<D, G> &s,
-                                            int b, int g, int t0, int n, int wt0, int tpw, int lane,
-                                            int wave) {
-    constexpr int LPR = D / 8;
-    constexpr int TPI = 64 / LPR;
-    constexpr int NSTEP = kTokPerWaveMax / TPI;
-    constexpr int HPL = (G + LPR - 1) / LPR; // heads owned per lane
-    constexpr int SB = NSTEP < 8 ? NSTEP : 8; // steps per load batch
-    const int     r = lane / LPR;
-    const int     p = lane % LPR;
-    uint4         qv[G];
-    {
-        const __half *qb = a.q + ((int64_t)b * a.Hq + (int64_t)g * G) * D + 8 * p;
+        for (int i = 0; i < 4; ++i) {
+            const int h = 4 * kq + i;
+            float     m = -INFINITY;
 #pragma unroll
-        for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const uint4 *>(qb + h * D);
-    }
-    float sc[HPL][NSTEP];
+            for (int j = 0; j < NG; ++j) m = fmaxf(m, sc[j][i]);
+            m = row_max16(m);
+            const float mnew = fmaxf(mrun[i], m);
+            alpha[i] = mrun[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun[i] - mnew);
+            mrun[i] = mnew;
+            float l = 0.0f;
+            if (h < G) {
 #pragma unroll
-    for (int hh = 0; hh < HPL; ++hh)
-#pragma unroll
-        for (int i = 0; i < NSTEP; ++i) sc[hh][i] = -INFINITY;
-
-#pragma unroll
-    for (int s0 = 0; s0 < NSTEP; s0 += SB) {
-        if (s0 * TPI < tpw && wt0 + s0 * TPI < n) {
-            uint4 kr[SB];
-#pragma unroll
-            for (int u = 0; u < SB; ++u) {
-                const int   ss = wt0 + (s0 + u) * TPI; // step start (chunk-local)
-                const int   ssc = ss < n ? ss : n - 1;
-                const int   tl = ss + r;
-                const int   tc = tl < n ? tl : n - 1;
-                const char *base = ra.kbase + ra.block_off(t0 + ssc);
-                kr[u] = ld16nt(base + ra.in_block(t0 + tc) + 16 * p);
-            }
-#pragma unroll
-            for (int u = 0; u < SB; ++u) {
-                if ((s0 + u) * TPI < tpw) {
-                    float mine[HPL];
-#pragma unroll
-                    for (int hh = 0; hh < HPL; ++hh) mine[hh] = 0.0f;
-#pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        float d = fdot2(qv[h].x, kr[u].x, 0.0f);
-                        d = fdot2(qv[h].y, kr[u].y, d);
-                        d = fdot2(qv[h].z, kr[u].z, d);
-                        d = fdot2(qv[h].w, kr[u].w, d);
-                        d = row_reduce_sum<LPR>(d);
-                        if (h % LPR == p) mine[h / LPR] = d;
-                    }
-                    const bool ok = wt0 + (s0 + u) * TPI + r < n;
-#pragma unroll
-                    for (int hh = 0; hh < HPL; ++hh)
-                        sc[hh][s0 + u] = ok ? mine[hh] * a.scale_log2 : -INFINITY;
-                }
-            }
-        }
-    }
-    // per-head max / sum over the wave: across the rows r for a fixed p
-    uint16_t *pp = s.pp[wave];
-#pragma unroll
-    for (int hh = 0; hh < HPL; ++hh) {
-        const int h = hh * LPR + p;
-        float     m = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < NSTEP; ++i) m = fmaxf(m, sc[hh][i]);
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-        float l = 0.0f;
-        if (h < G) {
-#pragma unroll
-            for (int i = 0; i < NSTEP; ++i) {
-                if (i * TPI < tpw) {
-                    const float    pv = sc[hh][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[hh][i] - m);
+                for (int j = 0; j < NG; ++j) {
+                    const float    pv = sc[j][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[j][i] - mnew);
                     const uint16_t ph = f2h_bits(pv);
                     l += h_bits2f(ph);
-                    // token i*TPI + r: pair block i/2, half i%2, q = r
-                    pp[(((i >> 1) * TPI + r) * G + h) * 2 + (i & 1)] = ph;
+                    const int t = j * 16 + r16; // tile-local token
+                    const int blk = t / (2 * TPI), rr = t - blk * 2 * TPI;
+                    pp[((blk * TPI + rr % TPI) * G + h) * 2 + rr / TPI] = ph;
                 }
             }
-        }
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) l += __shfl_xor(l, off);
-        if (r == 0 && h < G) {
-            s.m[wave][h] = m;
-            s.l[wave][h] = l;
+            lrun[i] = lrun[i] * alpha[i] + l;
         }
     }
-}
+    __device__ __forceinline__ float head_alpha(int h) const {
+        float a = alpha[0];
+        if (h % 4 == 1) a = alpha[1];
+        if (h % 4 == 2) a = alpha[2];
+        if (h % 4 == 3) a = alpha[3];
+        return bcast(a, 16 * (h / 4));
+    }
+    __device__ __forceinline__ void finish(float *sm, float *sl) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float l = row_sum16(lrun[i]);
+            const int   h = 4 * kq + i;
+            if (r16 == 0 && h < G) {
+                sm[h] = mrun[i];
+                sl[h] = l;
+            }
+        }
+    }
+};
 
-// ---------------------------------------------------------------- kernel
+// ------------------------------------------------------------------ kernel
 template <int D, int G, bool PAGED, bool MFMA>
-__global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(2 * kSlotsPerCU))) void attn_decode_kernel(AttnArgs a) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
-    constexpr int LPT = D / 8;    // phase-2 lanes per token (8 dims each)
-    constexpr int TPI = 64 / LPT; // phase-2 tokens per wave step
-    __shared__ Smem<D, G> s;
+    using SM = Smem<D, G, MFMA>;
+    using Scorer = typename std::conditional<MFMA, MfmaScorer<D, G>, ValuScorer<D, G>>::type;
+    constexpr int  LPR = D / 8;
+    constexpr int  TPI = 64 / LPR;
+    constexpr int  NSTEP = kTile / TPI;      // K load steps per tile
+    constexpr int  NBLK = kTile / (2 * TPI); // V pair blocks per tile
+    constexpr int  SPG = MFMA ? 16 / TPI : 1; // steps consumed together
+    constexpr int  KB0 = TL_ATTN_KB < NSTEP ? TL_ATTN_KB : NSTEP;
+    constexpr int  KB = KB0 < SPG ? SPG : KB0; // steps per K batch
+    constexpr int  NKB = NSTEP / KB;
+    constexpr int  VB = TL_ATTN_VB < NBLK ? TL_ATTN_VB : NBLK; // pair blocks per V batch
+    constexpr int  NVB = NBLK / VB;
+    constexpr bool kUniformPairs = 2 * TPI <= 16; // a pair block sits in one 16-token block
+    extern __shared__ __align__(16) char smem[];
 
     const int       lane = threadIdx.x & 63;
     const int       wave = threadIdx.x >> 6;
     const AttnPlan &pl = a.plan;
-    // 1-D grid, kv head fastest: the Hkv workgroups that read the pieces of
-    // the same token rows are dispatched together (one per XCD when Hkv = 8).
-    const int       item = blockIdx.x / a.Hkv;
-    const int       g = blockIdx.x - item * a.Hkv;
-    int             b, c;
+    // 1-D grid, kv head fastest: the Hkv workgroups reading the pieces of the
+    // same token rows are dispatched together.
+    const int item = blockIdx.x / a.Hkv;
+    const int g = blockIdx.x - item * a.Hkv;
+    int       b, c;
     if (pl.work) {
         b = pl.work[2 * item];
         c = pl.work[2 * item + 1];
@@ -421,8 +455,6 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
     const int widx = pl.part_base ? pl.part_base[b] + c : item;
     const int t0 = c * pl.chunk;
     const int n = min(pl.chunk, S - t0); // >= 1 by construction of the plan
-    const int tpw = pl.chunk / kWaves;   // multiple of 16
-    const int wt0 = wave * tpw;
 
     const RowAddr<PAGED> ra(a.kv, b, g);
 
@@ -432,132 +464,187 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnArgs a) {
         constexpr int P = D / 8; // 16-byte pieces per head row
         const int     tid = threadIdx.x;
         if (tid < 2 * P) {
-            const int      which = tid / P, e = tid - which * P;
-            const __half  *src = (which ? a.new_v : a.new_k) + ((int64_t)b * a.Hkv + g) * D + e * 8;
-            const char    *base = which ? ra.vbase : ra.kbase;
-            char          *dst = const_cast<char *>(base) + ra.lane_off(S - 1) + 16 * e;
+            const int     which = tid / P, e = tid - which * P;
+            const __half *src = (which ? a.new_v : a.new_k) + ((int64_t)b * a.Hkv + g) * D + e * 8;
+            const char   *base = which ? ra.vbase : ra.kbase;
+            char         *dst = const_cast<char *>(base) + ra.lane_off(S - 1) + 16 * e;
             *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
         }
         __threadfence_block();
         __syncthreads();
     }
 
-    // ---------------- phase 1 + per-wave softmax ----------------
-    const bool active = wt0 < n; // wave has tokens
-    if (active) {
-        if constexpr (MFMA) scores_mfma<D, G, PAGED>(a, ra, s, b, g, t0, n, wt0, tpw, lane, wave);
-        else scores_rows<D, G, PAGED>(a, ra, s, b, g, t0, n, wt0, tpw, lane, wave);
-    } else if (lane < G) {
-        s.m[wave][lane] = -INFINITY;
-        s.l[wave][lane] = 0.0f;
-    }
+    char     *wbuf = SM::wave(smem, wave);
+    uint16_t *pp = reinterpret_cast<uint16_t *>(wbuf);
+    uint16_t *kt = reinterpret_cast<uint16_t *>(wbuf);
+    const int r = lane / LPR; // row (token) within a load step
+    const int p = lane % LPR; // 16-byte piece of the row
 
-    // ---------------- phase 2: P.V on token pairs ----------------
-    const int tq = lane / LPT;
-    const int dg = lane % LPT;
-    float     acc[G][8];
+    Scorer sco;
+    sco.init(a.q + ((int64_t)b * a.Hq + (int64_t)g * G) * D, lane);
+    float acc[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
-    if (active) {
-        // pp was written by other lanes of this wave.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        constexpr int NB = kTokPerWaveMax / (2 * TPI); // pair blocks per wave
-        constexpr int BB = NB < 4 ? NB : 4;            // blocks per load batch
-        const uint16_t *pp = s.pp[wave];
-        constexpr bool uniform_blk = (2 * TPI <= 16);  // a pair block sits in one 16-token block
+    const int ntiles = (n + kTile - 1) / kTile;
+    uint4     kb[2][KB];
+    uint4     va[2][VB], vb[2][VB];
+    // Tile at chunk offset ts; tokens below tend are valid.
+    auto kload = [&](int ts, int tend, int bi, uint4(&buf)[KB]) {
 #pragma unroll
-        for (int jb = 0; jb < NB; jb += BB) {
-            if (jb * 2 * TPI < tpw && wt0 + jb * 2 * TPI < n) {
-                uint4 va[BB], vb[BB];
+        for (int u = 0; u < KB; ++u) {
+            const int   ss = t0 + ts + (bi * KB + u) * TPI; // step start (global token)
+            const int   lim = t0 + tend - 1;
+            const int   ssc = ss < lim ? ss : lim;
+            const int   t = ss + r < lim ? ss + r : lim;
+            const char *base = ra.kbase + ra.block_off(ssc);
+            buf[u] = ld16nt(base + ra.in_block(t) + 16 * p);
+        }
+    };
+    auto vload = [&](int ts, int tend, int bj, uint4(&bufa)[VB], uint4(&bufb)[VB]) {
 #pragma unroll
-                for (int u = 0; u < BB; ++u) {
-                    const int bs = wt0 + (jb + u) * 2 * TPI; // block start (chunk-local)
-                    const int ta = bs + tq, tb = bs + TPI + tq;
-                    const int tca = ta < n ? ta : n - 1, tcb = tb < n ? tb : n - 1;
-                    if constexpr (uniform_blk) {
-                        const int   bsc = bs < n ? bs : n - 1;
-                        const char *base = ra.vbase + ra.block_off(t0 + bsc);
-                        va[u] = ld16nt(base + ra.in_block(t0 + tca) + 16 * dg);
-                        vb[u] = ld16nt(base + ra.in_block(t0 + tcb) + 16 * dg);
-                    } else {
-                        va[u] = ld16nt(ra.vbase + ra.lane_off(t0 + tca) + 16 * dg);
-                        vb[u] = ld16nt(ra.vbase + ra.lane_off(t0 + tcb) + 16 * dg);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < BB; ++u) {
-                    if ((jb + u) * 2 * TPI < tpw) {
-                        // p pairs of the G heads for (block jb+u, q = tq)
-                        uint32_t pw[G];
-                        const uint32_t *src = reinterpret_cast<const uint32_t *>(pp) + ((jb + u) * TPI + tq) * G;
-                        if constexpr (G >= 4) {
-#pragma unroll
-                            for (int h4 = 0; h4 < G; h4 += 4) {
-                                const uint4 v = *reinterpret_cast<const uint4 *>(src + h4);
-                                pw[h4] = v.x;
-                                pw[h4 + 1] = v.y;
-                                pw[h4 + 2] = v.z;
-                                pw[h4 + 3] = v.w;
-                            }
-                        } else if constexpr (G == 2) {
-                            const uint2 v = *reinterpret_cast<const uint2 *>(src);
-                            pw[0] = v.x;
-                            pw[1] = v.y;
-                        } else {
-                            pw[0] = src[0];
-                        }
-                        const uint32_t wa[4] = {va[u].x, va[u].y, va[u].z, va[u].w};
-                        const uint32_t wb[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w};
-                        uint32_t       vp[8]; // (v[ta][d], v[tb][d]) for the lane's 8 dims
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            vp[2 * i] = __builtin_amdgcn_perm(wb[i], wa[i], 0x05040100u);
-                            vp[2 * i + 1] = __builtin_amdgcn_perm(wb[i], wa[i], 0x07060302u);
-                        }
-#pragma unroll
-                        for (int h = 0; h < G; ++h)
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) acc[h][e] = fdot2(pw[h], vp[e], acc[h][e]);
-                    }
-                }
+        for (int u = 0; u < VB; ++u) {
+            const int bs = t0 + ts + (bj * VB + u) * 2 * TPI; // pair block start
+            const int lim = t0 + tend - 1;
+            const int ta = bs + r < lim ? bs + r : lim;
+            const int tb = bs + TPI + r < lim ? bs + TPI + r : lim;
+            if constexpr (kUniformPairs) {
+                const int   bsc = bs < lim ? bs : lim;
+                const char *base = ra.vbase + ra.block_off(bsc);
+                bufa[u] = ld16nt(base + ra.in_block(ta) + 16 * p);
+                bufb[u] = ld16nt(base + ra.in_block(tb) + 16 * p);
+            } else {
+                bufa[u] = ld16nt(ra.vbase + ra.lane_off(ta) + 16 * p);
+                bufb[u] = ld16nt(ra.vbase + ra.lane_off(tb) + 16 * p);
             }
         }
-        // reduce over the token lanes (same dg)
+    };
+
+    int ti = wave;
+    if (ti < ntiles) kload(ti * kTile, min(n, ti * kTile + kTile), 0, kb[0]);
+    for (; ti < ntiles; ti += kNW) {
+        const int ts = ti * kTile;
+        const int tend = min(n, ts + kTile);
+        const int nt = tend - ts;
+        // ---- scores
 #pragma unroll
-        for (int off = LPT; off < 64; off <<= 1)
+        for (int bi = 0; bi < NKB; ++bi) {
+            if (bi + 1 < NKB) kload(ts, tend, bi + 1, kb[(bi + 1) & 1]);
+            else vload(ts, tend, 0, va[0], vb[0]);
+            if constexpr (MFMA) {
 #pragma unroll
-            for (int h = 0; h < G; ++h)
+                for (int u = 0; u < KB; u += SPG)
+                    sco.group((bi * KB + u) / SPG, &kb[bi & 1][u], kt, nt, a.scale_log2);
+            } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
-    }
-    if (tq == 0) {
+                for (int u = 0; u < KB; ++u) {
+                    const int s = bi * KB + u;
+                    sco.step(s, kb[bi & 1][u], s * TPI + r < nt, a.scale_log2);
+                }
+            }
+            // Keep the scheduler from hoisting later batches' loads (which
+            // would hold a whole tile in VGPRs): one batch in flight.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // ---- softmax; rescale the running P.V sums
+        sco.softmax(pp);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            float *dst = &s.o[wave][h * D + dg * 8];
+            const float al = sco.head_alpha(h);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] *= al;
+        }
+        wave_sync_lds();
+        // ---- P.V on token pairs
+#pragma unroll
+        for (int bj = 0; bj < NVB; ++bj) {
+            if (bj + 1 < NVB) {
+                vload(ts, tend, bj + 1, va[(bj + 1) & 1], vb[(bj + 1) & 1]);
+            } else if (ti + kNW < ntiles) {
+                const int tn = (ti + kNW) * kTile;
+                kload(tn, min(n, tn + kTile), 0, kb[0]);
+            }
+#pragma unroll
+            for (int u = 0; u < VB; ++u) {
+                const int       blk = bj * VB + u;
+                uint32_t        pw[G];
+                const uint32_t *src = reinterpret_cast<const uint32_t *>(pp) + (blk * TPI + r) * G;
+                if constexpr (G >= 4) {
+#pragma unroll
+                    for (int h4 = 0; h4 < G; h4 += 4) {
+                        const uint4 v = *reinterpret_cast<const uint4 *>(src + h4);
+                        pw[h4] = v.x;
+                        pw[h4 + 1] = v.y;
+                        pw[h4 + 2] = v.z;
+                        pw[h4 + 3] = v.w;
+                    }
+                } else if constexpr (G == 2) {
+                    const uint2 v = *reinterpret_cast<const uint2 *>(src);
+                    pw[0] = v.x;
+                    pw[1] = v.y;
+                } else {
+                    pw[0] = src[0];
+                }
+                const uint4    xa = va[bj & 1][u], xb = vb[bj & 1][u];
+                const uint32_t wa[4] = {xa.x, xa.y, xa.z, xa.w};
+                const uint32_t wb[4] = {xb.x, xb.y, xb.z, xb.w};
+                uint32_t       vp[8]; // (v[t][d], v[t+TPI][d]) for the lane's 8 dims
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    vp[2 * i] = __builtin_amdgcn_perm(wb[i], wa[i], 0x05040100u);
+                    vp[2 * i + 1] = __builtin_amdgcn_perm(wb[i], wa[i], 0x07060302u);
+                }
+#pragma unroll
+                for (int h = 0; h < G; ++h)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[h][e] = fdot2(pw[h], vp[e], acc[h][e]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wave_sync_lds(); // pp / kt are rewritten by the next tile
+    }
+
+    // ---- per-wave results -> LDS
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+    float *sm = SM::m(smem), *sl = SM::l(smem);
+    if (wave < ntiles) {
+        sco.finish(sm + wave * G, sl + wave * G);
+    } else if (lane < G) {
+        sm[wave * G + lane] = -INFINITY;
+        sl[wave * G + lane] = 0.0f;
+    }
+    float *so = reinterpret_cast<float *>(wbuf);
+    if (r == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float *dst = so + h * D + p * 8;
             *reinterpret_cast<float4 *>(dst) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
             *reinterpret_cast<float4 *>(dst + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
         }
     }
     __syncthreads();
 
-    // ---------------- combine waves, emit ----------------
+    // ---- combine the waves, emit
     for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
         const int h = idx / D;
         const int d = idx - h * D;
         float     mh = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mh = fmaxf(mh, s.m[w][h]);
+        for (int w = 0; w < kNW; ++w) mh = fmaxf(mh, sm[w * G + h]);
         float o = 0.0f, lh = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float wgt = s.m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s.m[w][h] - mh);
-            o = fmaf(wgt, s.o[w][h * D + d], o);
-            lh = fmaf(wgt, s.l[w][h], lh);
+        for (int w = 0; w < kNW; ++w) {
+            const float mw = sm[w * G + h];
+            const float wgt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mh);
+            o = fmaf(wgt, reinterpret_cast<const float *>(SM::wave(smem, w))[idx], o);
+            lh = fmaf(wgt, sl[w * G + h], lh);
         }
         const int64_t row = (int64_t)b * a.Hq + (int64_t)g * G + h;
         if (nch == 1) {
@@ -598,7 +685,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     const int        g = blockIdx.x - b * a.Hkv;
     const int        nch = a.part_base ? a.part_base[b + 1] - a.part_base[b] : a.nchunk;
     __half          *dst = a.out + ((int64_t)b * a.Hq + (int64_t)g * G) * D;
-    if (nch == 1) return; // written by attn_chunk_kernel
+    if (nch == 1) return; // written by attn_decode_kernel
     if (nch == 0) {
         for (int i = threadIdx.x; i < G * D; i += 256) dst[i] = __float2half(0.0f);
         return;
@@ -664,40 +751,75 @@ void launch_merge_g(const MergeArgs &m, int B, int Hkv, int G, hipStream_t strea
     }
 }
 
+template <int D, int G, bool PAGED, bool MFMA>
+void launch_one(const AttnArgs &args, int n_work, int Hkv, hipStream_t stream) {
+    using SM = Smem<D, G, MFMA>;
+    auto                 *fn = attn_decode_kernel<D, G, PAGED, MFMA>;
+    static std::once_flag once;
+    std::call_once(once, [&] {
+        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, SM::kBytes));
+    });
+    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * (unsigned)Hkv), dim3(kThreads), SM::kBytes, stream,
+                       args);
+}
+
 template <int D, int G>
-void launch_chunk(const AttnArgs &args, int n_work, int Hkv, bool paged, bool mfma, hipStream_t stream) {
-    dim3 grid((unsigned)n_work * (unsigned)Hkv);
-    if (paged) {
-        if (mfma) hipLaunchKernelGGL((attn_chunk_kernel<D, G, true, true>), grid, dim3(kThreads), 0, stream, args);
-        else hipLaunchKernelGGL((attn_chunk_kernel<D, G, true, false>), grid, dim3(kThreads), 0, stream, args);
-    } else {
-        if (mfma) hipLaunchKernelGGL((attn_chunk_kernel<D, G, false, true>), grid, dim3(kThreads), 0, stream, args);
-        else hipLaunchKernelGGL((attn_chunk_kernel<D, G, false, false>), grid, dim3(kThreads), 0, stream, args);
+void launch_dg(const AttnArgs &args, int n_work, int Hkv, bool paged, bool mfma, hipStream_t stream) {
+    if constexpr (D <= 128) { // the MFMA score path exists for head_dim <= 128
+        if (mfma) {
+            if (paged) launch_one<D, G, true, true>(args, n_work, Hkv, stream);
+            else launch_one<D, G, false, true>(args, n_work, Hkv, stream);
+            return;
+        }
     }
+    if (paged) launch_one<D, G, true, false>(args, n_work, Hkv, stream);
+    else launch_one<D, G, false, false>(args, n_work, Hkv, stream);
 }
 
 template <int D>
-void launch_chunk_g(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool mfma,
-                    hipStream_t stream) {
+void launch_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool mfma,
+              hipStream_t stream) {
     switch (G) {
-    case 1: launch_chunk<D, 1>(args, n_work, Hkv, paged, mfma, stream); break;
-    case 2: launch_chunk<D, 2>(args, n_work, Hkv, paged, mfma, stream); break;
-    case 4: launch_chunk<D, 4>(args, n_work, Hkv, paged, mfma, stream); break;
-    case 8: launch_chunk<D, 8>(args, n_work, Hkv, paged, mfma, stream); break;
+    case 1: launch_dg<D, 1>(args, n_work, Hkv, paged, mfma, stream); break;
+    case 2: launch_dg<D, 2>(args, n_work, Hkv, paged, mfma, stream); break;
+    case 4: launch_dg<D, 4>(args, n_work, Hkv, paged, mfma, stream); break;
+    case 8: launch_dg<D, 8>(args, n_work, Hkv, paged, mfma, stream); break;
     default: break;
     }
 }
 
-// Score variant: VALU rows unless TL_ATTN_QK=mfma.
+// Score path: TL_ATTN_QK ("valu" / "mfma") at first use, else VALU;
+// tl_attn_set_score_path overrides it.
+std::atomic<int> g_score_path{-1};
+
 bool use_mfma_scores() {
-    static const bool mfma = [] {
+    int v = g_score_path.load(std::memory_order_relaxed);
+    if (v < 0) {
         const char *e = std::getenv("TL_ATTN_QK");
-        return e && std::strcmp(e, "mfma") == 0;
-    }();
-    return mfma;
+        v = (e && std::strcmp(e, "mfma") == 0) ? 1 : 0;
+        g_score_path.store(v);
+    }
+    return v == 1;
+}
+
+int device_cus() {
+    static std::atomic<int> cus{0};
+    int                     v = cus.load(std::memory_order_relaxed);
+    if (v == 0) {
+        int dev = 0;
+        HIP_CHECK(hipGetDevice(&dev));
+        HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+        if (v <= 0) v = 256;
+        cus.store(v);
+    }
+    return v;
 }
 
 } // namespace
+
+void set_score_path(int path) { g_score_path.store(path ? 1 : 0); }
+int  score_path() { return use_mfma_scores() ? 1 : 0; }
 
 bool attn_shape_supported(int D, int G) {
     return (D == 32 || D == 64 || D == 128 || D == 256) && (G == 1 || G == 2 || G == 4 || G == 8);
@@ -707,28 +829,35 @@ size_t attn_workspace_floats(int n_work, int Hq, int D) {
     return (size_t)n_work * (size_t)Hq * (size_t)(D + 2);
 }
 
+// Chunk length (tokens per work item), a multiple of kQuantum.  Work items
+// are sized so that they roughly match the resident workgroup slots: uniform
+// lengths get one item per slot's share of the total (usually the whole
+// sequence, so no partials), ragged lengths half of that so long sequences
+// split and the tail balances.  TL_ATTN_CHUNK overrides.
 int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim) {
-    // A wave's quarter of the chunk must hold whole pair blocks of 2*TPI
-    // tokens (TPI = 512 / head_dim) and whole 16-token score groups.
-    const int min_chunk = std::max(64, kWaves * 2 * (512 / head_dim));
+    (void)head_dim;
+    int64_t total = 0;
+    int     mx = 0, mn = INT_MAX;
+    for (int i = 0; i < (lens ? n : 0); ++i) {
+        total += lens[i];
+        mx = std::max(mx, (int)lens[i]);
+        mn = std::min(mn, (int)lens[i]);
+    }
+    if (!lens) {
+        total = (int64_t)n * uniform_len;
+        mx = mn = uniform_len;
+    }
+    const int cap = std::max(kQuantum, (mx + kQuantum - 1) / kQuantum * kQuantum);
     if (const char *env = std::getenv("TL_ATTN_CHUNK")) {
         const int c = std::atoi(env);
-        if (c >= min_chunk && c <= kChunkMax && c % min_chunk == 0) return c;
+        if (c >= kQuantum && c % kQuantum == 0) return std::min(c, cap);
     }
-    // Largest chunk that still yields >= ~8 workgroups per CU on 256 CUs.
-    constexpr long kTargetWgs = 2048;
-    int            chunk = kChunkMax;
-    while (chunk > min_chunk) {
-        long items = 0;
-        if (lens) {
-            for (int i = 0; i < n; ++i) items += (lens[i] + chunk - 1) / chunk;
-        } else {
-            items = (long)n * ((uniform_len + chunk - 1) / chunk);
-        }
-        if (items * num_kv_heads >= kTargetWgs) break;
-        chunk >>= 1;
-    }
-    return chunk;
+    const int64_t slots = (int64_t)device_cus() * kSlotsPerCU;
+    int64_t       per = (total * num_kv_heads + slots - 1) / slots;
+    const bool    uniform = mn >= mx - mx / 10;
+    if (!uniform) per /= 2;
+    const int64_t chunk = (per + kQuantum - 1) / kQuantum * kQuantum;
+    return (int)std::min<int64_t>(std::max<int64_t>(chunk, kQuantum), cap);
 }
 
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
@@ -736,6 +865,14 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
                         const __half *new_v, hipStream_t stream) {
     const int G = Hq / Hkv;
     if (plan.n_work <= 0 && !plan.any_empty) return;
+    const bool paged = kv.block_table != nullptr;
+    const bool mfma = use_mfma_scores() && D <= 128;
+    if (plan.chunk % kQuantum != 0 || plan.chunk <= 0)
+        throw std::invalid_argument("attention: chunk length must be a positive multiple of 512");
+    if (!paged && (int64_t)plan.max_len * kv.tok_stride * 2 > (int64_t)UINT32_MAX)
+        throw std::invalid_argument("attention: token offsets exceed 32 bits (max_len * row bytes)");
+    if (plan.any_multi && !part)
+        throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
     AttnArgs args;
     args.q = q;
     args.out = out;
@@ -743,27 +880,19 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     args.part_ml = part ? part + (size_t)plan.n_work * Hq * D : nullptr;
     args.new_k = new_k;
     args.new_v = new_v;
-    if (plan.any_multi && !part)
-        throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
     args.kv = kv;
     args.plan = plan;
     args.Hq = Hq;
     args.Hkv = Hkv;
     args.scale_log2 = scale * 1.4426950408889634f;
-    const bool paged = kv.block_table != nullptr;
-    const bool mfma = use_mfma_scores();
-    if (plan.chunk % std::max(64, kWaves * 2 * (512 / D)) != 0 || plan.chunk > kChunkMax)
-        throw std::invalid_argument("attention: chunk length does not fit the head size");
-    if (!paged && (int64_t)plan.max_len * kv.tok_stride * 2 > (int64_t)UINT32_MAX)
-        throw std::invalid_argument("attention: token offsets exceed 32 bits (max_len * row bytes)");
 
     if (plan.n_work > 0) {
         profile_begin(KernelId::AttnChunk, stream);
         switch (D) {
-        case 32: launch_chunk_g<32>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
-        case 64: launch_chunk_g<64>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
-        case 128: launch_chunk_g<128>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
-        case 256: launch_chunk_g<256>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
+        case 32: launch_d<32>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
+        case 64: launch_d<64>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
+        case 128: launch_d<128>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
+        case 256: launch_d<256>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
         default: break;
         }
         HIP_CHECK(hipGetLastError());

@@ -41,18 +41,14 @@ struct AttnPlan {
     int            uniform_len = 0;
     int            nchunk = 1;
     int            n_work = 0;
-    int            chunk = 512;  // tokens per work item, multiple of 64, <= kChunkMax
+    int            chunk = 512;  // tokens per work item, a positive multiple of 512
     bool           any_multi = false;  // some entry spans more than one chunk
     bool           any_empty = false;  // some entry attends to zero tokens
     int            max_len = 0;        // longest attended length (offset-width check)
 };
 
-constexpr int kChunkMax = 512;
-
-// Work-list chunk size for a set of lengths (tokens per work item).  The
-// chunk is a multiple of 64 and of the smallest chunk the head size allows
-// (each wave's quarter must hold whole P.V pair blocks: 128 tokens for
-// head_dim 32, 64 otherwise).
+// Work-list chunk length (tokens per work item, a multiple of 512) for a set
+// of attended lengths (lens, or n entries of uniform_len when lens is NULL).
 int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim);
 
 // Partials workspace (floats) needed by launch_attn_decode for n_work items.
@@ -84,6 +80,11 @@ void launch_kv_append(const KvView &view, int64_t layer_stride, const int32_t *w
 // +0.0 for lens[b] <= t < s_max.  which: 0 = K, 1 = V.
 void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int uniform_len, int n,
                       int Hkv, int D, int s_max, __half *out, hipStream_t stream);
+
+// Score path of the attention kernels: 0 = VALU dot products over the
+// loaded rows, 1 = MFMA over an LDS-transposed K tile.
+void set_score_path(int path);
+int  score_path();
 
 // Per-kernel event timing (tl_profile_*).
 enum class KernelId { AttnChunk = 0, AttnMerge = 1, KvAppend = 2, KvGather = 3, Count = 4 };

@@ -18,7 +18,9 @@ import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _REPO = os.path.dirname(_HERE)
-LIB_PATH = os.path.join(_HERE, "_build", "libtinyllm_kv.so")
+# TINYLLM_KV_LIB points at an alternative build of the same library (tuning
+# experiments); by default the in-tree build is loaded.
+LIB_PATH = os.environ.get("TINYLLM_KV_LIB") or os.path.join(_HERE, "_build", "libtinyllm_kv.so")
 HEADER_PATH = os.path.join(_REPO, "include", "tinyllm_kv.h")
 
 TL_OK = 0
@@ -99,6 +101,8 @@ def _declare(L: C.CDLL) -> None:
         "tl_kv_batch_gather": (i, [vp, i, vp, vp, i, vp]),
         "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
+        "tl_attn_set_score_path": (i, [i]),
+        "tl_attn_get_score_path": (i, []),
         "tl_profile_enable": (None, [i]),
         "tl_profile_reset": (None, []),
         "tl_profile_query": (i, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
@@ -282,6 +286,19 @@ def attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, s
     """tiny_llm::kernels::attention_decode (void; errors go to the log and
     tl_last_error)."""
     load().tl_attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, stream)
+
+
+SCORE_VALU = 0
+SCORE_MFMA = 1
+
+
+def set_score_path(path: int):
+    """0 = VALU dot products, 1 = MFMA over an LDS-transposed K tile."""
+    _check(load().tl_attn_set_score_path(path))
+
+
+def get_score_path() -> int:
+    return load().tl_attn_get_score_path()
 
 
 def profile_enable(on: bool = True):
