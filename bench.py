@@ -28,7 +28,7 @@ sys.path.insert(0, os.path.join(REPO, "tiny-llm_amd"))
 METRIC = ("decode attn+KV append µs/step and achieved HBM GB/s (% of peak), "
           "8B GQA b64 ctx8k")
 HBM_PEAK_GBPS = 8000.0
-PMC_SUMMARY = os.path.join(REPO, "profiles", "attn_chunk_cfg3_pmc.txt")
+PMC_SUMMARY = os.path.join(REPO, "profiles", "attn_decode_kernel_cfg3_pmc.txt")
 
 
 def parse():
@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU work of the cpu_baseline sample")
+    ap.add_argument("--q-heads", type=int, default=0,
+                    help="override the number of query heads (64 gives the group-8 head shape of "
+                         "the churn configuration on the same batch/context); 0 = config 3's 32")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run one device-to-device copy of this many MiB (HBM counter "
                          "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) and exit")
@@ -147,6 +150,9 @@ def main():
     import workloads
 
     cfg = workloads.config(3, steps=args.steps)
+    if args.q_heads:
+        cfg.hq = args.q_heads
+        cfg.name += f"_hq{args.q_heads}"
     B, Hq, Hkv, D, ctx0 = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, int(cfg.contexts[0])
     M = ((ctx0 + args.steps + 1 + 63) // 64) * 64
     torch.cuda.set_device(0)
@@ -225,6 +231,8 @@ def main():
     achieved = (sum(attn_bytes) / len(attn_bytes)) / (chunk_avg_ms * 1e-3) / 1e9
     traffic = read_pmc(cfg.name)
 
+    sp = tl.get_score_path()
+    score_kind = "mfma" if sp == 1 or (sp == 2 and Hq // Hkv >= 8) else "valu"
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -251,7 +259,8 @@ def main():
                        "attn_merge": round(merge_ms / max(1, merge_n) * 1e3, 2),
                        "kv_append": round(app_ms / max(1, app_n) * 1e3, 2)},
         "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
-        "roofline": {"kernel": "attn_chunk_kernel<128,4>", "bound": "hbm",
+        "roofline": {"kernel": f"attn_decode_kernel<D={D},G={Hq // Hkv},{score_kind}>",
+                     "bound": "hbm",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},
         "cpu_baseline": None,

@@ -267,7 +267,8 @@ void tl_attention_decode(const void *q, const void *k, const void *v, void *out,
 }
 
 int tl_attn_set_score_path(int path) {
-    if (path != 0 && path != 1) return fail(TL_ERR_INVALID, "tl_attn_set_score_path: path must be 0 or 1");
+    if (path < 0 || path > 2)
+        return fail(TL_ERR_INVALID, "tl_attn_set_score_path: path must be 0 (valu), 1 (mfma) or 2 (auto)");
     tiny_llm::detail::set_score_path(path);
     return TL_OK;
 }

@@ -789,18 +789,29 @@ void launch_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool
     }
 }
 
-// Score path: TL_ATTN_QK ("valu" / "mfma") at first use, else VALU;
-// tl_attn_set_score_path overrides it.
+// Score path: TL_ATTN_QK ("valu" / "mfma" / "auto") at first use, else
+// auto; tl_attn_set_score_path overrides it.  Auto takes MFMA from group 8 up:
+// measured on cfg3's batch and context, group 4 runs at the same speed on
+// both paths and group 8 is faster on MFMA (the VALU path's 8 heads x 8 dims
+// of P.V accumulators plus 8 q rows crowd the register file).
 std::atomic<int> g_score_path{-1};
 
-bool use_mfma_scores() {
+int score_path_setting() {
     int v = g_score_path.load(std::memory_order_relaxed);
     if (v < 0) {
         const char *e = std::getenv("TL_ATTN_QK");
-        v = (e && std::strcmp(e, "mfma") == 0) ? 1 : 0;
+        v = 2;
+        if (e && std::strcmp(e, "mfma") == 0) v = 1;
+        if (e && std::strcmp(e, "valu") == 0) v = 0;
         g_score_path.store(v);
     }
-    return v == 1;
+    return v;
+}
+
+bool use_mfma_scores(int D, int G) {
+    if (D > 128) return false;
+    const int v = score_path_setting();
+    return v == 1 || (v == 2 && G >= 8);
 }
 
 int device_cus() {
@@ -818,8 +829,8 @@ int device_cus() {
 
 } // namespace
 
-void set_score_path(int path) { g_score_path.store(path ? 1 : 0); }
-int  score_path() { return use_mfma_scores() ? 1 : 0; }
+void set_score_path(int path) { g_score_path.store(path); }
+int  score_path() { return score_path_setting(); }
 
 bool attn_shape_supported(int D, int G) {
     return (D == 32 || D == 64 || D == 128 || D == 256) && (G == 1 || G == 2 || G == 4 || G == 8);
@@ -866,7 +877,7 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     const int G = Hq / Hkv;
     if (plan.n_work <= 0 && !plan.any_empty) return;
     const bool paged = kv.block_table != nullptr;
-    const bool mfma = use_mfma_scores() && D <= 128;
+    const bool mfma = use_mfma_scores(D, G);
     if (plan.chunk % kQuantum != 0 || plan.chunk <= 0)
         throw std::invalid_argument("attention: chunk length must be a positive multiple of 512");
     if (!paged && (int64_t)plan.max_len * kv.tok_stride * 2 > (int64_t)UINT32_MAX)

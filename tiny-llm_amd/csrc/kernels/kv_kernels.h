@@ -82,7 +82,8 @@ void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int un
                       int Hkv, int D, int s_max, __half *out, hipStream_t stream);
 
 // Score path of the attention kernels: 0 = VALU dot products over the
-// loaded rows, 1 = MFMA over an LDS-transposed K tile.
+// loaded rows, 1 = MFMA over an LDS-transposed K tile, 2 = auto (MFMA for
+// groups of >= 8 query heads per kv head).
 void set_score_path(int path);
 int  score_path();
 

@@ -290,10 +290,12 @@ def attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, s
 
 SCORE_VALU = 0
 SCORE_MFMA = 1
+SCORE_AUTO = 2
 
 
 def set_score_path(path: int):
-    """0 = VALU dot products, 1 = MFMA over an LDS-transposed K tile."""
+    """0 = VALU dot products, 1 = MFMA over an LDS-transposed K tile,
+    2 = auto (MFMA for groups of >= 8 query heads per kv head)."""
     _check(load().tl_attn_set_score_path(path))
 
 
