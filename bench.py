@@ -1,18 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the KV-cache decode hot path on one MI355X.
 
-Headline workload: Llama-3-8B-shaped GQA decode, one
-layer, 32 query / 8 KV heads, head_dim 128, batch 64, context 8192, fp16 KV
-drawn from N(0,1).  A step = the decode branch of TransformerLayer::attention
-for the whole batch: DecodeBatch.prepare (host snapshot + one metadata
-upload), fused append of one token per sequence, split-K GQA attention over
-S = context + 1 tokens, merge, then advanceSeqLen per sequence (host).  Each
-timed step appends one token (S: 8193 -> 8192 + steps).  Warm-up steps run
-the same kernels without advancing the lengths.
+Default (the driver's line) = configuration 3: Llama-3-8B-shaped GQA decode,
+one layer, 32 query / 8 KV heads, head_dim 128, batch 64, context 8192, fp16
+KV drawn from N(0,1), 100 timed steps.  A step is the decode branch of
+TransformerLayer::attention (src/transformer.cpp:222-237) for the whole
+batch plus InferenceEngine::decodeStep's commit (inference_engine.cpp:291):
+DecodeBatch.prepare (host snapshot + one metadata upload), per layer the
+fused append of one token per sequence + split-K GQA attention over
+S = context + 1 tokens (+ merge when a sequence spans several chunks), then
+advanceSeqLen(seq, 1) for every sequence.  Each timed step appends one token
+(S: 8193 -> 8192 + steps); warm-up steps run the same kernels without
+advancing the lengths.
 
-Prints ONE JSON line.  `value` is achieved HBM throughput in GB/s computed
-from the algorithmic bytes of each step (K+V cache read of S_b tokens, Q read
-+ O write, new K/V read + append write) over the measured step time.
+--config 2 / 4 / 5 measure the other configurations of the same path
+(32-layer MHA; ragged paged batch 128; allocation churn with group 8).
+
+Prints ONE JSON line.  `value` is achieved HBM throughput in GB/s: the
+algorithmic bytes of every step (K+V cache read of S_b tokens, Q read + O
+write, new K/V read + append write, block-table reads when paged, prompt
+appends under churn) over the measured time of the timed steps.
 """
 from __future__ import annotations
 
@@ -34,15 +41,17 @@ PMC_SUMMARY = os.path.join(REPO, "profiles", "attn_decode_kernel_cfg3_pmc.txt")
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=0,
+                    help="timed steps (default: 100 for configs 2-4, 1000 for config 5)")
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5))
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU work of the cpu_baseline sample")
     ap.add_argument("--q-heads", type=int, default=0,
-                    help="override the number of query heads (64 gives the group-8 head shape of "
-                         "the churn configuration on the same batch/context); 0 = config 3's 32")
+                    help="override the number of query heads of configs 2-4 (64 on config 3 "
+                         "gives the group-8 head shape of config 5 at batch 64 / context 8192)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run one device-to-device copy of this many MiB (HBM counter "
                          "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) and exit")
@@ -55,6 +64,17 @@ def cpu_threads() -> int:
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(16, n))
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(cfg, target_s: float):
@@ -83,7 +103,7 @@ def cpu_baseline(cfg, target_s: float):
     q = rng.standard_normal((nseq, Hq, D), dtype=np.float32).astype(np.float16).view(np.uint16)
     nk = rng.standard_normal((nseq, Hkv * D), dtype=np.float32).astype(np.float16).view(np.uint16)
     steps, total_bytes, t_used = 0, 0, 0.0
-    while t_used < target_s and steps < 64:
+    while t_used < target_s and steps < 1024:
         lens = np.array([kv.seq_len(s) + 1 for s in ids])
         t0 = time.perf_counter()
         for i, sid in enumerate(ids):
@@ -102,20 +122,10 @@ def cpu_baseline(cfg, target_s: float):
                       f"{threads} OpenMP threads, cpu={_cpu_model()}"}
 
 
-def _cpu_model() -> str:
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
-
-
 def read_pmc(workload: str):
-    """HBM bytes per launch of attn_chunk from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated with a copy kernel)."""
+    """HBM bytes per launch of attn_decode_kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated with a copy
+    kernel), or None when no summary covers this workload."""
     try:
         with open(PMC_SUMMARY) as f:
             for line in f:
@@ -127,6 +137,213 @@ def read_pmc(workload: str):
     except (OSError, ValueError):
         pass
     return None
+
+
+def kernel_stats(tl):
+    out = {}
+    for k in ("attn_chunk", "attn_merge", "kv_append"):
+        ms, n = tl.profile_query(k)
+        out[k] = (ms, n)
+    return out
+
+
+def fixed_batch(args, tl, torch, workloads, np):
+    """Configurations 2-4: a fixed batch prefilled through appendKV, then K
+    decode steps over every layer."""
+    cfg = workloads.config(args.config)
+    if args.q_heads:
+        cfg.hq = args.q_heads
+        cfg.name += f"_hq{args.q_heads}"
+    K = args.steps or 100
+    B, Hq, Hkv, D, L = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, cfg.num_layers
+    ctx = cfg.contexts.astype(np.int64)
+    bt = cfg.block_tokens
+    M = int((ctx.max() + K + 1 + 63) // 64 * 64)
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    mgr = tl.KVCacheManager(L, Hkv, D, M, B)
+    if bt:  # config 4: 16-token blocks behind a seeded random permutation
+        perm = workloads.block_permutation(B * M // bt, workloads.seed(cfg.cfg, 4))
+        assert mgr.setBlockMap(bt, perm) is None
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(workloads.seed(cfg.cfg, 1))
+    ids = []
+    for b in range(B):  # prefill through appendKV, as InferenceEngine::prefill does
+        sid, err = mgr.allocateSequence(M)
+        assert err is None, err
+        c = int(ctx[b])
+        for layer in range(L):
+            k = torch.randn((c, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
+            v = torch.randn((c, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
+            assert mgr.appendKV(sid, layer, k.data_ptr(), v.data_ptr(), c, stream) is None
+        mgr.advanceSeqLen(sid, c)
+        ids.append(sid)
+    q = torch.randn((L, B, Hq, D), generator=gen, device=dev, dtype=torch.float16) * cfg.q_std
+    nk = torch.randn((L, B, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
+    nv = torch.randn((L, B, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
+    out = torch.empty((B, Hq, D), device=dev, dtype=torch.float16)
+    batch = tl.DecodeBatch(mgr, B, Hq)
+    torch.cuda.synchronize()
+
+    def step(advance):
+        batch.prepare(ids, stream)
+        for layer in range(L):
+            batch.decode(layer, q[layer].data_ptr(), nk[layer].data_ptr(), nv[layer].data_ptr(),
+                         out.data_ptr(), cfg.scale, stream)
+        if advance:
+            batch.commit(1)
+
+    for _ in range(args.warmup):
+        step(advance=False)
+    torch.cuda.synchronize()
+
+    # Timed region: K full steps, no per-kernel hooks (hipEventRecord between
+    # kernels inserts markers that widen the inter-kernel gaps).
+    lens0 = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int64)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    ev0.record()
+    for _ in range(K):
+        step(advance=True)
+    ev1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    elapsed_ms = ev0.elapsed_time(ev1)
+    info = batch.info()
+
+    # Kernel-timing pass: the same steps (lengths not advanced) with hipEvents
+    # around every launch on the launch stream.
+    tl.profile_reset()
+    tl.profile_enable(True)
+    kpass = max(10, min(K, 30))
+    for _ in range(kpass):
+        step(advance=False)
+    torch.cuda.synchronize()
+    tl.profile_enable(False)
+    ks = kernel_stats(tl)
+    tl.profile_reset()
+    lens_k = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int64)
+
+    total_bytes = sum(workloads.step_bytes(lens0 + i, Hq, Hkv, D, layers=L, paged_block=bt)
+                      for i in range(K))
+    attn_bytes = workloads.attention_bytes(lens_k, Hq, Hkv, D)
+    if bt:
+        attn_bytes += 4 * B + 4 * int(((lens_k + 1 + bt - 1) // bt).sum())
+    conf = {"workload": cfg.name, "layers": L, "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+            "head_dim": D, "context_first": int(lens0.min()), "context_max_first": int(lens0.max()),
+            "context_sum_first": int(lens0.sum()), "block_tokens": bt, "kv_std": cfg.kv_std,
+            "chunk_tokens": info["chunk_tokens"], "work_items": info["work_items"],
+            "parallelism": "single GPU"}
+    data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) (torch.randn, seeded), prefilled "
+            f"via appendKV" + (", 16-token blocks behind a seeded random permutation" if bt else ""))
+    return dict(cfg=cfg, K=K, elapsed_ms=elapsed_ms, t_wall=t_wall, total_bytes=total_bytes,
+                attn_bytes=attn_bytes, ks=ks, kpass=kpass, conf=conf, data=data,
+                kpass_desc=f"separate pass of {kpass} steps (lengths not advanced)")
+
+
+def churn(args, tl, torch, workloads, np):
+    """Configuration 5: Poisson(2) arrivals per step (prompt U{256..4096}
+    appended through appendKV), geometric(1/512) lifetimes, release on
+    finish; every step appends one token to and attends over every live
+    sequence (64 q / 8 kv heads, D=128).  Run twice with the same seed: once
+    timed without hooks, once with per-launch hipEvents."""
+    K = args.steps or 1000
+    sim_args = dict(steps=K)
+    Hq, Hkv, D, M, slots = 64, 8, 128, 5120, 1280
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(workloads.seed(5, 1))
+    src_k = torch.randn((4096, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    src_v = torch.randn((4096, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    q = torch.randn((slots, Hq, D), generator=gen, device=dev, dtype=torch.float16)
+    nk = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    nv = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    out = torch.empty((slots, Hq, D), device=dev, dtype=torch.float16)
+    scale = 1.0 / float(np.sqrt(D))
+    mgr = tl.KVCacheManager(1, Hkv, D, M, slots)
+    batch = tl.DecodeBatch(mgr, slots, Hq)
+
+    def run(profile):
+        sim = workloads.ChurnSim(hq=Hq, hkv=Hkv, head_dim=D, max_seq_len=M, slots=slots, **sim_args)
+        live = {}    # seq id -> remaining decode steps
+        length = {}  # seq id -> getSeqLen, tracked on the host side of the loop
+        nbytes, attn_nbytes, rejected, live_sum, peak = 0, 0, 0, 0, 0
+        if profile:
+            tl.profile_reset()
+            tl.profile_enable(True)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record()
+        for ev in sim.events():
+            for prompt, life in zip(ev.arrivals, ev.lifetimes):
+                sid, err = mgr.allocateSequence(M)
+                if err is not None:
+                    rejected += 1
+                    continue
+                assert mgr.appendKV(sid, 0, src_k.data_ptr(), src_v.data_ptr(), prompt, stream) is None
+                mgr.advanceSeqLen(sid, prompt)
+                nbytes += 2 * prompt * Hkv * D * 2 * 2  # read + write of K and V
+                live[sid] = max(1, life)
+                length[sid] = prompt
+            ids = list(live)
+            if ids:
+                batch.prepare(ids, stream)
+                ctx = np.fromiter((length[s] for s in ids), dtype=np.int64, count=len(ids))
+                batch.decode(0, q.data_ptr(), nk.data_ptr(), nv.data_ptr(), out.data_ptr(), scale,
+                             stream)
+                batch.commit(1)
+                sb = workloads.step_bytes(ctx, Hq, Hkv, D)
+                nbytes += sb
+                attn_nbytes += sb
+            live_sum += len(ids)
+            peak = max(peak, len(ids))
+            for s in ids:
+                live[s] -= 1
+                length[s] += 1
+                if live[s] == 0 or length[s] >= M:
+                    del live[s]
+                    del length[s]
+                    assert mgr.releaseSequence(s) is None
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = ev0.elapsed_time(ev1)
+        for s in list(live):
+            mgr.releaseSequence(s)
+        ks = None
+        if profile:
+            tl.profile_enable(False)
+            ks = kernel_stats(tl)
+            tl.profile_reset()
+        return dict(ms=ms, wall=wall, nbytes=nbytes, attn_nbytes=attn_nbytes, rejected=rejected,
+                    live_avg=live_sum / sim.steps,
+                    live_peak=peak, ks=ks)
+
+    for _ in range(1 if args.warmup else 0):  # one short untimed pass warms the kernels
+        sim_args["steps"] = min(K, 50)
+        run(profile=False)
+    sim_args["steps"] = K
+    timed = run(profile=False)
+    prof = run(profile=True)
+    ks = prof["ks"]
+    # algorithmic bytes of the average attention launch (fused append
+    # included, prompt appends excluded) over the profiled pass
+    launches = max(1, ks["attn_chunk"][1])
+    conf = {"workload": "cfg5_churn_g8", "layers": 1, "q_heads": Hq, "kv_heads": Hkv,
+            "head_dim": D, "max_seq_len": M, "slots": slots, "arrivals_per_step": 2.0,
+            "prompt": "U{256..4096}", "lifetime": "geometric(1/512)",
+            "live_avg": round(timed["live_avg"], 1), "live_peak": timed["live_peak"],
+            "rejected": timed["rejected"], "parallelism": "single GPU"}
+    return dict(cfg=None, K=K, elapsed_ms=timed["ms"], t_wall=timed["wall"],
+                total_bytes=timed["nbytes"], attn_bytes=prof["attn_nbytes"] / launches, ks=ks,
+                kpass=K, conf=conf,
+                data="synthetic: KV/Q ~ N(0,1) (torch.randn, seeded); Poisson/uniform/geometric "
+                     "events from the seeded simulator",
+                kpass_desc=f"second run of the same {K}-step event sequence")
 
 
 def main():
@@ -149,92 +366,25 @@ def main():
     import tinyllm_kv as tl
     import workloads
 
-    cfg = workloads.config(3, steps=args.steps)
-    if args.q_heads:
-        cfg.hq = args.q_heads
-        cfg.name += f"_hq{args.q_heads}"
-    B, Hq, Hkv, D, ctx0 = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, int(cfg.contexts[0])
-    M = ((ctx0 + args.steps + 1 + 63) // 64) * 64
     torch.cuda.set_device(0)
-    dev = torch.device("cuda", 0)
-    stream = torch.cuda.current_stream().cuda_stream
-
-    mgr = tl.KVCacheManager(cfg.num_layers, Hkv, D, M, B)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(workloads.seed(3, 1))
-    ids = []
-    for _ in range(B):  # prefill through appendKV, as InferenceEngine::prefill does
-        sid, err = mgr.allocateSequence(M)
-        assert err is None, err
-        k = torch.randn((ctx0, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-        v = torch.randn((ctx0, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-        assert mgr.appendKV(sid, 0, k.data_ptr(), v.data_ptr(), ctx0, stream) is None
-        mgr.advanceSeqLen(sid, ctx0)
-        ids.append(sid)
-    K = args.steps
-    nsteps_in = max(1, K)
-    q = torch.randn((nsteps_in, B, Hq, D), generator=gen, device=dev, dtype=torch.float16)
-    nk = torch.randn((nsteps_in, B, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    nv = torch.randn((nsteps_in, B, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    out = torch.empty((B, Hq, D), device=dev, dtype=torch.float16)
-    batch = tl.DecodeBatch(mgr, B, Hq)
-    torch.cuda.synchronize()
-
-    def step(i, advance):
-        batch.prepare(ids, stream)
-        j = i % nsteps_in
-        batch.decode(0, q[j].data_ptr(), nk[j].data_ptr(), nv[j].data_ptr(), out.data_ptr(),
-                     cfg.scale, stream)
-        if advance:
-            for sid in ids:
-                mgr.advanceSeqLen(sid, 1)
-
-    for i in range(args.warmup):
-        step(i, advance=False)
-    torch.cuda.synchronize()
-
-    # Timed region: K full steps, no per-kernel hooks (hipEventRecord between
-    # kernels inserts markers that widen the inter-kernel gaps).
-    ctx_per_step = []
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    ev0.record()
-    for i in range(K):
-        ctx_per_step.append(mgr.getSeqLen(ids[0]))
-        step(i, advance=True)
-    ev1.record()
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter() - t_wall
-    elapsed_ms = ev0.elapsed_time(ev1)
-
-    # Kernel-timing pass: the same steps (lengths not advanced) with hipEvents
-    # around every launch on the launch stream.
-    tl.profile_reset()
-    tl.profile_enable(True)
-    kpass = max(10, min(K, 30))
-    for i in range(kpass):
-        step(i, advance=False)
-    torch.cuda.synchronize()
-    tl.profile_enable(False)
-    chunk_ms, chunk_n = tl.profile_query("attn_chunk")
-    merge_ms, merge_n = tl.profile_query("attn_merge")
-    app_ms, app_n = tl.profile_query("kv_append")
-    tl.profile_reset()
-    ctx_kpass = mgr.getSeqLen(ids[0])
-
-    total_bytes = sum(workloads.step_bytes(np.full(B, c), Hq, Hkv, D) for c in ctx_per_step)
-    attn_bytes = [workloads.attention_bytes(np.full(B, ctx_kpass), Hq, Hkv, D)]
-    ms_per_step = elapsed_ms / K
-    value = total_bytes / (elapsed_ms * 1e-3) / 1e9
+    r = churn(args, tl, torch, workloads, np) if args.config == 5 else \
+        fixed_batch(args, tl, torch, workloads, np)
+    K, conf = r["K"], r["conf"]
+    Hq, Hkv, D = conf["q_heads"], conf["kv_heads"], conf["head_dim"]
+    ms_per_step = r["elapsed_ms"] / K
+    value = r["total_bytes"] / (r["elapsed_ms"] * 1e-3) / 1e9
+    ks = r["ks"]
+    chunk_ms, chunk_n = ks["attn_chunk"]
+    merge_ms, merge_n = ks["attn_merge"]
+    app_ms, app_n = ks["kv_append"]
     chunk_avg_ms = chunk_ms / max(1, chunk_n)
-    achieved = (sum(attn_bytes) / len(attn_bytes)) / (chunk_avg_ms * 1e-3) / 1e9
-    traffic = read_pmc(cfg.name)
-
+    achieved = r["attn_bytes"] / (chunk_avg_ms * 1e-3) / 1e9 if chunk_n else 0.0
     sp = tl.get_score_path()
     score_kind = "mfma" if sp == 1 or (sp == 2 and Hq // Hkv >= 8) else "valu"
+    metric = METRIC if args.config == 3 and not args.q_heads else \
+        f"decode attn+KV append µs/step and achieved HBM GB/s (% of peak), {conf['workload']}"
     line = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -247,26 +397,22 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic: KV and Q from N(0,1) (torch.randn, seeded), prefilled via appendKV",
-        "config": {"workload": cfg.name, "layers": 1, "batch": B, "q_heads": Hq, "kv_heads": Hkv,
-                   "head_dim": D, "context_start": ctx0, "attended_first": ctx_per_step[0] + 1,
-                   "attended_last": ctx_per_step[-1] + 1, "chunk_tokens": batch.info()["chunk_tokens"],
-                   "work_items": batch.info()["work_items"],
-                   "parallelism": "single GPU"},
-        "kernel_timing": f"hipEvent pairs around each launch, separate pass of {kpass} steps at "
-                         f"context {ctx_kpass}",
+        "data": r["data"],
+        "config": conf,
+        "kernel_timing": "hipEvent pairs around each launch on its stream, " + r["kpass_desc"],
         "kernels_us": {"attn_chunk": round(chunk_avg_ms * 1e3, 2),
                        "attn_merge": round(merge_ms / max(1, merge_n) * 1e3, 2),
                        "kv_append": round(app_ms / max(1, app_n) * 1e3, 2)},
-        "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
+        "kernel_launches": {"attn_chunk": chunk_n, "attn_merge": merge_n, "kv_append": app_n},
+        "host_wall_us_per_step": round(r["t_wall"] / K * 1e6, 2),
         "roofline": {"kernel": f"attn_decode_kernel<D={D},G={Hq // Hkv},{score_kind}>",
-                     "bound": "hbm",
-                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},
+                     "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": read_pmc(conf["workload"])},
         "cpu_baseline": None,
     }
-    if args.cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    if args.cpu_baseline and args.config == 3 and not args.q_heads:
+        line["cpu_baseline"] = cpu_baseline(r["cfg"], args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 

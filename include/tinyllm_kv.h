@@ -153,6 +153,10 @@ int tl_kv_batch_decode(tl_kv_batch *batch, int layer, const void *q, const void 
  * sequence's attended length are written as +0.0.  Either output may be NULL. */
 int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, int s_max,
                        void *stream);
+/* The commit of InferenceEngine::decodeStep (src/inference_engine.cpp:291):
+ * advanceSeqLen(seq_id, num_tokens) for every sequence of the last prepare,
+ * in batch order; stops at (and reports) the first failing sequence. */
+int tl_kv_batch_commit(tl_kv_batch *batch, int num_tokens);
 
 /* ------------------------------------------------------------------------
  * Stateless kernels over an explicit cache view (no manager).

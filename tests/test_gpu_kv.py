@@ -236,3 +236,21 @@ def test_paged_pool_append_bit_exact(tl, orc):
             write(g.slot_of(sid), layer, g.getSeqLen(sid), nk[r:r + H * D], nv[r:r + H * D], 1)
     assert np.array_equal(read_dev(g.pool(), pool.size), pool)
     assert "no live sequences" in g.setBlockMap(16, perm)
+
+
+def test_batch_commit_advances_every_sequence(tl):
+    """DecodeBatch.commit(n) == advanceSeqLen(seq, n) for every prepared
+    sequence (inference_engine.cpp:291), with the reference's clamp and
+    error on non-positive n (kv_cache.cpp:240-259)."""
+    g = tl.KVCacheManager(1, 2, 64, 64, 4)
+    ids = [g.allocateSequence(m)[0] for m in (64, 10, 64)]
+    g.advanceSeqLen(ids[1], 9)
+    batch = tl.DecodeBatch(g, 4, 2)
+    batch.prepare(ids, stream())
+    batch.commit(1)
+    assert [g.getSeqLen(s) for s in ids] == [1, 10, 1]
+    batch.prepare_lengths(ids, [1, 10, 1], stream())
+    batch.commit(5)  # clamps at each sequence's max_len
+    assert [g.getSeqLen(s) for s in ids] == [6, 10, 6]
+    with pytest.raises(tl.TinyLLMError, match="positive"):
+        batch.commit(0)

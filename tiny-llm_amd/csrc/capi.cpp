@@ -228,6 +228,11 @@ int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, 
     });
 }
 
+int tl_kv_batch_commit(tl_kv_batch *batch, int num_tokens) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_commit: null batch");
+    return guarded([&] { return status(batch->b->commit(num_tokens)); });
+}
+
 int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_lens_host, int B,
                        int Hq, int Hkv, int D, float scale, void *out, void *stream) {
     if (!kv) return fail(TL_ERR_INVALID, "tl_attn_decode_gqa: kv is null");

@@ -371,6 +371,7 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
     if (n > 0 && seq_ids == nullptr) return Result<void>::err("DecodeBatch: seq_ids is null");
     const KVCacheConfig &cfg = mgr_.getConfig();
     std::vector<char>    taken(static_cast<size_t>(cfg.max_batch_size), 0);
+    ids_.assign(seq_ids, seq_ids + n);
     lens_.assign(static_cast<size_t>(n), 0);
     wpos_.assign(static_cast<size_t>(n), 0);
     slot_.assign(static_cast<size_t>(n), 0);
@@ -439,6 +440,16 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
 
 Result<void> DecodeBatch::prepare(const int *seq_ids, int n, hipStream_t stream) {
     return upload(seq_ids, nullptr, n, true, stream);
+}
+
+// The commit of InferenceEngine::decodeStep (inference_engine.cpp:291),
+// advanceSeqLen(seq, num_tokens), for every sequence of the last prepare.
+Result<void> DecodeBatch::commit(int num_tokens) {
+    for (const int id : ids_) {
+        auto r = mgr_.advanceSeqLen(id, num_tokens);
+        if (r.isErr()) return r;
+    }
+    return Result<void>::ok();
 }
 
 Result<void> DecodeBatch::prepareLengths(const int *seq_ids, const int *attended, int n,

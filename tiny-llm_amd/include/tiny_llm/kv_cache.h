@@ -122,6 +122,8 @@ class DecodeBatch {
     Result<void> decode(int layer_idx, const half *q, const half *new_k, const half *new_v, half *out,
                         float scale, hipStream_t stream);
     Result<void> gather(int layer_idx, half *k_out, half *v_out, int s_max, hipStream_t stream);
+    // advanceSeqLen(seq, num_tokens) for every sequence of the last prepare.
+    Result<void> commit(int num_tokens);
 
     int size() const noexcept { return n_; }
     int chunkTokens() const noexcept { return chunk_; }
@@ -144,7 +146,7 @@ class DecodeBatch {
     int             n_work_ = 0;
     bool            any_multi_ = false;
     bool            any_empty_ = false;
-    std::vector<int32_t> lens_, wpos_, slot_;
+    std::vector<int32_t> ids_, lens_, wpos_, slot_;
     std::unique_ptr<detail::MetaRing>  meta_;
     std::unique_ptr<detail::Workspace> work_;
     const int32_t  *d_lens_ = nullptr, *d_wpos_ = nullptr, *d_slot_ = nullptr;

@@ -99,6 +99,7 @@ def _declare(L: C.CDLL) -> None:
         "tl_kv_batch_attention": (i, [vp, i, vp, vp, f, vp]),
         "tl_kv_batch_decode": (i, [vp, i, vp, vp, vp, vp, f, vp]),
         "tl_kv_batch_gather": (i, [vp, i, vp, vp, i, vp]),
+        "tl_kv_batch_commit": (i, [vp, i]),
         "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
         "tl_attn_set_score_path": (i, [i]),
@@ -273,6 +274,10 @@ class DecodeBatch:
 
     def gather(self, layer, k_out, v_out, s_max, stream=0):
         _check(load().tl_kv_batch_gather(self._h, layer, k_out or None, v_out or None, s_max, stream))
+
+    def commit(self, num_tokens=1):
+        """advanceSeqLen(seq, num_tokens) for every sequence of the last prepare."""
+        _check(load().tl_kv_batch_commit(self._h, num_tokens))
 
 
 def attn_decode_gqa(q, view: KVView, seq_lens, Hq, Hkv, D, scale, out, stream=0):
