@@ -23,14 +23,15 @@ def f16bits(rng, shape):
     return rng.standard_normal(shape).astype(np.float32).astype(np.float16).view(np.uint16)
 
 
-@pytest.mark.parametrize("chunk", ["auto", "512"])
+@pytest.mark.parametrize("chunk", ["auto", "256"])
 @pytest.mark.parametrize("paged", [False, True])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 @pytest.mark.parametrize("D", [32, 64, 128, 256])
 @pytest.mark.parametrize("path", [0, 1])
 def test_decode_step_all_shapes(tl, orc, score_path, monkeypatch, path, D, G, paged, chunk):
-    """chunk=512 forces full 512-token work items (the full-wave fast path);
-    "auto" lets the planner shrink chunks for this small batch."""
+    """chunk=256 forces the smallest work items (one 64-token tile per wave,
+    most entries split into several chunks and merged); "auto" lets the
+    planner choose for this small batch."""
     score_path(path)
     if chunk != "auto":
         monkeypatch.setenv("TL_ATTN_CHUNK", chunk)

@@ -42,41 +42,29 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
     for (int b = 0; b < B; ++b)
         if (seq_lens_host[b] < 0) return "tl_attn_decode_gqa: negative sequence length";
 
-    const int            chunk = choose_chunk(seq_lens_host, B, Hkv, 0, D);
-    std::vector<int32_t> part_base(static_cast<size_t>(B) + 1, 0);
-    bool                 any_multi = false, any_empty = false;
-    for (int b = 0; b < B; ++b) {
-        const int c = (seq_lens_host[b] + chunk - 1) / chunk;
-        any_multi |= c > 1;
-        any_empty |= c == 0;
-        part_base[static_cast<size_t>(b) + 1] = part_base[static_cast<size_t>(b)] + c;
-    }
-    const int     n_work = part_base[static_cast<size_t>(B)];
-    const size_t  nb = static_cast<size_t>(B);
+    WorkList wl;
+    plan_work(seq_lens_host, B, Hkv, D, wl);
+    const int      n_work = wl.n_work;
+    const size_t   nb = static_cast<size_t>(B);
     DeviceContext &ctx = DeviceContext::get(current_device());
     std::lock_guard<std::mutex> lk(ctx.mu);
     ctx.claim(stream);
     const size_t words = nb + (nb + 1) + 2 * static_cast<size_t>(n_work);
     int32_t     *h = static_cast<int32_t *>(ctx.ring.begin(words * 4));
     std::memcpy(h, seq_lens_host, nb * 4);
-    std::memcpy(h + nb, part_base.data(), (nb + 1) * 4);
-    int32_t *w = h + 2 * nb + 1;
-    for (int b = 0; b < B; ++b)
-        for (int c = part_base[static_cast<size_t>(b)]; c < part_base[static_cast<size_t>(b) + 1]; ++c) {
-            *w++ = b;
-            *w++ = c - part_base[static_cast<size_t>(b)];
-        }
+    std::memcpy(h + nb, wl.part_base.data(), (nb + 1) * 4);
+    if (n_work > 0) std::memcpy(h + 2 * nb + 1, wl.work.data(), 2 * static_cast<size_t>(n_work) * 4);
     const int32_t *d = static_cast<const int32_t *>(ctx.ring.commit(stream));
     AttnPlan       plan;
     plan.seq_lens = d;
     plan.part_base = d + nb;
     plan.work = d + 2 * nb + 1;
     plan.n_work = n_work;
-    plan.chunk = chunk;
-    plan.any_multi = any_multi;
-    plan.any_empty = any_empty;
-    plan.max_len = *std::max_element(seq_lens_host, seq_lens_host + B);
-    float *part = any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
+    plan.chunk = wl.chunk;
+    plan.any_multi = wl.any_multi;
+    plan.any_empty = wl.any_empty;
+    plan.max_len = wl.max_len;
+    float *part = wl.any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
     launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, nullptr, nullptr, stream);
     return "";
 }

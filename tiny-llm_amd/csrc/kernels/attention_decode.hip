@@ -7,13 +7,15 @@
 // 11-112: scores, max, expf, 1/(sum+1e-6f), P.V, RNE fp16 output), extended to
 // GQA over the token-major cache of kv_cache.cpp:226-233.
 //
-// Work decomposition.  One workgroup of 8 wave64 per work item (entry b, kv
-// head g, chunk of the sequence); the planner sizes chunks so that work items
-// roughly match the resident workgroup slots of the device, which for long
-// sequences usually means one chunk per sequence and no split-K partials at
-// all (partials are HBM writes interleaved with the read stream, which costs
-// far more than their byte count).  Inside a chunk the waves take interleaved
-// 64-token tiles (wave w: tiles w, w+8, ...) and keep a running softmax
+// Work decomposition.  One workgroup of kNW (4) wave64 per work item (entry
+// b, kv head g, chunk of the sequence), two workgroups resident per CU, so
+// one workgroup's ramp-up and drain overlap the other's streaming.  The
+// planner sizes chunks so that work items roughly match the resident
+// workgroup slots of the device, which for long sequences usually means one
+// chunk per sequence and no split-K partials at all (partials are HBM writes
+// interleaved with the read stream, which costs far more than their byte
+// count), and orders the work list longest first.  Inside a chunk the waves
+// take interleaved 64-token tiles (wave w: tiles w, w+kNW, ...) and keep a running softmax
 // (max m, sum l, o[G][D]) in registers, rescaling by 2^(m_old - m_new) from
 // tile to tile.  The G query heads of the group share every K/V byte: each
 // K/V row is loaded once into VGPRs and used for all G heads.
@@ -38,7 +40,7 @@
 //   P.V      v_dot2_f32_f16 on token pairs: a lane holds 8 dims of tokens t
 //            and t+TPI, v_perm_b32 interleaves them into half2
 //            (v[t][d], v[t+TPI][d]); one dot2 per (head, dim) takes two tokens.
-// End: per-wave (m, l, o) combined across the 8 waves in LDS; a work item that
+// End: per-wave (m, l, o) combined across the kNW waves in LDS; a work item that
 // covers its whole sequence is normalised and written as fp16, otherwise
 // (m, l, o[D]) partials go to the workspace and attn_merge_kernel combines
 // the chunks: m* = max m_c, l = sum l_c 2^(m_c-m*), o = sum o_c 2^(m_c-m*)/(l+1e-6).
@@ -62,6 +64,7 @@
 #include <cstring>
 #include <mutex>
 #include <stdexcept>
+#include <string>
 #include <type_traits>
 
 namespace tiny_llm {
@@ -69,16 +72,22 @@ namespace detail {
 
 namespace {
 
-constexpr int kNW = 8;                // waves per workgroup
+// Waves per workgroup and resident workgroups per CU the planner assumes;
+// the kernel asks the register allocator for kNW * kSlotsPerCU / 4 waves per
+// SIMD to make the latter true.
+#ifndef TL_ATTN_NW
+#define TL_ATTN_NW 4
+#endif
+#ifndef TL_ATTN_SLOTS
+#define TL_ATTN_SLOTS (8 / TL_ATTN_NW)
+#endif
+constexpr int kNW = TL_ATTN_NW;
 constexpr int kThreads = kNW * 64;
 constexpr int kTile = 64;             // tokens per wave tile
 constexpr int kQuantum = kNW * kTile; // chunk lengths are multiples of this
-// Resident workgroups per CU the planner assumes; the kernel asks the
-// register allocator for 2 * kSlotsPerCU waves per SIMD to make it true.
-#ifndef TL_ATTN_SLOTS
-#define TL_ATTN_SLOTS 1
-#endif
 constexpr int kSlotsPerCU = TL_ATTN_SLOTS;
+constexpr int kWavesPerEU = kNW * kSlotsPerCU / 4;
+static_assert(kWavesPerEU >= 1, "at least one wave per SIMD");
 
 // Tuning (compile-time): K load steps per batch, V pair blocks per batch.
 #ifndef TL_ATTN_KB
@@ -135,12 +144,25 @@ struct RowAddr {
             vbase = reinterpret_cast<const char *>(v.v_base) + head + (int64_t)row * blk_bytes;
         }
     }
-    // Base of the block holding token t (t wave-uniform); the <= 16 tokens of
-    // one aligned load step share it (blocks hold >= 16 tokens).
-    __device__ __forceinline__ int64_t block_off(int t) const {
+    // Block ids of the tokens [t_first, t_last] of one tile (at most
+    // kTile / 16 + 1 blocks): lane i holds the id of block (t_first >> log2)
+    // + i, clamped to the last one.  Loaded one tile ahead, so the address
+    // arithmetic of the loads never waits on the block table.
+    __device__ __forceinline__ int tile_blocks(int t_first, int t_last, int lane) const {
         if constexpr (PAGED) {
-            const int j = __builtin_amdgcn_readfirstlane(t >> log2_blk);
-            return (int64_t)bt_row[j] * blk_bytes;
+            const int j0 = t_first >> log2_blk, j1 = t_last >> log2_blk;
+            return lane <= kTile / 16 ? bt_row[min(j0 + lane, j1)] : 0;
+        } else {
+            return 0;
+        }
+    }
+    // Base of the block holding token t (t wave-uniform) from the tile's
+    // block ids (j0 = first block of the tile); the <= 16 tokens of one
+    // aligned load step share it (blocks hold >= 16 tokens).
+    __device__ __forceinline__ int64_t block_off(int t, int btv, int j0) const {
+        if constexpr (PAGED) {
+            const int i = __builtin_amdgcn_readfirstlane((t >> log2_blk) - j0);
+            return (int64_t)__builtin_amdgcn_readlane(btv, i) * blk_bytes;
         } else {
             return 0;
         }
@@ -149,7 +171,12 @@ struct RowAddr {
         if constexpr (PAGED) return ((uint32_t)t & mask) * tok_bytes;
         else return (uint32_t)t * tok_bytes;
     }
-    // Per-lane full offset (token may lie in any block).
+    // Per-lane full offset of token t (any block of the tile).
+    __device__ __forceinline__ int64_t lane_off(int t, int btv, int j0) const {
+        if constexpr (PAGED) return (int64_t)__shfl(btv, (t >> log2_blk) - j0) * blk_bytes + in_block(t);
+        else return in_block(t);
+    }
+    // Per-lane full offset straight from the block table (one-off accesses).
     __device__ __forceinline__ int64_t lane_off(int t) const {
         if constexpr (PAGED) return (int64_t)bt_row[t >> log2_blk] * blk_bytes + in_block(t);
         else return in_block(t);
@@ -417,7 +444,7 @@ struct MfmaScorer {
 // ------------------------------------------------------------------ kernel
 template <int D, int G, bool PAGED, bool MFMA>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(2 * kSlotsPerCU))) void attn_decode_kernel(AttnArgs a) {
+__attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnArgs a) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
     using SM = Smem<D, G, MFMA>;
@@ -491,19 +518,20 @@ __attribute__((amdgpu_waves_per_eu(2 * kSlotsPerCU))) void attn_decode_kernel(At
     const int ntiles = (n + kTile - 1) / kTile;
     uint4     kb[2][KB];
     uint4     va[2][VB], vb[2][VB];
-    // Tile at chunk offset ts; tokens below tend are valid.
-    auto kload = [&](int ts, int tend, int bi, uint4(&buf)[KB]) {
+    // Tile at chunk offset ts; tokens below tend are valid; btv / j0: the
+    // tile's block ids (tile_blocks) and first block.
+    auto kload = [&](int ts, int tend, int bi, uint4(&buf)[KB], int btv, int j0) {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int   ss = t0 + ts + (bi * KB + u) * TPI; // step start (global token)
             const int   lim = t0 + tend - 1;
             const int   ssc = ss < lim ? ss : lim;
             const int   t = ss + r < lim ? ss + r : lim;
-            const char *base = ra.kbase + ra.block_off(ssc);
+            const char *base = ra.kbase + ra.block_off(ssc, btv, j0);
             buf[u] = ld16nt(base + ra.in_block(t) + 16 * p);
         }
     };
-    auto vload = [&](int ts, int tend, int bj, uint4(&bufa)[VB], uint4(&bufb)[VB]) {
+    auto vload = [&](int ts, int tend, int bj, uint4(&bufa)[VB], uint4(&bufb)[VB], int btv, int j0) {
 #pragma unroll
         for (int u = 0; u < VB; ++u) {
             const int bs = t0 + ts + (bj * VB + u) * 2 * TPI; // pair block start
@@ -512,27 +540,38 @@ __attribute__((amdgpu_waves_per_eu(2 * kSlotsPerCU))) void attn_decode_kernel(At
             const int tb = bs + TPI + r < lim ? bs + TPI + r : lim;
             if constexpr (kUniformPairs) {
                 const int   bsc = bs < lim ? bs : lim;
-                const char *base = ra.vbase + ra.block_off(bsc);
+                const char *base = ra.vbase + ra.block_off(bsc, btv, j0);
                 bufa[u] = ld16nt(base + ra.in_block(ta) + 16 * p);
                 bufb[u] = ld16nt(base + ra.in_block(tb) + 16 * p);
             } else {
-                bufa[u] = ld16nt(ra.vbase + ra.lane_off(ta) + 16 * p);
-                bufb[u] = ld16nt(ra.vbase + ra.lane_off(tb) + 16 * p);
+                bufa[u] = ld16nt(ra.vbase + ra.lane_off(ta, btv, j0) + 16 * p);
+                bufb[u] = ld16nt(ra.vbase + ra.lane_off(tb, btv, j0) + 16 * p);
             }
         }
     };
+    // First block and block ids of the wave's tile ti (paged views only).
+    auto tile_j0 = [&](int ti_) { return PAGED ? (t0 + ti_ * kTile) >> ra.log2_blk : 0; };
+    auto tile_bt = [&](int ti_) {
+        return ra.tile_blocks(t0 + ti_ * kTile, t0 + min(n, ti_ * kTile + kTile) - 1, lane);
+    };
 
     int ti = wave;
-    if (ti < ntiles) kload(ti * kTile, min(n, ti * kTile + kTile), 0, kb[0]);
+    int bt_cur = 0, bt_next = 0;
+    if (ti < ntiles) {
+        bt_cur = tile_bt(ti);
+        kload(ti * kTile, min(n, ti * kTile + kTile), 0, kb[0], bt_cur, tile_j0(ti));
+    }
     for (; ti < ntiles; ti += kNW) {
         const int ts = ti * kTile;
         const int tend = min(n, ts + kTile);
         const int nt = tend - ts;
+        const int j0 = tile_j0(ti);
+        if (PAGED && ti + kNW < ntiles) bt_next = tile_bt(ti + kNW); // consumed one tile later
         // ---- scores
 #pragma unroll
         for (int bi = 0; bi < NKB; ++bi) {
-            if (bi + 1 < NKB) kload(ts, tend, bi + 1, kb[(bi + 1) & 1]);
-            else vload(ts, tend, 0, va[0], vb[0]);
+            if (bi + 1 < NKB) kload(ts, tend, bi + 1, kb[(bi + 1) & 1], bt_cur, j0);
+            else vload(ts, tend, 0, va[0], vb[0], bt_cur, j0);
             if constexpr (MFMA) {
 #pragma unroll
                 for (int u = 0; u < KB; u += SPG)
@@ -561,10 +600,10 @@ __attribute__((amdgpu_waves_per_eu(2 * kSlotsPerCU))) void attn_decode_kernel(At
 #pragma unroll
         for (int bj = 0; bj < NVB; ++bj) {
             if (bj + 1 < NVB) {
-                vload(ts, tend, bj + 1, va[(bj + 1) & 1], vb[(bj + 1) & 1]);
+                vload(ts, tend, bj + 1, va[(bj + 1) & 1], vb[(bj + 1) & 1], bt_cur, j0);
             } else if (ti + kNW < ntiles) {
                 const int tn = (ti + kNW) * kTile;
-                kload(tn, min(n, tn + kTile), 0, kb[0]);
+                kload(tn, min(n, tn + kTile), 0, kb[0], bt_next, tile_j0(ti + kNW));
             }
 #pragma unroll
             for (int u = 0; u < VB; ++u) {
@@ -604,6 +643,7 @@ __attribute__((amdgpu_waves_per_eu(2 * kSlotsPerCU))) void attn_decode_kernel(At
             __builtin_amdgcn_sched_barrier(0);
         }
         wave_sync_lds(); // pp / kt are rewritten by the next tile
+        bt_cur = bt_next;
     }
 
     // ---- per-wave results -> LDS
@@ -840,11 +880,17 @@ size_t attn_workspace_floats(int n_work, int Hq, int D) {
     return (size_t)n_work * (size_t)Hq * (size_t)(D + 2);
 }
 
-// Chunk length (tokens per work item), a multiple of kQuantum.  Work items
-// are sized so that they roughly match the resident workgroup slots: uniform
-// lengths get one item per slot's share of the total (usually the whole
-// sequence, so no partials), ragged lengths half of that so long sequences
-// split and the tail balances.  TL_ATTN_CHUNK overrides.
+// Chunk length (tokens per work item), a multiple of kQuantum.  With
+// W = sum(lens) * Hkv token-heads of work, C CUs and P = C * kSlotsPerCU
+// resident workgroup slots:
+//  - uniform lengths: chunks of W / P (rounded up), so the items fill the
+//    slots in whole rounds -- usually the whole sequence, hence no partials;
+//  - ragged lengths no longer than the per-CU share W / C: no split (the
+//    workgroups sharing a CU share its bandwidth, and longest-first ordering
+//    balances the CUs without partials or a merge launch);
+//  - longer ragged lengths: chunks of W / (2P), so that longest-first list
+//    scheduling ends within about one small item of the ideal.
+// TL_ATTN_CHUNK (a multiple of kQuantum) overrides.
 int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim) {
     (void)head_dim;
     int64_t total = 0;
@@ -863,12 +909,51 @@ int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, 
         const int c = std::atoi(env);
         if (c >= kQuantum && c % kQuantum == 0) return std::min(c, cap);
     }
-    const int64_t slots = (int64_t)device_cus() * kSlotsPerCU;
-    int64_t       per = (total * num_kv_heads + slots - 1) / slots;
+    const int64_t cus = device_cus();
+    const int64_t slots = cus * kSlotsPerCU;
+    const int64_t work = total * num_kv_heads;
     const bool    uniform = mn >= mx - mx / 10;
-    if (!uniform) per /= 2;
+    int64_t       per;
+    if (uniform) per = (work + slots - 1) / slots;
+    else if (mx <= (work + cus - 1) / cus) per = mx;
+    else per = (work + slots - 1) / slots / 2;
     const int64_t chunk = (per + kQuantum - 1) / kQuantum * kQuantum;
     return (int)std::min<int64_t>(std::max<int64_t>(chunk, kQuantum), cap);
+}
+
+void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out) {
+    out.chunk = choose_chunk(lens, n, num_kv_heads, 0, head_dim);
+    out.part_base.assign((size_t)n + 1, 0);
+    out.any_multi = false;
+    out.any_empty = false;
+    out.max_len = 0;
+    for (int i = 0; i < n; ++i) {
+        const int c = (lens[i] + out.chunk - 1) / out.chunk;
+        out.any_multi |= c > 1;
+        out.any_empty |= c == 0;
+        out.max_len = std::max(out.max_len, (int)lens[i]);
+        out.part_base[(size_t)i + 1] = out.part_base[(size_t)i] + c;
+    }
+    out.n_work = out.part_base[(size_t)n];
+    // (length, entry, chunk) sorted by length descending, then entry, chunk.
+    std::vector<int64_t> key((size_t)out.n_work);
+    size_t               k = 0;
+    for (int i = 0; i < n; ++i)
+        for (int c = 0; c < out.part_base[(size_t)i + 1] - out.part_base[(size_t)i]; ++c) {
+            const int len = std::min(out.chunk, lens[i] - c * out.chunk);
+            // larger length first; ties keep (entry, chunk) order
+            key[k++] = ((int64_t)(INT32_MAX - len) << 32) | (int64_t)(out.part_base[(size_t)i] + c);
+        }
+    std::sort(key.begin(), key.end());
+    out.work.resize(2 * (size_t)out.n_work);
+    // part_base is non-decreasing: entry of partial row r = last i with part_base[i] <= r
+    for (size_t w = 0; w < key.size(); ++w) {
+        const int32_t row = (int32_t)(key[w] & 0xffffffff);
+        const int     i = (int)(std::upper_bound(out.part_base.begin(), out.part_base.end(), row) -
+                            out.part_base.begin()) - 1;
+        out.work[2 * w] = i;
+        out.work[2 * w + 1] = row - out.part_base[(size_t)i];
+    }
 }
 
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
@@ -879,7 +964,8 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     const bool paged = kv.block_table != nullptr;
     const bool mfma = use_mfma_scores(D, G);
     if (plan.chunk % kQuantum != 0 || plan.chunk <= 0)
-        throw std::invalid_argument("attention: chunk length must be a positive multiple of 512");
+        throw std::invalid_argument("attention: chunk length must be a positive multiple of " +
+                                    std::to_string(kQuantum));
     if (!paged && (int64_t)plan.max_len * kv.tok_stride * 2 > (int64_t)UINT32_MAX)
         throw std::invalid_argument("attention: token offsets exceed 32 bits (max_len * row bytes)");
     if (plan.any_multi && !part)

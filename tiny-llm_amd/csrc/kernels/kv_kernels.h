@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <vector>
 
 namespace tiny_llm {
 namespace detail {
@@ -33,7 +34,8 @@ struct KvView {
 //  - uniform: every entry has uniform_len tokens and nchunk chunks; work item
 //    w = b * nchunk + c (work, seq_lens and part_base are NULL).
 //  - ragged:  seq_lens[b] tokens; work[2w], work[2w+1] = (b, c); the items of
-//    entry b are part_base[b] .. part_base[b+1]-1 in chunk order.
+//    entry b own partial rows part_base[b] .. part_base[b+1]-1 in chunk
+//    order; the work list itself is ordered longest item first.
 struct AttnPlan {
     const int32_t *seq_lens = nullptr;
     const int32_t *work = nullptr;
@@ -41,15 +43,32 @@ struct AttnPlan {
     int            uniform_len = 0;
     int            nchunk = 1;
     int            n_work = 0;
-    int            chunk = 512;  // tokens per work item, a positive multiple of 512
+    int            chunk = 256;  // tokens per work item, a positive multiple of the
+                                 // kernel's quantum (waves per workgroup x 64)
     bool           any_multi = false;  // some entry spans more than one chunk
     bool           any_empty = false;  // some entry attends to zero tokens
     int            max_len = 0;        // longest attended length (offset-width check)
 };
 
-// Work-list chunk length (tokens per work item, a multiple of 512) for a set
+// Work-list chunk length (tokens per work item, a multiple of the kernel's
+// quantum of waves-per-workgroup x 64 tokens) for a set
 // of attended lengths (lens, or n entries of uniform_len when lens is NULL).
 int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim);
+
+// Host side of a ragged plan: chunk length, per-entry partial-row bases and
+// the (entry, chunk) work list in longest-first order, so the hardware
+// dispatcher, which hands workgroups to CUs as they free up, schedules the
+// longest items first (LPT list scheduling).
+struct WorkList {
+    int                  chunk = 256;
+    int                  n_work = 0;
+    int                  max_len = 0;
+    bool                 any_multi = false;
+    bool                 any_empty = false;
+    std::vector<int32_t> part_base; // n + 1
+    std::vector<int32_t> work;      // 2 * n_work
+};
+void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out);
 
 // Partials workspace (floats) needed by launch_attn_decode for n_work items.
 size_t attn_workspace_floats(int n_work, int Hq, int D);

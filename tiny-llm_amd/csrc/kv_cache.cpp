@@ -344,7 +344,7 @@ KvView KVCacheManager::layerView(int layer_idx, const int32_t *seq_row_dev) cons
 
 DecodeBatch::DecodeBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads)
     : mgr_(mgr), max_seqs_(max_seqs), num_q_heads_(num_q_heads), meta_(new detail::MetaRing(4)),
-      work_(new detail::Workspace()) {}
+      work_(new detail::Workspace()), plan_(new detail::WorkList()) {}
 
 DecodeBatch::~DecodeBatch() = default;
 
@@ -401,18 +401,13 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
             lens_[static_cast<size_t>(i)] = a;
         }
     }
-    // Split-K plan: work items (entry, chunk) in entry order.
-    chunk_ = detail::choose_chunk(lens_.data(), n, cfg.num_heads, 0, cfg.head_dim);
-    std::vector<int32_t> part_base(static_cast<size_t>(n) + 1, 0);
-    any_multi_ = false;
-    any_empty_ = false;
-    for (int i = 0; i < n; ++i) {
-        const int c = (lens_[static_cast<size_t>(i)] + chunk_ - 1) / chunk_;
-        any_multi_ |= c > 1;
-        any_empty_ |= c == 0;
-        part_base[static_cast<size_t>(i) + 1] = part_base[static_cast<size_t>(i)] + c;
-    }
-    n_work_ = part_base[static_cast<size_t>(n)];
+    // Split-K plan: work items (entry, chunk), longest first.
+    detail::WorkList &wl = *plan_;
+    detail::plan_work(lens_.data(), n, cfg.num_heads, cfg.head_dim, wl);
+    chunk_ = wl.chunk;
+    any_multi_ = wl.any_multi;
+    any_empty_ = wl.any_empty;
+    n_work_ = wl.n_work;
 
     const size_t n1 = static_cast<size_t>(n);
     const size_t words = 3 * n1 + (n1 + 1) + 2 * static_cast<size_t>(n_work_);
@@ -420,13 +415,8 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
     std::memcpy(h, lens_.data(), n1 * 4);
     std::memcpy(h + n1, wpos_.data(), n1 * 4);
     std::memcpy(h + 2 * n1, slot_.data(), n1 * 4);
-    std::memcpy(h + 3 * n1, part_base.data(), (n1 + 1) * 4);
-    int32_t *w = h + 4 * n1 + 1;
-    for (int i = 0; i < n; ++i)
-        for (int c = part_base[static_cast<size_t>(i)]; c < part_base[static_cast<size_t>(i) + 1]; ++c) {
-            *w++ = i;
-            *w++ = c - part_base[static_cast<size_t>(i)];
-        }
+    std::memcpy(h + 3 * n1, wl.part_base.data(), (n1 + 1) * 4);
+    if (n_work_ > 0) std::memcpy(h + 4 * n1 + 1, wl.work.data(), 2 * static_cast<size_t>(n_work_) * 4);
     const int32_t *d = static_cast<const int32_t *>(meta_->commit(stream));
     d_lens_ = d;
     d_wpos_ = d + n1;

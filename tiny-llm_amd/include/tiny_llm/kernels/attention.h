@@ -11,7 +11,7 @@ namespace kernels {
 // head_dim], O: [batch, num_heads, 1, head_dim]; fp16, fp32 accumulate.
 // Same contract as the reference: silently returns when a dimension is not
 // positive (attention.cu:117-119).  Unlike the reference, seq_len is not
-// limited by shared memory (split-K over 512-token chunks) and launch errors
+// limited by shared memory (split-K over chunks of the sequence) and launch errors
 // are reported through the logger instead of being dropped.
 void attention_decode(const half *__restrict__ query, const half *__restrict__ k_cache,
                       const half *__restrict__ v_cache, half *__restrict__ output, float scale,

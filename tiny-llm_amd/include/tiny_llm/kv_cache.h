@@ -24,6 +24,7 @@ namespace tiny_llm {
 
 namespace detail {
 struct KvView;
+struct WorkList;
 class MetaRing;
 class Workspace;
 } // namespace detail
@@ -149,6 +150,7 @@ class DecodeBatch {
     std::vector<int32_t> ids_, lens_, wpos_, slot_;
     std::unique_ptr<detail::MetaRing>  meta_;
     std::unique_ptr<detail::Workspace> work_;
+    std::unique_ptr<detail::WorkList>  plan_;
     const int32_t  *d_lens_ = nullptr, *d_wpos_ = nullptr, *d_slot_ = nullptr;
     const int32_t  *d_part_base_ = nullptr, *d_work_ = nullptr;
 };
