@@ -380,7 +380,7 @@ def main():
     chunk_avg_ms = chunk_ms / max(1, chunk_n)
     achieved = r["attn_bytes"] / (chunk_avg_ms * 1e-3) / 1e9 if chunk_n else 0.0
     sp = tl.get_score_path()
-    score_kind = "mfma" if sp == 1 or (sp == 2 and Hq // Hkv >= 8) else "valu"
+    score_kind = "mfma" if sp == 1 and D <= 128 else "valu"
     metric = METRIC if args.config == 3 and not args.q_heads else \
         f"decode attn+KV append µs/step and achieved HBM GB/s (% of peak), {conf['workload']}"
     line = {

@@ -192,14 +192,23 @@ void tl_attention_decode(const void *q, const void *k, const void *v, void *out,
 
 /* Score (q.K^T) path of the decode attention kernels, process-wide:
  * 0 = VALU v_dot2 over the loaded K rows, 1 = MFMA v_mfma_f32_16x16x32_f16
- * over an LDS-transposed K tile (head_dim <= 128; VALU above), 2 = auto:
- * MFMA for GQA groups of 8 or more query heads per kv head, VALU below (at
- * group 4 both run at the same HBM-bound speed; at group 8 MFMA is faster).
+ * over an LDS-transposed K tile (head_dim <= 128; VALU above), 2 = auto,
+ * which resolves to VALU for every supported group (<= 8): both paths are
+ * HBM-bound and MFMA was never faster on the measured decode workloads.
  * Both give results within the 1e-3 gate of the same oracle.  Initial value
  * from the environment variable TL_ATTN_QK ("valu" / "mfma" / "auto"), else
  * 2.  No reference counterpart (tuning knob). */
 int tl_attn_set_score_path(int path);
 int tl_attn_get_score_path(void);
+
+/* Waves per decode-attention workgroup, process-wide: 4, 8, or 0 = auto (8
+ * when the launch gives every CU at most two workgroups in turn, else two
+ * 4-wave workgroups per CU whose ramp-up and drain overlap).  Initial value
+ * from the environment variable TL_ATTN_WAVES ("4" / "8" / "auto"), else 0.
+ * Every setting gives results within the same 1e-3 gate.  No reference
+ * counterpart (tuning knob). */
+int tl_attn_set_waves(int waves);
+int tl_attn_get_waves(void);
 
 /* ------------------------------------------------------------------------
  * Kernel timing (the reference has only an unused CudaEvent wrapper,

@@ -1,7 +1,8 @@
 """GPU: every instantiated (head_dim, group) shape, both score paths (VALU and
-MFMA), contiguous and paged cache layouts, ragged lengths that span one and
-several split-K chunks -- one decode step (append + attention) each, against
-the oracle (attention <= 1e-3 normwise, cache bytes bit-exact)."""
+MFMA), both workgroup sizes (4 and 8 waves), contiguous and paged cache
+layouts, ragged lengths that span one and several split-K chunks -- one
+decode step (append + attention) each, against the oracle (attention <= 1e-3
+normwise, cache bytes bit-exact)."""
 import numpy as np
 import pytest
 
@@ -19,20 +20,30 @@ def score_path(tl):
     tl.set_score_path(before)
 
 
+@pytest.fixture
+def waves(tl):
+    before = tl.get_waves()
+    yield tl.set_waves
+    tl.set_waves(before)
+
+
 def f16bits(rng, shape):
     return rng.standard_normal(shape).astype(np.float32).astype(np.float16).view(np.uint16)
 
 
+@pytest.mark.parametrize("nw", [4, 8])
 @pytest.mark.parametrize("chunk", ["auto", "256"])
 @pytest.mark.parametrize("paged", [False, True])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 @pytest.mark.parametrize("D", [32, 64, 128, 256])
 @pytest.mark.parametrize("path", [0, 1])
-def test_decode_step_all_shapes(tl, orc, score_path, monkeypatch, path, D, G, paged, chunk):
+def test_decode_step_all_shapes(tl, orc, score_path, waves, monkeypatch, path, D, G, paged, chunk,
+                                nw):
     """chunk=256 forces the smallest work items (one 64-token tile per wave,
     most entries split into several chunks and merged); "auto" lets the
     planner choose for this small batch."""
     score_path(path)
+    waves(nw)
     if chunk != "auto":
         monkeypatch.setenv("TL_ATTN_CHUNK", chunk)
     rng = np.random.default_rng(path * 1000 + D * 10 + G + (500 if paged else 0))

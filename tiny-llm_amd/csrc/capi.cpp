@@ -280,6 +280,15 @@ int tl_attn_set_score_path(int path) {
 
 int tl_attn_get_score_path(void) { return tiny_llm::detail::score_path(); }
 
+int tl_attn_set_waves(int waves) {
+    if (waves != 0 && waves != 4 && waves != 8)
+        return fail(TL_ERR_INVALID, "tl_attn_set_waves: waves must be 0 (auto), 4 or 8");
+    tiny_llm::detail::set_waves(waves);
+    return TL_OK;
+}
+
+int tl_attn_get_waves(void) { return tiny_llm::detail::waves(); }
+
 void tl_profile_enable(int on) { tiny_llm::detail::profile_set(on != 0); }
 void tl_profile_reset(void) { tiny_llm::detail::profile_reset(); }
 

@@ -7,15 +7,17 @@
 // 11-112: scores, max, expf, 1/(sum+1e-6f), P.V, RNE fp16 output), extended to
 // GQA over the token-major cache of kv_cache.cpp:226-233.
 //
-// Work decomposition.  One workgroup of kNW (4) wave64 per work item (entry
-// b, kv head g, chunk of the sequence), two workgroups resident per CU, so
-// one workgroup's ramp-up and drain overlap the other's streaming.  The
-// planner sizes chunks so that work items roughly match the resident
-// workgroup slots of the device, which for long sequences usually means one
-// chunk per sequence and no split-K partials at all (partials are HBM writes
-// interleaved with the read stream, which costs far more than their byte
-// count), and orders the work list longest first.  Inside a chunk the waves
-// take interleaved 64-token tiles (wave w: tiles w, w+kNW, ...) and keep a running softmax
+// Work decomposition.  One workgroup of NW wave64 per work item (entry b, kv
+// head g, chunk of the sequence), 8 waves resident per CU: one 8-wave
+// workgroup, or two 4-wave workgroups whose ramp-up and drain overlap each
+// other's streaming (chosen per launch: 8 waves when every CU gets at most two
+// workgroups in turn, 4 waves for longer work lists).  The planner sizes
+// chunks so that work items roughly match the resident workgroup slots of the
+// device, which for long sequences usually means one chunk per sequence and
+// no split-K partials at all (partials are HBM writes interleaved with the
+// read stream, which costs far more than their byte count), and orders the
+// work list longest first.  Inside a chunk the waves take interleaved 64-token
+// tiles (wave w: tiles w, w+NW, ...) and keep a running softmax
 // (max m, sum l, o[G][D]) in registers, rescaling by 2^(m_old - m_new) from
 // tile to tile.  The G query heads of the group share every K/V byte: each
 // K/V row is loaded once into VGPRs and used for all G heads.
@@ -40,7 +42,7 @@
 //   P.V      v_dot2_f32_f16 on token pairs: a lane holds 8 dims of tokens t
 //            and t+TPI, v_perm_b32 interleaves them into half2
 //            (v[t][d], v[t+TPI][d]); one dot2 per (head, dim) takes two tokens.
-// End: per-wave (m, l, o) combined across the kNW waves in LDS; a work item that
+// End: per-wave (m, l, o) combined across the NW waves in LDS; a work item that
 // covers its whole sequence is normalised and written as fp16, otherwise
 // (m, l, o[D]) partials go to the workspace and attn_merge_kernel combines
 // the chunks: m* = max m_c, l = sum l_c 2^(m_c-m*), o = sum o_c 2^(m_c-m*)/(l+1e-6).
@@ -72,22 +74,13 @@ namespace detail {
 
 namespace {
 
-// Waves per workgroup and resident workgroups per CU the planner assumes;
-// the kernel asks the register allocator for kNW * kSlotsPerCU / 4 waves per
-// SIMD to make the latter true.
-#ifndef TL_ATTN_NW
-#define TL_ATTN_NW 4
-#endif
-#ifndef TL_ATTN_SLOTS
-#define TL_ATTN_SLOTS (8 / TL_ATTN_NW)
-#endif
-constexpr int kNW = TL_ATTN_NW;
-constexpr int kThreads = kNW * 64;
+// Resident waves per SIMD the kernels ask the register allocator for (8 per
+// CU: one 8-wave or two 4-wave workgroups); the planner's slot count is
+// expressed in 4-wave workgroups.
+constexpr int kWavesPerEU = 2;
 constexpr int kTile = 64;             // tokens per wave tile
-constexpr int kQuantum = kNW * kTile; // chunk lengths are multiples of this
-constexpr int kSlotsPerCU = TL_ATTN_SLOTS;
-constexpr int kWavesPerEU = kNW * kSlotsPerCU / 4;
-static_assert(kWavesPerEU >= 1, "at least one wave per SIMD");
+constexpr int kQuantum = 4 * kTile;   // chunk lengths are multiples of this
+constexpr int kSlotsPerCU = kWavesPerEU;
 
 // Tuning (compile-time): K load steps per batch, V pair blocks per batch.
 #ifndef TL_ATTN_KB
@@ -242,7 +235,7 @@ __device__ __forceinline__ void wave_sync_lds() {
 // in turn, the K transpose tile of the MFMA path (16 rows of D halves, padded
 // by 8 halves so that column reads of 16 rows fall in distinct bank groups),
 // the tile's fp16 p, and at the end the wave's o[G][D] for the combine.
-template <int D, int G, bool MFMA>
+template <int D, int G, bool MFMA, int kNW>
 struct Smem {
     static constexpr int kKt = MFMA ? 16 * (D + 8) * 2 : 0; // bytes
     static constexpr int kPp = kTile * G * 2;
@@ -442,12 +435,14 @@ struct MfmaScorer {
 };
 
 // ------------------------------------------------------------------ kernel
-template <int D, int G, bool PAGED, bool MFMA>
-__global__ __launch_bounds__(kThreads)
+template <int D, int G, bool PAGED, bool MFMA, int kNW>
+__global__ __launch_bounds__(kNW * 64)
 __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnArgs a) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
-    using SM = Smem<D, G, MFMA>;
+    static_assert(kNW == 4 || kNW == 8, "waves per workgroup");
+    constexpr int kThreads = kNW * 64;
+    using SM = Smem<D, G, MFMA, kNW>;
     using Scorer = typename std::conditional<MFMA, MfmaScorer<D, G>, ValuScorer<D, G>>::type;
     constexpr int  LPR = D / 8;
     constexpr int  TPI = 64 / LPR;
@@ -791,49 +786,60 @@ void launch_merge_g(const MergeArgs &m, int B, int Hkv, int G, hipStream_t strea
     }
 }
 
-template <int D, int G, bool PAGED, bool MFMA>
+template <int D, int G, bool PAGED, bool MFMA, int NW>
 void launch_one(const AttnArgs &args, int n_work, int Hkv, hipStream_t stream) {
-    using SM = Smem<D, G, MFMA>;
-    auto                 *fn = attn_decode_kernel<D, G, PAGED, MFMA>;
+    using SM = Smem<D, G, MFMA, NW>;
+    auto                 *fn = attn_decode_kernel<D, G, PAGED, MFMA, NW>;
     static std::once_flag once;
     std::call_once(once, [&] {
         HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, SM::kBytes));
     });
-    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * (unsigned)Hkv), dim3(kThreads), SM::kBytes, stream,
+    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * (unsigned)Hkv), dim3(NW * 64), SM::kBytes, stream,
                        args);
 }
 
+template <int D, int G, bool MFMA>
+void launch_dgm(const AttnArgs &args, int n_work, int Hkv, bool paged, int nw, hipStream_t stream) {
+    if (nw == 8) {
+        if (paged) launch_one<D, G, true, MFMA, 8>(args, n_work, Hkv, stream);
+        else launch_one<D, G, false, MFMA, 8>(args, n_work, Hkv, stream);
+    } else {
+        if (paged) launch_one<D, G, true, MFMA, 4>(args, n_work, Hkv, stream);
+        else launch_one<D, G, false, MFMA, 4>(args, n_work, Hkv, stream);
+    }
+}
+
 template <int D, int G>
-void launch_dg(const AttnArgs &args, int n_work, int Hkv, bool paged, bool mfma, hipStream_t stream) {
+void launch_dg(const AttnArgs &args, int n_work, int Hkv, bool paged, bool mfma, int nw,
+               hipStream_t stream) {
     if constexpr (D <= 128) { // the MFMA score path exists for head_dim <= 128
         if (mfma) {
-            if (paged) launch_one<D, G, true, true>(args, n_work, Hkv, stream);
-            else launch_one<D, G, false, true>(args, n_work, Hkv, stream);
+            launch_dgm<D, G, true>(args, n_work, Hkv, paged, nw, stream);
             return;
         }
     }
-    if (paged) launch_one<D, G, true, false>(args, n_work, Hkv, stream);
-    else launch_one<D, G, false, false>(args, n_work, Hkv, stream);
+    launch_dgm<D, G, false>(args, n_work, Hkv, paged, nw, stream);
 }
 
 template <int D>
-void launch_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool mfma,
+void launch_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool mfma, int nw,
               hipStream_t stream) {
     switch (G) {
-    case 1: launch_dg<D, 1>(args, n_work, Hkv, paged, mfma, stream); break;
-    case 2: launch_dg<D, 2>(args, n_work, Hkv, paged, mfma, stream); break;
-    case 4: launch_dg<D, 4>(args, n_work, Hkv, paged, mfma, stream); break;
-    case 8: launch_dg<D, 8>(args, n_work, Hkv, paged, mfma, stream); break;
+    case 1: launch_dg<D, 1>(args, n_work, Hkv, paged, mfma, nw, stream); break;
+    case 2: launch_dg<D, 2>(args, n_work, Hkv, paged, mfma, nw, stream); break;
+    case 4: launch_dg<D, 4>(args, n_work, Hkv, paged, mfma, nw, stream); break;
+    case 8: launch_dg<D, 8>(args, n_work, Hkv, paged, mfma, nw, stream); break;
     default: break;
     }
 }
 
 // Score path: TL_ATTN_QK ("valu" / "mfma" / "auto") at first use, else
-// auto; tl_attn_set_score_path overrides it.  Auto takes MFMA from group 8 up:
-// measured on cfg3's batch and context, group 4 runs at the same speed on
-// both paths and group 8 is faster on MFMA (the VALU path's 8 heads x 8 dims
-// of P.V accumulators plus 8 q rows crowd the register file).
+// auto; tl_attn_set_score_path overrides it.  Auto resolves to VALU for every
+// supported group: measured on the decode workloads (group 4 and 8, uniform
+// and ragged contexts) the MFMA path is never faster -- both are HBM-bound,
+// and at group 8 the MFMA path's LDS staging and K double buffer spill a few
+// more registers than the VALU path.
 std::atomic<int> g_score_path{-1};
 
 int score_path_setting() {
@@ -849,9 +855,36 @@ int score_path_setting() {
 }
 
 bool use_mfma_scores(int D, int G) {
+    (void)G;
     if (D > 128) return false;
-    const int v = score_path_setting();
-    return v == 1 || (v == 2 && G >= 8);
+    return score_path_setting() == 1;
+}
+
+// Waves per workgroup: TL_ATTN_WAVES ("4" / "8" / "auto") at first use,
+// else auto; tl_attn_set_waves overrides it (0 = auto).  Auto: 8-wave
+// workgroups when the launch gives every CU at most two workgroups in turn
+// (one resident at a time streams with all 8 waves to the end), else 4-wave
+// workgroups two per CU, whose ramp-up and drain overlap.
+std::atomic<int> g_waves{-1};
+
+int waves_setting() {
+    int v = g_waves.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char *e = std::getenv("TL_ATTN_WAVES");
+        v = 0;
+        if (e && std::strcmp(e, "4") == 0) v = 4;
+        if (e && std::strcmp(e, "8") == 0) v = 8;
+        g_waves.store(v);
+    }
+    return v;
+}
+
+int device_cus();
+
+int waves_for(int64_t workgroups) {
+    const int v = waves_setting();
+    if (v) return v;
+    return workgroups <= 2 * (int64_t)device_cus() ? 8 : 4;
 }
 
 int device_cus() {
@@ -870,6 +903,8 @@ int device_cus() {
 } // namespace
 
 void set_score_path(int path) { g_score_path.store(path); }
+void set_waves(int waves) { g_waves.store(waves); }
+int  waves() { return waves_setting(); }
 int  score_path() { return score_path_setting(); }
 
 bool attn_shape_supported(int D, int G) {
@@ -984,12 +1019,13 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     args.scale_log2 = scale * 1.4426950408889634f;
 
     if (plan.n_work > 0) {
+        const int nw = waves_for((int64_t)plan.n_work * Hkv);
         profile_begin(KernelId::AttnChunk, stream);
         switch (D) {
-        case 32: launch_d<32>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
-        case 64: launch_d<64>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
-        case 128: launch_d<128>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
-        case 256: launch_d<256>(args, plan.n_work, Hkv, G, paged, mfma, stream); break;
+        case 32: launch_d<32>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
+        case 64: launch_d<64>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
+        case 128: launch_d<128>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
+        case 256: launch_d<256>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
         default: break;
         }
         HIP_CHECK(hipGetLastError());

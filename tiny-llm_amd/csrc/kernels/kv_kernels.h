@@ -101,10 +101,14 @@ void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int un
                       int Hkv, int D, int s_max, __half *out, hipStream_t stream);
 
 // Score path of the attention kernels: 0 = VALU dot products over the
-// loaded rows, 1 = MFMA over an LDS-transposed K tile, 2 = auto (MFMA for
-// groups of >= 8 query heads per kv head).
+// loaded rows, 1 = MFMA over an LDS-transposed K tile, 2 = auto (VALU for
+// every supported group).
 void set_score_path(int path);
 int  score_path();
+
+// Waves per attention workgroup: 0 = auto, 4 or 8.
+void set_waves(int waves);
+int  waves();
 
 // Per-kernel event timing (tl_profile_*).
 enum class KernelId { AttnChunk = 0, AttnMerge = 1, KvAppend = 2, KvGather = 3, Count = 4 };

@@ -104,6 +104,8 @@ def _declare(L: C.CDLL) -> None:
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
         "tl_attn_set_score_path": (i, [i]),
         "tl_attn_get_score_path": (i, []),
+        "tl_attn_set_waves": (i, [i]),
+        "tl_attn_get_waves": (i, []),
         "tl_profile_enable": (None, [i]),
         "tl_profile_reset": (None, []),
         "tl_profile_query": (i, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
@@ -300,12 +302,21 @@ SCORE_AUTO = 2
 
 def set_score_path(path: int):
     """0 = VALU dot products, 1 = MFMA over an LDS-transposed K tile,
-    2 = auto (MFMA for groups of >= 8 query heads per kv head)."""
+    2 = auto (VALU for every supported group)."""
     _check(load().tl_attn_set_score_path(path))
 
 
 def get_score_path() -> int:
     return load().tl_attn_get_score_path()
+
+
+def set_waves(waves: int):
+    """Waves per attention workgroup: 0 = auto, 4 or 8."""
+    _check(load().tl_attn_set_waves(waves))
+
+
+def get_waves() -> int:
+    return load().tl_attn_get_waves()
 
 
 def profile_enable(on: bool = True):
