@@ -45,6 +45,24 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
     WorkList wl;
     plan_work(seq_lens_host, B, Hkv, D, wl);
     const int      n_work = wl.n_work;
+    if (kv.seq_row == nullptr) { // small plans travel in the kernel arguments
+        InlineMeta inl;
+        if (pack_inline(seq_lens_host, wl, nullptr, B, inl)) {
+            DeviceContext &ctx = DeviceContext::get(current_device());
+            std::lock_guard<std::mutex> lk(ctx.mu);
+            ctx.claim(stream);
+            AttnPlan plan;
+            plan.n_work = n_work;
+            plan.chunk = wl.chunk;
+            plan.any_multi = wl.any_multi;
+            plan.any_empty = wl.any_empty;
+            plan.max_len = wl.max_len;
+            float *part = wl.any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
+            launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, nullptr, nullptr, stream,
+                               &inl);
+            return "";
+        }
+    }
     const size_t   nb = static_cast<size_t>(B);
     DeviceContext &ctx = DeviceContext::get(current_device());
     std::lock_guard<std::mutex> lk(ctx.mu);

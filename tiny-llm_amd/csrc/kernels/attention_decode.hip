@@ -107,6 +107,7 @@ struct AttnArgs {
     int           Hq;
     int           Hkv;
     float         scale_log2; // scale * log2(e)
+    InlineMeta    meta;       // used when meta.n > 0
 };
 
 // Byte addressing of the token rows of one (entry, kv head).
@@ -120,8 +121,7 @@ struct RowAddr {
     int            log2_blk;
     uint32_t       mask;
 
-    __device__ __forceinline__ RowAddr(const KvView &v, int b, int g) {
-        const int     row = v.seq_row ? v.seq_row[b] : b;
+    __device__ __forceinline__ RowAddr(const KvView &v, int row, int g) {
         const int64_t head = (int64_t)g * v.head_stride * 2;
         blk_bytes = v.blk_stride * 2;
         tok_bytes = (uint32_t)(v.tok_stride * 2);
@@ -464,21 +464,33 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     // same token rows are dispatched together.
     const int item = blockIdx.x / a.Hkv;
     const int g = blockIdx.x - item * a.Hkv;
-    int       b, c;
-    if (pl.work) {
-        b = pl.work[2 * item];
-        c = pl.work[2 * item + 1];
+    int       b, c, S, nch, widx, row;
+    if (a.meta.n) { // metadata in the kernel arguments
+        const int32_t *w = a.meta.w;
+        b = w[a.meta.off_work + 2 * item];
+        c = w[a.meta.off_work + 2 * item + 1];
+        S = w[b];
+        const int pb = w[a.meta.off_part + b];
+        nch = w[a.meta.off_part + b + 1] - pb;
+        widx = pb + c;
+        row = a.meta.has_rows ? w[a.meta.off_rows + b] : b;
     } else {
-        b = item / pl.nchunk;
-        c = item - b * pl.nchunk;
+        if (pl.work) {
+            b = pl.work[2 * item];
+            c = pl.work[2 * item + 1];
+        } else {
+            b = item / pl.nchunk;
+            c = item - b * pl.nchunk;
+        }
+        S = pl.seq_lens ? pl.seq_lens[b] : pl.uniform_len;
+        nch = pl.part_base ? pl.part_base[b + 1] - pl.part_base[b] : pl.nchunk;
+        widx = pl.part_base ? pl.part_base[b] + c : item;
+        row = a.kv.seq_row ? a.kv.seq_row[b] : b;
     }
-    const int S = pl.seq_lens ? pl.seq_lens[b] : pl.uniform_len;
-    const int nch = pl.part_base ? pl.part_base[b + 1] - pl.part_base[b] : pl.nchunk;
-    const int widx = pl.part_base ? pl.part_base[b] + c : item;
     const int t0 = c * pl.chunk;
     const int n = min(pl.chunk, S - t0); // >= 1 by construction of the plan
 
-    const RowAddr<PAGED> ra(a.kv, b, g);
+    const RowAddr<PAGED> ra(a.kv, row, g);
 
     if (a.new_k && c == nch - 1) {
         // Fused appendKV(n=1) of head g at position S-1 (same bytes as the
@@ -703,6 +715,7 @@ struct MergeArgs {
     int            nchunk;
     int            Hq;
     int            Hkv;
+    InlineMeta     meta; // part_base from here when meta.n > 0
 };
 
 constexpr int kMergeMaxChunks = 64;
@@ -718,14 +731,24 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     __shared__ float s_m[G], s_l[G];
     const int        b = blockIdx.x / a.Hkv;
     const int        g = blockIdx.x - b * a.Hkv;
-    const int        nch = a.part_base ? a.part_base[b + 1] - a.part_base[b] : a.nchunk;
+    int              pb0, nch;
+    if (a.meta.n) {
+        pb0 = a.meta.w[a.meta.off_part + b];
+        nch = a.meta.w[a.meta.off_part + b + 1] - pb0;
+    } else if (a.part_base) {
+        pb0 = a.part_base[b];
+        nch = a.part_base[b + 1] - pb0;
+    } else {
+        pb0 = b * a.nchunk;
+        nch = a.nchunk;
+    }
     __half          *dst = a.out + ((int64_t)b * a.Hq + (int64_t)g * G) * D;
     if (nch == 1) return; // written by attn_decode_kernel
     if (nch == 0) {
         for (int i = threadIdx.x; i < G * D; i += 256) dst[i] = __float2half(0.0f);
         return;
     }
-    const int w0 = a.part_base ? a.part_base[b] : b * a.nchunk;
+    const int w0 = pb0;
     for (int c0 = 0; c0 < nch; c0 += kMergeMaxChunks) {
         const int cn = min(kMergeMaxChunks, nch - c0);
         for (int i = threadIdx.x; i < cn * G; i += 256) {
@@ -991,9 +1014,25 @@ void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkL
     }
 }
 
+bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
+                 InlineMeta &out) {
+    const int words = n + (n + 1) + 2 * plan.n_work + (rows ? n : 0);
+    if (n <= 0 || words > kInlineWords) return false;
+    out.n = n;
+    out.has_rows = rows ? 1 : 0;
+    out.off_part = n;
+    out.off_work = 2 * n + 1;
+    out.off_rows = out.off_work + 2 * plan.n_work;
+    std::memcpy(out.w, lens, (size_t)n * 4);
+    std::memcpy(out.w + out.off_part, plan.part_base.data(), (size_t)(n + 1) * 4);
+    if (plan.n_work) std::memcpy(out.w + out.off_work, plan.work.data(), (size_t)plan.n_work * 8);
+    if (rows) std::memcpy(out.w + out.off_rows, rows, (size_t)n * 4);
+    return true;
+}
+
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
                         int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
-                        const __half *new_v, hipStream_t stream) {
+                        const __half *new_v, hipStream_t stream, const InlineMeta *inl) {
     const int G = Hq / Hkv;
     if (plan.n_work <= 0 && !plan.any_empty) return;
     const bool paged = kv.block_table != nullptr;
@@ -1017,6 +1056,8 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     args.Hq = Hq;
     args.Hkv = Hkv;
     args.scale_log2 = scale * 1.4426950408889634f;
+    if (inl) std::memcpy(&args.meta, inl, sizeof(InlineMeta));
+    else args.meta.n = 0;
 
     if (plan.n_work > 0) {
         const int nw = waves_for((int64_t)plan.n_work * Hkv);
@@ -1041,6 +1082,8 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         m.nchunk = plan.nchunk;
         m.Hq = Hq;
         m.Hkv = Hkv;
+        if (inl) std::memcpy(&m.meta, inl, sizeof(InlineMeta));
+        else m.meta.n = 0;
         profile_begin(KernelId::AttnMerge, stream);
         switch (D) {
         case 32: launch_merge_g<32>(m, B, Hkv, G, stream); break;

@@ -70,6 +70,23 @@ struct WorkList {
 };
 void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out);
 
+// Plan metadata small enough to travel in the kernel arguments, so that a
+// launch needs no separate host-to-device copy.  Words:
+//   [lens n | part_base n+1 | work 2*n_work | rows n (if has_rows)]
+// rows[b] is the cache row (slot) of entry b, replacing KvView::seq_row.
+constexpr int kInlineWords = 896;
+struct InlineMeta {
+    int32_t n = 0; // entries; 0 = metadata comes through the AttnPlan pointers
+    int32_t has_rows = 0;
+    int32_t off_part = 0;
+    int32_t off_work = 0;
+    int32_t off_rows = 0;
+    int32_t w[kInlineWords];
+};
+// Packs lens / plan / rows (rows may be NULL) into out; false if they do not fit.
+bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
+                 InlineMeta &out);
+
 // Partials workspace (floats) needed by launch_attn_decode for n_work items.
 size_t attn_workspace_floats(int n_work, int Hq, int D);
 
@@ -82,9 +99,11 @@ bool attn_shape_supported(int D, int G);
 // seq_lens[b]-1 before attending (the decode branch of a transformer layer).
 // Throws HipException on launch failure, std::invalid_argument when a token
 // offset of a non-paged view does not fit in 32 bits.
+// inl (optional): the plan's metadata in kernel arguments; when given, the
+// seq_lens / work / part_base pointers of plan and kv.seq_row are not read.
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
                         int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
-                        const __half *new_v, hipStream_t stream);
+                        const __half *new_v, hipStream_t stream, const InlineMeta *inl = nullptr);
 
 // One token row ([Hkv][D] contiguous: tok_stride == Hkv*D, head_stride == D)
 // per (entry i, layer l) for n entries and num_layers layers.

@@ -344,7 +344,8 @@ KvView KVCacheManager::layerView(int layer_idx, const int32_t *seq_row_dev) cons
 
 DecodeBatch::DecodeBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads)
     : mgr_(mgr), max_seqs_(max_seqs), num_q_heads_(num_q_heads), meta_(new detail::MetaRing(4)),
-      work_(new detail::Workspace()), plan_(new detail::WorkList()) {}
+      work_(new detail::Workspace()), plan_(new detail::WorkList()),
+      inl_(new detail::InlineMeta()) {}
 
 DecodeBatch::~DecodeBatch() = default;
 
@@ -408,10 +409,23 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
     any_multi_ = wl.any_multi;
     any_empty_ = wl.any_empty;
     n_work_ = wl.n_work;
+    n_ = n;
+    appendable_ = appendable;
+    // Small batches carry their metadata in the attention kernel's arguments;
+    // the device copy is made only when a kernel that reads it is launched.
+    inline_ok_ = detail::pack_inline(lens_.data(), wl, slot_.data(), n, *inl_);
+    uploaded_ = false;
+    if (!inline_ok_) upload_device(stream);
+    return Result<void>::ok();
+}
 
-    const size_t n1 = static_cast<size_t>(n);
-    const size_t words = 3 * n1 + (n1 + 1) + 2 * static_cast<size_t>(n_work_);
-    int32_t     *h = static_cast<int32_t *>(meta_->begin(words * sizeof(int32_t)));
+// Device copy of [lens | wpos | slot | part_base | work] through the ring.
+void DecodeBatch::upload_device(hipStream_t stream) {
+    if (uploaded_) return;
+    const detail::WorkList &wl = *plan_;
+    const size_t            n1 = static_cast<size_t>(n_);
+    const size_t            words = 3 * n1 + (n1 + 1) + 2 * static_cast<size_t>(n_work_);
+    int32_t                *h = static_cast<int32_t *>(meta_->begin(words * sizeof(int32_t)));
     std::memcpy(h, lens_.data(), n1 * 4);
     std::memcpy(h + n1, wpos_.data(), n1 * 4);
     std::memcpy(h + 2 * n1, slot_.data(), n1 * 4);
@@ -423,9 +437,7 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
     d_slot_ = d + 2 * n1;
     d_part_base_ = d + 3 * n1;
     d_work_ = d + 4 * n1 + 1;
-    n_ = n;
-    appendable_ = appendable;
-    return Result<void>::ok();
+    uploaded_ = true;
 }
 
 Result<void> DecodeBatch::prepare(const int *seq_ids, int n, hipStream_t stream) {
@@ -460,6 +472,7 @@ Result<void> DecodeBatch::append(int layer_begin, int num_layers, const half *ne
                                  std::to_string(layer_begin + num_layers) + ") outside [0, " +
                                  std::to_string(cfg.num_layers) + ")");
     if (n_ == 0) return Result<void>::ok();
+    upload_device(stream);
     const KvView  v = mgr_.layerView(layer_begin, d_slot_);
     const int64_t layer_stride =
         2 * static_cast<int64_t>(cfg.num_heads) * cfg.max_seq_len * cfg.head_dim;
@@ -481,6 +494,7 @@ Result<void> DecodeBatch::run_attention(int layer_idx, const half *q, const half
     if (layer_idx < 0 || layer_idx >= cfg.num_layers)
         return Result<void>::err("DecodeBatch: Invalid layer_idx: " + std::to_string(layer_idx));
     if (n_ == 0) return Result<void>::ok();
+    if (!inline_ok_) upload_device(stream);
     detail::AttnPlan plan;
     plan.seq_lens = d_lens_;
     plan.work = d_work_;
@@ -494,7 +508,8 @@ Result<void> DecodeBatch::run_attention(int layer_idx, const half *q, const half
     if (any_multi_)
         part = work_->get(detail::attn_workspace_floats(n_work_, num_q_heads_, cfg.head_dim));
     detail::launch_attn_decode(q, mgr_.layerView(layer_idx, d_slot_), plan, n_, num_q_heads_,
-                               cfg.num_heads, cfg.head_dim, scale, out, part, new_k, new_v, stream);
+                               cfg.num_heads, cfg.head_dim, scale, out, part, new_k, new_v, stream,
+                               inline_ok_ ? inl_.get() : nullptr);
     return Result<void>::ok();
 }
 
@@ -516,6 +531,7 @@ Result<void> DecodeBatch::gather(int layer_idx, half *k_out, half *v_out, int s_
         return Result<void>::err("DecodeBatch: Invalid layer_idx: " + std::to_string(layer_idx));
     if (s_max < 0) return Result<void>::err("DecodeBatch: s_max must be >= 0");
     if (n_ == 0 || s_max == 0) return Result<void>::ok();
+    upload_device(stream);
     const KvView v = mgr_.layerView(layer_idx, d_slot_);
     if (k_out)
         detail::launch_kv_gather(v, 0, d_lens_, 0, n_, cfg.num_heads, cfg.head_dim, s_max, k_out, stream);

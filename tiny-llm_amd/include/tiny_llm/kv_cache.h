@@ -25,6 +25,7 @@ namespace tiny_llm {
 namespace detail {
 struct KvView;
 struct WorkList;
+struct InlineMeta;
 class MetaRing;
 class Workspace;
 } // namespace detail
@@ -137,6 +138,7 @@ class DecodeBatch {
                         hipStream_t stream);
     Result<void> run_attention(int layer_idx, const half *q, const half *new_k, const half *new_v,
                                half *out, float scale, hipStream_t stream);
+    void         upload_device(hipStream_t stream);
 
     KVCacheManager &mgr_;
     int             max_seqs_;
@@ -151,6 +153,9 @@ class DecodeBatch {
     std::unique_ptr<detail::MetaRing>  meta_;
     std::unique_ptr<detail::Workspace> work_;
     std::unique_ptr<detail::WorkList>  plan_;
+    std::unique_ptr<detail::InlineMeta> inl_;
+    bool                               inline_ok_ = false; // metadata fits in kernel arguments
+    bool                               uploaded_ = false;  // device copy of this prepare made
     const int32_t  *d_lens_ = nullptr, *d_wpos_ = nullptr, *d_slot_ = nullptr;
     const int32_t  *d_part_base_ = nullptr, *d_work_ = nullptr;
 };
