@@ -153,6 +153,20 @@ int tl_kv_batch_decode(tl_kv_batch *batch, int layer, const void *q, const void 
  * sequence's attended length are written as +0.0.  Either output may be NULL. */
 int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, int s_max,
                        void *stream);
+/* DecodeBatch projection with the append fused into its epilogue
+ * (transformer.cpp:214-226: w8a16_matmul of wk/wv into k_buf_/v_buf_, then
+ * appendKV(n=1)): for every entry i of the last prepare,
+ *   K_i = x_i @ dequant(wk, sk), V_i = x_i @ dequant(wv, sv)
+ * (W8A16 arithmetic of kernels/w8a16_matmul.cu) are written straight into
+ * the cache of `layer` at the entry's write position -- byte-identical to
+ * tl_w8a16_matmul into a buffer followed by tl_kv_append(n=1).  x:
+ * [n][hidden] fp16; wk/wv: [hidden][num_heads*head_dim] int8; sk/sv:
+ * [ceil(hidden/group_size)][num_heads*head_dim] fp16.  Optionally (wq, sq,
+ * q_out all non-NULL) q_out[n][num_q_heads*head_dim] = x @ dequant(wq, sq) in
+ * the same launch.  Does not advance lengths (commit does). */
+int tl_kv_batch_project(tl_kv_batch *batch, int layer, const void *x, int hidden, int group_size,
+                        const int8_t *wk, const void *sk, const int8_t *wv, const void *sv,
+                        const int8_t *wq, const void *sq, void *q_out, void *stream);
 /* The commit of InferenceEngine::decodeStep (src/inference_engine.cpp:291):
  * advanceSeqLen(seq_id, num_tokens) for every sequence of the last prepare,
  * in batch order; stops at (and reports) the first failing sequence. */
@@ -189,6 +203,24 @@ int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_l
  * Silently returns on non-positive dimensions, like the reference. */
 void tl_attention_decode(const void *q, const void *k, const void *v, void *out, float scale,
                          int batch, int num_heads, int seq_len, int head_dim, void *stream);
+
+/* w8a16_matmul (kernels/w8a16_matmul.cuh:22-26, w8a16_matmul.cu:219-236):
+ * output[M][N] = fp16(input[M][K] @ dequant(weight[K][N] int8,
+ * scales[ceil(K/group_size)][N] fp16)), fp32 accumulation.  Returns TL_OK
+ * without work on non-positive dimensions, like the reference's silent
+ * return.  MFMA path for K % 32 == 0, group_size % 32 == 0, N % 16 == 0 and
+ * 16-byte aligned input/weight; otherwise the reference's per-element order. */
+int tl_w8a16_matmul(const void *input, const int8_t *weight, const void *scales, void *output, int M,
+                    int N, int K, int group_size, void *stream);
+/* o_proj + residual of TransformerLayer::forward (transformer.cpp:149-151,
+ * 246-247; add_inplace of kernels/elementwise.cu:7-14) in one launch:
+ * hidden[M][N] = fp16(f(hidden) + f(fp16(input @ dequant(weight, scales)))). */
+int tl_w8a16_matmul_residual(const void *input, const int8_t *weight, const void *scales,
+                             void *hidden, int M, int N, int K, int group_size, void *stream);
+/* W8A16 kernel selection, process-wide: 0 = normal (MFMA where the shape
+ * allows), 1 = always the reference-order kernel.  No reference counterpart
+ * (test knob). */
+int tl_w8a16_set_path(int path);
 
 /* Score (q.K^T) path of the decode attention kernels, process-wide:
  * 0 = VALU v_dot2 over the loaded K rows, 1 = MFMA v_mfma_f32_16x16x32_f16

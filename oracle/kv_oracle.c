@@ -31,6 +31,16 @@
  *   orc_kv_gather          brute-force element loop in numpy over the same
  *                          view parameters plus the identity
  *                          gather(cache layout) == reshaped reference pool.
+ *   orc_w8a16_matmul       float64 numpy product of the dequantized weights;
+ *                          closed forms (identity weights give x back, all-one
+ *                          data gives sum_g s_g * |group g|, which pins the
+ *                          k / group_size scale row); exact doubling under
+ *                          doubled scales; the reference's own test shapes and
+ *                          its 1% bound against an fp16 matmul of
+ *                          dequantize_weights (tests/test_w8a16_matmul.cu)
+ *                          (tests/test_oracle_w8a16.py).
+ *   orc_add_inplace        elementwise identity checks (x + 0 = x, exact
+ *                          small-integer sums, RNE ties) in the same test.
  * No function is left "parity unpinned" at the 1e-3 / bit-exact bars.  The
  * exact output BITS of the CUDA kernel (warp-tree reduction order, CUDA's expf
  * ULP behaviour) cannot be pinned without running it, which is impossible
@@ -524,3 +534,29 @@ void orc_kv_gather(const orc_kv_view *kv, int which, const int32_t *seq_lens, in
                 }
             }
 }
+
+void orc_w8a16_matmul(const uint16_t *x, const int8_t *w, const uint16_t *s, float *out_f32,
+                      uint16_t *out_f16, int M, int N, int K, int group_size) {
+    if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int m = 0; m < M; ++m) {
+        for (int n = 0; n < N; ++n) {
+            float sum = 0.0f;
+            for (int k = 0; k < K; ++k) {
+                const float a = orc_h2f(x[(size_t)m * K + k]);
+                const float sc = orc_h2f(s[(size_t)(k / group_size) * N + n]);
+                const float wf = (float)w[(size_t)k * N + n] * sc;
+                sum = fmaf(a, wf, sum);
+            }
+            if (out_f32) out_f32[(size_t)m * N + n] = sum;
+            out_f16[(size_t)m * N + n] = orc_f2h(sum);
+        }
+    }
+}
+
+void orc_add_inplace(uint16_t *data, const uint16_t *add, size_t n) {
+    for (size_t i = 0; i < n; ++i) data[i] = orc_f2h(orc_h2f(data[i]) + orc_h2f(add[i]));
+}
+

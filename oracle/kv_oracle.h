@@ -113,6 +113,18 @@ void orc_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *
 
 /* Gather: out[b][g][t][d] = cache(b,g,t,d) for t < seq_lens[b], 0 otherwise.
  * out is [B][Hkv][S_max][D]; which = 0 gathers K, 1 gathers V.             */
+/* ---- W8A16 matmul (kernels/w8a16_matmul.cu:71-98, the reference kernel
+ * that w8a16_matmul also uses for M*N < 4096, :225-228):
+ *   out[m][n] = fp16( sum_k f(x[m][k]) * ((float)w[k][n] * f(s[k/gs][n])) )
+ * summed over k in order in fp32; `sum += a * w` is an FMA under nvcc's
+ * default contraction (--fmad=true), so each step is fmaf(a, w, sum).
+ * Silent no-op on non-positive dimensions (:101-104).  out_f32 may be NULL. */
+void orc_w8a16_matmul(const uint16_t *x, const int8_t *w, const uint16_t *s, float *out_f32,
+                      uint16_t *out_f16, int M, int N, int K, int group_size);
+
+/* add_inplace (kernels/elementwise.cu:7-14): data[i] = fp16(f(data[i]) + f(add[i])). */
+void orc_add_inplace(uint16_t *data, const uint16_t *add, size_t n);
+
 void orc_kv_gather(const orc_kv_view *kv, int which, const int32_t *seq_lens, int B, int Hkv,
                    int D, int S_max, uint16_t *out);
 

@@ -74,6 +74,10 @@ def _declare(L: C.CDLL) -> None:
     L.orc_attn_decode_gqa.argtypes = [vp, C.POINTER(_View), vp, i, i, i, i, C.c_float, vp, vp, i]
     L.orc_attention_decode.argtypes = [vp, vp, vp, vp, vp, C.c_float, i, i, i, i]
     L.orc_kv_gather.argtypes = [C.POINTER(_View), i, vp, i, i, i, i, vp]
+    L.orc_w8a16_matmul.argtypes = [vp, vp, vp, vp, vp, i, i, i, i]
+    L.orc_w8a16_matmul.restype = None
+    L.orc_add_inplace.argtypes = [vp, vp, C.c_size_t]
+    L.orc_add_inplace.restype = None
 
 
 def _ptr(a: np.ndarray | None) -> int | None:
@@ -274,3 +278,24 @@ def gather(view: View, which, seq_lens, Hkv, D, S_max):
     cv = view.c_view()
     lib().orc_kv_gather(C.byref(cv), which, _ptr(lens), B, Hkv, D, S_max, _ptr(out))
     return out
+
+
+def w8a16_matmul(x, w, s, M, N, K, group_size):
+    """Reference-order W8A16 product: x [M][K] fp16 bits, w [K][N] int8,
+    s [ceil(K/gs)][N] fp16 bits -> (out_f32 [M][N], out_f16 bits [M][N])."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    s = np.ascontiguousarray(s, dtype=np.uint16)
+    o32 = np.zeros((M, N), dtype=np.float32)
+    o16 = np.zeros((M, N), dtype=np.uint16)
+    lib().orc_w8a16_matmul(_ptr(x), _ptr(w), _ptr(s), _ptr(o32), _ptr(o16), M, N, K, group_size)
+    return o32, o16
+
+
+def add_inplace(data, add):
+    """data (fp16 bits, modified in place) += add, rounded like add_inplace."""
+    a = np.ascontiguousarray(add, dtype=np.uint16)
+    assert data.flags.c_contiguous and data.dtype == np.uint16 and data.size == a.size
+    lib().orc_add_inplace(_ptr(data), _ptr(a), data.size)
+    return data
+

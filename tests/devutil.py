@@ -43,3 +43,8 @@ def rel_err(a: np.ndarray, b: np.ndarray) -> float:
     b = np.asarray(b, dtype=np.float64)
     mx = max(np.abs(a).max(initial=0.0), np.abs(b).max(initial=0.0))
     return float(np.abs(a - b).max(initial=0.0) / mx) if mx > 0 else 0.0
+
+
+def to_dev_raw(arr: np.ndarray) -> torch.Tensor:
+    """Any numpy array (e.g. int8 weights) to a device tensor of the same bytes."""
+    return torch.from_numpy(np.ascontiguousarray(arr).copy()).to("cuda")

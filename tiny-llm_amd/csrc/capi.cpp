@@ -18,6 +18,9 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
                              int Hq, int Hkv, int D, float scale, __half *out, hipStream_t stream);
 std::string attn_decode_compact(const __half *q, const __half *k, const __half *v, __half *out,
                                 float scale, int B, int H, int S, int D, hipStream_t stream);
+std::string w8a16_call(const __half *x, const int8_t *w, const __half *s, __half *out, int M, int N,
+                       int K, int gs, bool residual, hipStream_t stream);
+void        w8a16_force_generic(int on);
 } // namespace detail
 } // namespace tiny_llm
 
@@ -228,6 +231,17 @@ int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, 
     });
 }
 
+int tl_kv_batch_project(tl_kv_batch *batch, int layer, const void *x, int hidden, int group_size,
+                        const int8_t *wk, const void *sk, const int8_t *wv, const void *sv,
+                        const int8_t *wq, const void *sq, void *q_out, void *stream) {
+    if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_project: null batch");
+    return guarded([&] {
+        return status(batch->b->project(layer, as_half(x), hidden, group_size, wk, as_half(sk), wv,
+                                        as_half(sv), wq, as_half(sq), as_half(q_out),
+                                        as_stream(stream)));
+    });
+}
+
 int tl_kv_batch_commit(tl_kv_batch *batch, int num_tokens) {
     if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_commit: null batch");
     return guarded([&] { return status(batch->b->commit(num_tokens)); });
@@ -253,6 +267,37 @@ int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_l
         g_last_error.clear();
         return TL_OK;
     });
+}
+
+int tl_w8a16_matmul(const void *input, const int8_t *weight, const void *scales, void *output, int M,
+                    int N, int K, int group_size, void *stream) {
+    return guarded([&] {
+        const std::string err = tiny_llm::detail::w8a16_call(as_half(input), weight, as_half(scales),
+                                                             as_half(output), M, N, K, group_size,
+                                                             false, as_stream(stream));
+        if (!err.empty()) return fail(TL_ERR_INVALID, err);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+int tl_w8a16_matmul_residual(const void *input, const int8_t *weight, const void *scales,
+                             void *hidden, int M, int N, int K, int group_size, void *stream) {
+    return guarded([&] {
+        const std::string err = tiny_llm::detail::w8a16_call(as_half(input), weight, as_half(scales),
+                                                             as_half(hidden), M, N, K, group_size,
+                                                             true, as_stream(stream));
+        if (!err.empty()) return fail(TL_ERR_INVALID, err);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+int tl_w8a16_set_path(int path) {
+    if (path != 0 && path != 1) return fail(TL_ERR_INVALID, "tl_w8a16_set_path: path must be 0 or 1");
+    tiny_llm::detail::w8a16_force_generic(path);
+    g_last_error.clear();
+    return TL_OK;
 }
 
 void tl_attention_decode(const void *q, const void *k, const void *v, void *out, float scale,

@@ -902,25 +902,10 @@ int waves_setting() {
     return v;
 }
 
-int device_cus();
-
 int waves_for(int64_t workgroups) {
     const int v = waves_setting();
     if (v) return v;
     return workgroups <= 2 * (int64_t)device_cus() ? 8 : 4;
-}
-
-int device_cus() {
-    static std::atomic<int> cus{0};
-    int                     v = cus.load(std::memory_order_relaxed);
-    if (v == 0) {
-        int dev = 0;
-        HIP_CHECK(hipGetDevice(&dev));
-        HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
-        if (v <= 0) v = 256;
-        cus.store(v);
-    }
-    return v;
 }
 
 } // namespace

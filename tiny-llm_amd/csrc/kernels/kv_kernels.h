@@ -129,6 +129,9 @@ int  score_path();
 void set_waves(int waves);
 int  waves();
 
+// Compute units of the current device (cached per device).
+int device_cus();
+
 // Per-kernel event timing (tl_profile_*).
 enum class KernelId { AttnChunk = 0, AttnMerge = 1, KvAppend = 2, KvGather = 3, Count = 4 };
 void profile_begin(KernelId id, hipStream_t stream);

@@ -9,6 +9,7 @@
 #include "tiny_llm/kv_cache.h"
 
 #include "kernels/kv_kernels.h"
+#include "kernels/w8a16.h"
 #include "runtime.h"
 #include "tiny_llm/logger.h"
 
@@ -344,7 +345,8 @@ KvView KVCacheManager::layerView(int layer_idx, const int32_t *seq_row_dev) cons
 
 DecodeBatch::DecodeBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads)
     : mgr_(mgr), max_seqs_(max_seqs), num_q_heads_(num_q_heads), meta_(new detail::MetaRing(4)),
-      work_(new detail::Workspace()), plan_(new detail::WorkList()),
+      work_(new detail::Workspace()), gemm_work_(new detail::Workspace()),
+      plan_(new detail::WorkList()),
       inl_(new detail::InlineMeta()) {}
 
 DecodeBatch::~DecodeBatch() = default;
@@ -537,6 +539,54 @@ Result<void> DecodeBatch::gather(int layer_idx, half *k_out, half *v_out, int s_
         detail::launch_kv_gather(v, 0, d_lens_, 0, n_, cfg.num_heads, cfg.head_dim, s_max, k_out, stream);
     if (v_out)
         detail::launch_kv_gather(v, 1, d_lens_, 0, n_, cfg.num_heads, cfg.head_dim, s_max, v_out, stream);
+    return Result<void>::ok();
+}
+
+Result<void> DecodeBatch::project(int layer_idx, const half *x, int hidden, int group_size,
+                                  const int8_t *wk, const half *sk, const int8_t *wv,
+                                  const half *sv, const int8_t *wq, const half *sq, half *q_out,
+                                  hipStream_t stream) {
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    if (!appendable_)
+        return Result<void>::err("DecodeBatch: project needs a batch made by prepare()");
+    if (layer_idx < 0 || layer_idx >= cfg.num_layers)
+        return Result<void>::err("DecodeBatch: Invalid layer_idx: " + std::to_string(layer_idx));
+    if (hidden <= 0 || group_size <= 0)
+        return Result<void>::err("DecodeBatch: hidden and group_size must be positive");
+    if (!x || !wk || !sk || !wv || !sv) return Result<void>::err("DecodeBatch: null x or K/V weights");
+    const bool with_q = wq || sq || q_out;
+    if (with_q && (!wq || !sq || !q_out))
+        return Result<void>::err("DecodeBatch: wq, sq and q_out must be all set or all null");
+    if (n_ == 0) return Result<void>::ok();
+    upload_device(stream);
+    const KvView v = mgr_.layerView(layer_idx, d_slot_);
+    detail::CacheRows rows;
+    rows.seq_row = d_slot_;
+    rows.wpos = d_wpos_;
+    rows.block_table = v.block_table;
+    rows.bt_stride = v.bt_stride;
+    rows.log2_blk = v.log2_blk;
+    rows.blk_stride = v.blk_stride;
+    rows.tok_stride = v.tok_stride;
+    const int        row = cfg.num_heads * cfg.head_dim;
+    detail::W8A16Seg segs[3];
+    int              nseg = 0;
+    auto add = [&](const int8_t *w, const half *s, int n, int kind, half *out, int64_t ld) {
+        segs[nseg].w = w;
+        segs[nseg].s = s;
+        segs[nseg].n = n;
+        segs[nseg].kind = kind;
+        segs[nseg].out = out;
+        segs[nseg].ld = ld;
+        ++nseg;
+    };
+    add(wk, sk, row, detail::kEpiCache, const_cast<half *>(v.k_base), 0);
+    add(wv, sv, row, detail::kEpiCache, const_cast<half *>(v.v_base), 0);
+    if (with_q) add(wq, sq, num_q_heads_ * cfg.head_dim, detail::kEpiDense, q_out, num_q_heads_ * cfg.head_dim);
+    float *ws = nullptr;
+    if (const size_t f = detail::w8a16_workspace_floats(n_, hidden, group_size, segs, nseg))
+        ws = gemm_work_->get(f);
+    detail::launch_w8a16(x, hidden, n_, hidden, group_size, segs, nseg, &rows, ws, stream);
     return Result<void>::ok();
 }
 

@@ -66,6 +66,20 @@ int current_device() {
     return d;
 }
 
+int device_cus() {
+    static std::mutex         mu;
+    static std::map<int, int> cus;
+    const int                 dev = current_device();
+    std::lock_guard<std::mutex> lk(mu);
+    auto                      it = cus.find(dev);
+    if (it != cus.end()) return it->second;
+    int v = 0;
+    HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+    if (v <= 0) v = 256;
+    cus[dev] = v;
+    return v;
+}
+
 // ---------------------------------------------------------------- MetaRing
 MetaRing::MetaRing(int slots) : slots_(static_cast<size_t>(slots)) {}
 

@@ -1,0 +1,29 @@
+// W8A16 matrix multiplication (replaces kernels/w8a16_matmul.cuh:22-26).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+namespace tiny_llm {
+namespace kernels {
+
+// output[M][N] = input[M][K] @ dequant(weight[K][N] int8, scales[ceil(K/gs)][N])
+// with fp32 accumulation and fp16 output, like the reference; silently
+// returns when a dimension or group_size is not positive.  MFMA path when
+// K % 32 == 0, group_size % 32 == 0, N % 16 == 0 and the pointers are 16-byte
+// aligned, else a kernel that follows the reference's per-element formula.
+void w8a16_matmul(const half *input, const int8_t *weight, const half *scales, half *output, int M,
+                  int N, int K, int group_size, hipStream_t stream = 0);
+
+// The o_proj + residual step of TransformerLayer::forward
+// (src/transformer.cpp:149-151, 246-247): hidden[M][N] = fp16(f(hidden) +
+// f(fp16(input @ dequant(weight, scales)))), i.e. w8a16_matmul into a
+// temporary followed by add_inplace (kernels/elementwise.cu:7-14), in one
+// launch.
+void w8a16_matmul_residual(const half *input, const int8_t *weight, const half *scales, half *hidden,
+                           int M, int N, int K, int group_size, hipStream_t stream = 0);
+
+} // namespace kernels
+} // namespace tiny_llm

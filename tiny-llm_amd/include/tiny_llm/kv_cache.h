@@ -124,6 +124,18 @@ class DecodeBatch {
     Result<void> decode(int layer_idx, const half *q, const half *new_k, const half *new_v, half *out,
                         float scale, hipStream_t stream);
     Result<void> gather(int layer_idx, half *k_out, half *v_out, int s_max, hipStream_t stream);
+    // The K/V projections of the decode step with the append fused into their
+    // epilogue: for every entry i, K_i = x_i @ dequant(wk, sk) and V_i likewise
+    // (W8A16, kernels/w8a16_matmul.cu) are written straight into the cache at
+    // the entry's write position -- the bytes w8a16_matmul + appendKV(n=1)
+    // leave there (transformer.cpp:214-226), without the k_buf_/v_buf_ round
+    // trip.  x: [n][hidden] fp16; wk/wv: [hidden][num_heads*head_dim] int8;
+    // scales [ceil(hidden/group_size)][num_heads*head_dim].  Optionally also
+    // q_out[n][num_q_heads*head_dim] = x @ dequant(wq, sq) in the same launch
+    // (wq/sq/q_out all null to skip).
+    Result<void> project(int layer_idx, const half *x, int hidden, int group_size, const int8_t *wk,
+                         const half *sk, const int8_t *wv, const half *sv, const int8_t *wq,
+                         const half *sq, half *q_out, hipStream_t stream);
     // advanceSeqLen(seq, num_tokens) for every sequence of the last prepare.
     Result<void> commit(int num_tokens);
 
@@ -152,6 +164,7 @@ class DecodeBatch {
     std::vector<int32_t> ids_, lens_, wpos_, slot_;
     std::unique_ptr<detail::MetaRing>  meta_;
     std::unique_ptr<detail::Workspace> work_;
+    std::unique_ptr<detail::Workspace> gemm_work_;
     std::unique_ptr<detail::WorkList>  plan_;
     std::unique_ptr<detail::InlineMeta> inl_;
     bool                               inline_ok_ = false; // metadata fits in kernel arguments

@@ -100,6 +100,10 @@ def _declare(L: C.CDLL) -> None:
         "tl_kv_batch_decode": (i, [vp, i, vp, vp, vp, vp, f, vp]),
         "tl_kv_batch_gather": (i, [vp, i, vp, vp, i, vp]),
         "tl_kv_batch_commit": (i, [vp, i]),
+        "tl_kv_batch_project": (i, [vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, vp, vp]),
+        "tl_w8a16_matmul": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
+        "tl_w8a16_matmul_residual": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
+        "tl_w8a16_set_path": (i, [i]),
         "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
         "tl_attn_set_score_path": (i, [i]),
@@ -277,6 +281,12 @@ class DecodeBatch:
     def gather(self, layer, k_out, v_out, s_max, stream=0):
         _check(load().tl_kv_batch_gather(self._h, layer, k_out or None, v_out or None, s_max, stream))
 
+    def project(self, layer, x, hidden, group_size, wk, sk, wv, sv, wq=None, sq=None, q_out=None,
+                stream=0):
+        """K/V projections with the append fused (tl_kv_batch_project)."""
+        _check(load().tl_kv_batch_project(self._h, layer, x, hidden, group_size, wk, sk, wv, sv,
+                                          wq or None, sq or None, q_out or None, stream))
+
     def commit(self, num_tokens=1):
         """advanceSeqLen(seq, num_tokens) for every sequence of the last prepare."""
         _check(load().tl_kv_batch_commit(self._h, num_tokens))
@@ -331,3 +341,19 @@ def profile_query(kernel: str):
     ms, n = C.c_double(), C.c_longlong()
     _check(load().tl_profile_query(kernel.encode(), C.byref(ms), C.byref(n)))
     return ms.value, n.value
+
+
+def w8a16_matmul(input, weight, scales, output, M, N, K, group_size, stream=0):
+    """kernels::w8a16_matmul over device pointers."""
+    _check(load().tl_w8a16_matmul(input, weight, scales, output, M, N, K, group_size, stream))
+
+
+def w8a16_matmul_residual(input, weight, scales, hidden, M, N, K, group_size, stream=0):
+    """hidden = fp16(hidden + fp16(input @ dequant(weight, scales))), in place."""
+    _check(load().tl_w8a16_matmul_residual(input, weight, scales, hidden, M, N, K, group_size,
+                                           stream))
+
+
+def w8a16_set_path(path: int):
+    """0 = MFMA where the shape allows, 1 = always the reference-order kernel."""
+    _check(load().tl_w8a16_set_path(path))
