@@ -45,6 +45,10 @@ def parse():
                     help="timed steps (default: 100 for configs 2-4, 1000 for config 5)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5))
+    ap.add_argument("--path", default="decode", choices=("decode", "project", "oproj"),
+                    help="decode: append + attention (the headline); project: the decode step's "
+                         "fused QKV W8A16 projection writing K/V into the cache; oproj: the W8A16 "
+                         "o_proj + residual (Llama-3-8B layer shapes, batch 64)")
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -346,6 +350,105 @@ def churn(args, tl, torch, workloads, np):
                 kpass_desc=f"second run of the same {K}-step event sequence")
 
 
+def gemm_bench(args, tl, torch, np):
+    """W8A16 projection kernels at Llama-3-8B layer shapes (hidden 4096, 32 q /
+    8 kv heads, head_dim 128, group 128) for a decode batch of 64.  Weights of
+    16 layers rotate, so that every call streams its weights from HBM (16 x 25
+    MB > the 256 MB MALL).  project: one launch computes Q into a buffer and K/V
+    straight into the cache at each sequence's write position; oproj: hidden +=
+    fp16(attn_out @ W_o)."""
+    B, hidden, Hq, Hkv, D, gs, sets = 64, 4096, 32, 8, 128, 128, 16
+    K = args.steps or 100
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261201 + 7)
+
+    def weights(n):
+        """int8 weights in the MFMA-fragment layout (packed once, as an engine
+        would at load time) and their fp16 group scales."""
+        w = torch.randint(-128, 128, (hidden, n), generator=gen, device=dev, dtype=torch.int8)
+        wp = torch.empty_like(w)
+        tl.w8a16_pack(w.data_ptr(), hidden, n, wp.data_ptr(), stream)
+        sc = (torch.rand(((hidden + gs - 1) // gs, n), generator=gen, device=dev) * 0.02 + 1e-3).half()
+        return wp, sc
+    x = torch.randn((B, hidden), generator=gen, device=dev, dtype=torch.float16)
+    if args.path == "project":
+        nq, nkv = Hq * D, Hkv * D
+        W = [(weights(nq), weights(nkv), weights(nkv)) for _ in range(sets)]
+        M = ((16 + K + args.warmup + 10 + 63) // 64) * 64
+        mgr = tl.KVCacheManager(1, Hkv, D, M, B)
+        ids = [mgr.allocateSequence(M)[0] for _ in range(B)]
+        q_out = torch.empty((B, nq), device=dev, dtype=torch.float16)
+        batch = tl.DecodeBatch(mgr, B, Hq)
+
+        def call(i):
+            (wq, sq), (wk, sk), (wv, sv) = W[i % sets]
+            batch.prepare(ids, stream)
+            batch.project(0, x.data_ptr(), hidden, gs, wk.data_ptr(), sk.data_ptr(), wv.data_ptr(),
+                          sv.data_ptr(), wq.data_ptr(), sq.data_ptr(), q_out.data_ptr(), stream,
+                          packed=True)
+            batch.commit(1)
+        n_out = nq + 2 * nkv
+        nbytes = hidden * n_out + ((hidden + gs - 1) // gs) * n_out * 2 + B * hidden * 2 + B * n_out * 2
+        desc = "fused QKV projection: q -> buffer, K/V rows -> cache at the write position"
+    else:
+        W = [weights(hidden) for _ in range(sets)]
+        h = torch.randn((B, hidden), generator=gen, device=dev, dtype=torch.float16)
+        n_out = hidden
+
+        def call(i):
+            w, sc = W[i % sets]
+            tl.w8a16_matmul_residual(x.data_ptr(), w.data_ptr(), sc.data_ptr(), h.data_ptr(), B,
+                                     hidden, hidden, gs, stream, packed=True)
+        nbytes = hidden * hidden + ((hidden + gs - 1) // gs) * hidden * 2 + B * hidden * 2 + 2 * B * hidden * 2
+        desc = "o_proj + residual: hidden += fp16(attn_out @ W_o)"
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    ev0.record()
+    for i in range(K):
+        call(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms = ev0.elapsed_time(ev1) / K
+    tl.profile_reset()
+    tl.profile_enable(True)
+    for i in range(min(K, 32)):
+        call(i)
+    torch.cuda.synchronize()
+    tl.profile_enable(False)
+    g_ms, g_n = tl.profile_query("w8a16")
+    r_ms, r_n = tl.profile_query("w8a16_reduce")
+    tl.profile_reset()
+    g_avg = g_ms / max(1, g_n)
+    r_avg = r_ms / max(1, r_n)
+    flops = 2.0 * B * hidden * n_out
+    kern_ms = g_avg + r_avg
+    gbps = nbytes / (kern_ms * 1e-3) / 1e9
+    return {
+        "metric": f"W8A16 {args.path} µs/call and achieved HBM GB/s, Llama-3-8B layer, batch 64",
+        "value": round(nbytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16 x int8",
+        "data": "synthetic: x ~ N(0,1), int8 weights uniform (packed layout), scales U(0.001, "
+                "0.021) (torch, seeded)",
+        "config": {"workload": f"llama3_8b_{args.path}_b64", "batch": B, "hidden": hidden,
+                   "out_columns": n_out, "group_size": gs, "weight_sets": sets, "what": desc},
+        "kernels_us": {"w8a16": round(g_avg * 1e3, 2), "w8a16_reduce": round(r_avg * 1e3, 2)},
+        "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
+        "roofline": {"kernel": "w8a16_mfma_kernel + w8a16_reduce_kernel", "bound": "hbm",
+                     "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "tflops": round(flops / (kern_ms * 1e-3) / 1e12, 2),
+                     "bytes_per_call": nbytes},
+        "cpu_baseline": None,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -367,6 +470,9 @@ def main():
     import workloads
 
     torch.cuda.set_device(0)
+    if args.path != "decode":
+        print(json.dumps(gemm_bench(args, tl, torch, np)), flush=True)
+        return
     r = churn(args, tl, torch, workloads, np) if args.config == 5 else \
         fixed_batch(args, tl, torch, workloads, np)
     K, conf = r["K"], r["conf"]

@@ -163,10 +163,12 @@ int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, 
  * [n][hidden] fp16; wk/wv: [hidden][num_heads*head_dim] int8; sk/sv:
  * [ceil(hidden/group_size)][num_heads*head_dim] fp16.  Optionally (wq, sq,
  * q_out all non-NULL) q_out[n][num_q_heads*head_dim] = x @ dequant(wq, sq) in
- * the same launch.  Does not advance lengths (commit does). */
+ * the same launch.  packed != 0: all weights are in the layout of
+ * tl_w8a16_pack (the fast path; hidden % 32 == 0 and group_size in
+ * {32, 64, 128, 256, 512}).  Does not advance lengths (commit does). */
 int tl_kv_batch_project(tl_kv_batch *batch, int layer, const void *x, int hidden, int group_size,
                         const int8_t *wk, const void *sk, const int8_t *wv, const void *sv,
-                        const int8_t *wq, const void *sq, void *q_out, void *stream);
+                        const int8_t *wq, const void *sq, void *q_out, int packed, void *stream);
 /* The commit of InferenceEngine::decodeStep (src/inference_engine.cpp:291):
  * advanceSeqLen(seq_id, num_tokens) for every sequence of the last prepare,
  * in batch order; stops at (and reports) the first failing sequence. */
@@ -208,15 +210,26 @@ void tl_attention_decode(const void *q, const void *k, const void *v, void *out,
  * output[M][N] = fp16(input[M][K] @ dequant(weight[K][N] int8,
  * scales[ceil(K/group_size)][N] fp16)), fp32 accumulation.  Returns TL_OK
  * without work on non-positive dimensions, like the reference's silent
- * return.  MFMA path for K % 32 == 0, group_size % 32 == 0, N % 16 == 0 and
+ * return.  MFMA path for K % 32 == 0, group_size in {32, 64, 128, 256, 512}, N % 16 == 0 and
  * 16-byte aligned input/weight; otherwise the reference's per-element order. */
 int tl_w8a16_matmul(const void *input, const int8_t *weight, const void *scales, void *output, int M,
                     int N, int K, int group_size, void *stream);
 /* o_proj + residual of TransformerLayer::forward (transformer.cpp:149-151,
  * 246-247; add_inplace of kernels/elementwise.cu:7-14) in one launch:
- * hidden[M][N] = fp16(f(hidden) + f(fp16(input @ dequant(weight, scales)))). */
+ * hidden[M][N] = fp16(f(hidden) + f(fp16(input @ dequant(weight, scales)))).
+ * packed != 0: weight is in the layout of tl_w8a16_pack. */
 int tl_w8a16_matmul_residual(const void *input, const int8_t *weight, const void *scales,
-                             void *hidden, int M, int N, int K, int group_size, void *stream);
+                             void *hidden, int M, int N, int K, int group_size, int packed,
+                             void *stream);
+/* One-time repack of a W8A16 weight [K][N] int8 (K % 32 == 0, N % 16 == 0)
+ * into the layout the packed entry points read (K*N bytes, device to device,
+ * stream-ordered): for column block nb = n/16 and k step ks = k/32, the 512
+ * bytes at ((nb*K/32 + ks)*64) * 8 hold, for lane l = 0..63, rows
+ * 32ks + 8(l/16) .. +7 of column 16nb + l%16 -- the B fragment of
+ * v_mfma_f32_16x16x32_f16, so the kernel streams weights straight into MFMA
+ * operands.  No reference counterpart (weights are static; an engine packs
+ * them once at load, like model_loader.cpp's quantised tensors). */
+int tl_w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, void *stream);
 /* W8A16 kernel selection, process-wide: 0 = normal (MFMA where the shape
  * allows), 1 = always the reference-order kernel.  No reference counterpart
  * (test knob). */
@@ -246,7 +259,8 @@ int tl_attn_get_waves(void);
  * Kernel timing (the reference has only an unused CudaEvent wrapper,
  * include/tiny_llm/cuda_streams.h:67-99).  When enabled, every launch of the
  * named kernels is bracketed by hipEvents on its own stream.
- * Names: "attn_chunk", "attn_merge", "kv_append", "kv_gather".
+ * Names: "attn_chunk", "attn_merge", "kv_append", "kv_gather", "w8a16"
+ * (the W8A16 GEMM kernel), "w8a16_reduce" (its split-K reduction).
  * ---------------------------------------------------------------------- */
 void tl_profile_enable(int on);
 void tl_profile_reset(void);

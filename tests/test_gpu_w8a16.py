@@ -38,6 +38,9 @@ SHAPES = [  # (M, N, K, gs, mfma-eligible)
     (17, 48, 96, 32, True),        # partial row tile, 16-column tail, K % 64 == 32
     (100, 80, 256, 64, True),      # two row tiles
     (300, 32, 512, 128, True),     # M > 256: no split-K
+    (17, 48, 96, 64, True),        # K % 64 == 32 with a partial last scale group
+    (5, 32, 160, 128, True),
+    (9, 64, 1056, 256, True),      # several batches, the last one short
     (4, 8, 16, 8, False),          # the reference's test shapes (reference-order kernel)
     (17, 33, 65, 32, False),
     (64, 1, 128, 32, False),
@@ -71,10 +74,47 @@ def test_w8a16_reference_order_kernel_is_bit_exact(tl, orc, generic, M, N, K, gs
     assert np.array_equal(to_host(out), ref16)
 
 
-@pytest.mark.parametrize("path", [0, 1])
+def pack_np(w):
+    """The packed layout, restated in numpy: fragment (nb, ks) = 64 lanes x 8
+    bytes, lane l holding rows 32ks + 8(l/16) .. +7 of column 16nb + l%16."""
+    K, N = w.shape
+    out = np.empty((N // 16, K // 32, 64, 8), np.int8)
+    lanes = np.arange(64)
+    for nb in range(N // 16):
+        for ks in range(K // 32):
+            rows = 32 * ks + 8 * (lanes // 16)[:, None] + np.arange(8)[None, :]
+            out[nb, ks] = w[rows, 16 * nb + (lanes % 16)[:, None]]
+    return out.reshape(-1)
+
+
+def test_w8a16_pack_layout(tl, orc):
+    rng = np.random.default_rng(3)
+    K, N = 128, 48
+    w = rng.integers(-128, 128, size=(K, N), dtype=np.int64).astype(np.int8)
+    dw = to_dev_raw(w)
+    out = to_dev_raw(np.zeros(K * N, np.int8))
+    tl.w8a16_pack(dw.data_ptr(), K, N, out.data_ptr(), stream())
+    import torch
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), pack_np(w))
+    with pytest.raises(tl.TinyLLMError, match="multiple"):
+        tl.w8a16_pack(dw.data_ptr(), 100, N, out.data_ptr(), stream())
+
+
+def packed_dev(tl, w):
+    K, N = w.shape
+    dw = to_dev_raw(w)
+    out = to_dev_raw(np.zeros(K * N, np.int8))
+    tl.w8a16_pack(dw.data_ptr(), K, N, out.data_ptr(), stream())
+    return out
+
+
+@pytest.mark.parametrize("path", [0, 1, 2])
 def test_w8a16_residual(tl, orc, generic, path):
-    """hidden = fp16(hidden + fp16(x @ W)) (transformer.cpp:149-151, 246-247)."""
-    generic(path)
+    """hidden = fp16(hidden + fp16(x @ W)) (transformer.cpp:149-151, 246-247);
+    path 0: MFMA on the reference layout, 1: reference-order kernel, 2: MFMA
+    on packed weights (bit-identical to path 0)."""
+    generic(1 if path == 1 else 0)
     M, N, K, gs = 64, 512, 4096, 128
     rng = np.random.default_rng(11)
     x, w, s = operands(orc, rng, M, N, K, gs)
@@ -91,6 +131,11 @@ def test_w8a16_residual(tl, orc, generic, path):
     else:
         ref32 = orc.h2f(hidden) + o32
         assert rows_close(got, ref32) <= TOL
+    if path == 2:
+        dp, dh2 = packed_dev(tl, w), to_dev(hidden)
+        tl.w8a16_matmul_residual(dx.data_ptr(), dp.data_ptr(), ds.data_ptr(), dh2.data_ptr(), M, N, K,
+                                 gs, stream(), packed=True)
+        assert np.array_equal(to_host(dh2), got)
 
 
 def test_w8a16_nonpositive_dims_noop(tl):
@@ -123,11 +168,13 @@ def _cache(tl, orc, rng, L, Hkv, D, M, lens, paged):
     return g, o, ids, keep
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("paged", [False, True])
-def test_project_fused_append(tl, orc, paged):
+def test_project_fused_append(tl, orc, paged, packed):
     """Fused projection: cache bytes == w8a16_matmul + appendKV(n=1) (bit-exact,
     whole pool), K/V rows within 1e-3 of the oracle, q_out == w8a16_matmul of
-    wq (bit-exact), and attention afterwards == decode() with the same rows."""
+    wq (bit-exact), and attention afterwards == decode() with the same rows.
+    With packed weights the same bytes as the reference-layout path."""
     rng = np.random.default_rng(21 + paged)
     L, Hkv, G, D, hidden, gs = 2, 4, 4, 64, 512, 128
     Hq, row = Hkv * G, Hkv * D
@@ -147,8 +194,14 @@ def test_project_fused_append(tl, orc, paged):
     batch = tl.DecodeBatch(g, B, Hq)
     batch.prepare(ids, stream())
     q_out = empty_dev((B, Hq * D))
-    batch.project(layer, dx.data_ptr(), hidden, gs, dwk.data_ptr(), dsk.data_ptr(), dwv.data_ptr(),
-                  dsv.data_ptr(), dwq.data_ptr(), dsq.data_ptr(), q_out.data_ptr(), stream())
+    if packed:
+        pk, pv, pq = packed_dev(tl, wk), packed_dev(tl, wv), packed_dev(tl, wq)
+        batch.project(layer, dx.data_ptr(), hidden, gs, pk.data_ptr(), dsk.data_ptr(), pv.data_ptr(),
+                      dsv.data_ptr(), pq.data_ptr(), dsq.data_ptr(), q_out.data_ptr(), stream(),
+                      packed=True)
+    else:
+        batch.project(layer, dx.data_ptr(), hidden, gs, dwk.data_ptr(), dsk.data_ptr(), dwv.data_ptr(),
+                      dsv.data_ptr(), dwq.data_ptr(), dsq.data_ptr(), q_out.data_ptr(), stream())
     # unfused: w8a16_matmul into buffers, then batched appendKV(n=1) of layer 1
     kb, vb, qb = empty_dev((B, row)), empty_dev((B, row)), empty_dev((B, Hq * D))
     for w_, s_, out_, n_ in ((dwk, dsk, kb, row), (dwv, dsv, vb, row), (dwq, dsq, qb, Hq * D)):

@@ -19,7 +19,8 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
 std::string attn_decode_compact(const __half *q, const __half *k, const __half *v, __half *out,
                                 float scale, int B, int H, int S, int D, hipStream_t stream);
 std::string w8a16_call(const __half *x, const int8_t *w, const __half *s, __half *out, int M, int N,
-                       int K, int gs, bool residual, hipStream_t stream);
+                       int K, int gs, bool residual, hipStream_t stream, bool packed);
+std::string w8a16_pack_call(const int8_t *w, int K, int N, int8_t *out, hipStream_t stream);
 void        w8a16_force_generic(int on);
 } // namespace detail
 } // namespace tiny_llm
@@ -233,12 +234,12 @@ int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, 
 
 int tl_kv_batch_project(tl_kv_batch *batch, int layer, const void *x, int hidden, int group_size,
                         const int8_t *wk, const void *sk, const int8_t *wv, const void *sv,
-                        const int8_t *wq, const void *sq, void *q_out, void *stream) {
+                        const int8_t *wq, const void *sq, void *q_out, int packed, void *stream) {
     if (!batch) return fail(TL_ERR_INVALID, "tl_kv_batch_project: null batch");
     return guarded([&] {
         return status(batch->b->project(layer, as_half(x), hidden, group_size, wk, as_half(sk), wv,
                                         as_half(sv), wq, as_half(sq), as_half(q_out),
-                                        as_stream(stream)));
+                                        as_stream(stream), packed != 0));
     });
 }
 
@@ -274,7 +275,7 @@ int tl_w8a16_matmul(const void *input, const int8_t *weight, const void *scales,
     return guarded([&] {
         const std::string err = tiny_llm::detail::w8a16_call(as_half(input), weight, as_half(scales),
                                                              as_half(output), M, N, K, group_size,
-                                                             false, as_stream(stream));
+                                                             false, as_stream(stream), false);
         if (!err.empty()) return fail(TL_ERR_INVALID, err);
         g_last_error.clear();
         return TL_OK;
@@ -282,11 +283,22 @@ int tl_w8a16_matmul(const void *input, const int8_t *weight, const void *scales,
 }
 
 int tl_w8a16_matmul_residual(const void *input, const int8_t *weight, const void *scales,
-                             void *hidden, int M, int N, int K, int group_size, void *stream) {
+                             void *hidden, int M, int N, int K, int group_size, int packed,
+                             void *stream) {
     return guarded([&] {
         const std::string err = tiny_llm::detail::w8a16_call(as_half(input), weight, as_half(scales),
                                                              as_half(hidden), M, N, K, group_size,
-                                                             true, as_stream(stream));
+                                                             true, as_stream(stream), packed != 0);
+        if (!err.empty()) return fail(TL_ERR_INVALID, err);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+int tl_w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, void *stream) {
+    return guarded([&] {
+        const std::string err =
+            tiny_llm::detail::w8a16_pack_call(weight, K, N, packed, as_stream(stream));
         if (!err.empty()) return fail(TL_ERR_INVALID, err);
         g_last_error.clear();
         return TL_OK;
@@ -338,9 +350,10 @@ void tl_profile_enable(int on) { tiny_llm::detail::profile_set(on != 0); }
 void tl_profile_reset(void) { tiny_llm::detail::profile_reset(); }
 
 int tl_profile_query(const char *kernel, double *total_ms, long long *launches) {
-    static const char *names[] = {"attn_chunk", "attn_merge", "kv_append", "kv_gather"};
+    static const char *names[] = {"attn_chunk", "attn_merge", "kv_append", "kv_gather", "w8a16",
+                                  "w8a16_reduce"};
     if (!kernel || !total_ms || !launches) return fail(TL_ERR_INVALID, "tl_profile_query: null argument");
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 6; ++i)
         if (std::strcmp(kernel, names[i]) == 0)
             return guarded([&] {
                 tiny_llm::detail::profile_query(i, total_ms, launches);

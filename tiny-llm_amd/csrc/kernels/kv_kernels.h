@@ -133,7 +133,15 @@ int  waves();
 int device_cus();
 
 // Per-kernel event timing (tl_profile_*).
-enum class KernelId { AttnChunk = 0, AttnMerge = 1, KvAppend = 2, KvGather = 3, Count = 4 };
+enum class KernelId {
+    AttnChunk = 0,
+    AttnMerge = 1,
+    KvAppend = 2,
+    KvGather = 3,
+    W8A16 = 4,       // main GEMM kernel (either path)
+    W8A16Reduce = 5, // split-K reduction + epilogue
+    Count = 6
+};
 void profile_begin(KernelId id, hipStream_t stream);
 void profile_end(KernelId id, hipStream_t stream);
 

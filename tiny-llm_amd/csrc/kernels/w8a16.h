@@ -37,7 +37,8 @@ struct CacheRows {
     int64_t        tok_stride = 0;
 };
 
-// True when the MFMA path covers the shape (K % 32 == 0, gs % 32 == 0, every
+// True when the MFMA path covers the shape (K % 32 == 0, gs a power of two in
+// [32, 512], every
 // segment's n % 16 == 0); other shapes take the reference-order kernel.
 bool w8a16_mfma_ok(int K, int gs, const W8A16Seg *segs, int nseg);
 
@@ -47,8 +48,15 @@ size_t w8a16_workspace_floats(int M, int K, int gs, const W8A16Seg *segs, int ns
 // out = x @ dequant(W_i, s_i) for each segment i, with its epilogue.  x [M][K]
 // fp16 at row pitch ldx; all pointers device; 16-byte alignment of x, W and
 // the row pitches (x: ldx % 8 == 0) is the caller's check.
+// packed: every segment's w is in the layout of launch_w8a16_pack (MFMA
+// path only; shapes it does not cover are rejected).
 void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A16Seg *segs, int nseg,
-                  const CacheRows *cache, float *workspace, hipStream_t stream);
+                  const CacheRows *cache, float *workspace, hipStream_t stream, bool packed = false);
+
+// W [K][N] int8 -> the MFMA-fragment layout (K % 32 == 0, N % 16 == 0; K*N
+// bytes): fragment (column block nb, k step ks) holds, for lane l, rows
+// 32ks + 8(l/16) .. +7 of column 16nb + l%16 as 8 contiguous bytes.
+void launch_w8a16_pack(const int8_t *w, int K, int N, int8_t *out, hipStream_t stream);
 
 // 1: every launch takes the reference-order kernel; 0 / -1: normal selection.
 void w8a16_force_generic(int on);

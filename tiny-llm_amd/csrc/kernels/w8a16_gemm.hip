@@ -4,22 +4,24 @@
 // with an fp32 accumulator, W [K][N] int8 row-major, scales
 // [ceil(K/gs)][N] fp16.
 //
-// MFMA path (K % 32 == 0, gs % 32 == 0, every segment's N % 16 == 0):
-//   One workgroup = 2 waves = a 64-row x 32-column output tile over one split
+// MFMA path (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
+// N % 16 == 0):
+//   One workgroup = 4 waves = a 64-row x 64-column output tile over one split
 //   of K (split-K across workgroups when the tiles alone would leave CUs
 //   idle).  Per 64-row K chunk:
 //     - the x chunk [64 rows][64 k] fp16 is loaded cooperatively and staged in
 //       LDS (row-major, padded), read back in the A layout of
 //       v_mfma_f32_16x16x32_f16 (lane l: row l%16, k 8*(l/16)..+7);
-//     - each wave loads its 16 columns of the W chunk (lane l: row l, 16
-//       bytes), converts the int8 values to fp16 (exact) and stores them
-//       transposed ([column][k]) in LDS, read back in the B layout (lane l:
-//       column l%16, k 8*(l/16)..+7);
+//     - the W chunk [64 k][64 columns] int8 is loaded cooperatively as
+//       dwords (4 rows x 4 columns per thread), transposed in registers,
+//       converted to fp16 (exact) and stored [column][k] in LDS, read back in
+//       the B layout (lane l: column l%16, k 8*(l/16)..+7); wave w owns
+//       columns 16w..16w+15;
 //     - two 32-deep k steps of MFMA on the integer weights; at the end of each
 //       scale group the group's partial product is folded into the fp32
-//       accumulator with its scale: acc += P_g * s[g][n] (gs % 32 == 0 keeps a
-//       k step inside one group).
-//   The next chunk's global loads are issued before the current chunk's MFMA.
+//       accumulator with its scale: acc += P_g * s[g][n] (a k step never
+//       straddles groups, and the fold points are compile-time constants).
+//   The loads of up to 8 chunks are issued before the first is consumed.
 //   With one split the workgroup applies the epilogue directly; otherwise it
 //   writes fp32 partials and w8a16_reduce_kernel sums the splits in a fixed
 //   order (deterministic) and applies the epilogue.  The split count depends
@@ -53,12 +55,13 @@ namespace detail {
 namespace {
 
 constexpr int kBM = 64;       // rows per workgroup
-constexpr int kBN = 32;       // columns per workgroup (16 per wave)
+constexpr int kBN = 64;       // columns per workgroup (16 per wave)
 constexpr int kBK = 64;       // k rows per chunk
-constexpr int kWaves = 2;
+constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kRing = 8;      // chunks whose loads are issued together
 constexpr int kXPitch = kBK + 8; // halves per staged x row (16-byte pad)
-constexpr int kWPitch = kBK + 8; // halves per staged transposed W column
+constexpr int kWPitch = kBK + 8; // halves per staged transposed W column (16-byte rows)
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
@@ -70,6 +73,9 @@ struct GemmArgs {
     int           nseg;
     int           splits;
     int           chunks_per_split; // 64-row chunks of K per split
+    int           tiles;            // column tiles over all segments
+    int           mtiles;           // row tiles
+    int           units;            // column-tile pairs x splits x row tiles
     float        *partial;          // [splits][M][ntot] when splits > 1
     int           ntot;
     W8A16Seg      seg[kMaxSegs];
@@ -103,47 +109,109 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, int si, int m, int n
     }
 }
 
+// Byte transpose of a 4x4 block: d[r] holds columns 0..3 of row r; returns
+// c[j] = (row 0..3 of column j).
+__device__ __forceinline__ void transpose4x4(const uint32_t (&d)[4], uint32_t (&c)[4]) {
+    const uint32_t lo01 = __builtin_amdgcn_perm(d[1], d[0], 0x05010400u); // r0c0 r1c0 r0c1 r1c1
+    const uint32_t hi01 = __builtin_amdgcn_perm(d[1], d[0], 0x07030602u); // r0c2 r1c2 r0c3 r1c3
+    const uint32_t lo23 = __builtin_amdgcn_perm(d[3], d[2], 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(d[3], d[2], 0x07030602u);
+    c[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+    c[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+    c[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+    c[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Four signed bytes -> four fp16 (exact), packed for one 8-byte LDS store.
+// u = b + 128 (b ^ 0x80) placed in the mantissa of 0x6400 (1024.0) is the
+// fp16 value 1024 + u; subtracting 1152 leaves b exactly.
+__device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t v) {
+    const uint32_t u = v ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u); // [u0 64 u1 64]
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x05030402u); // [u2 64 u3 64]
+    const f16x2    bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) + bias),
+                      __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) + bias));
+}
+
+// Workgroup (4 waves, 256 threads) -> (64-row tile, 64-column tile, K split).
+// Grid layout: the two column tiles of a pair (which share the 128-byte
+// lines of every weight row) get block indices 8 apart, i.e. the same XCD
+// under the round-robin dispatch of workgroups to XCDs, so each line is read
+// from HBM into one L2 once.  K is processed in batches of kRing 64-row
+// chunks; a batch starts on a multiple of 512 rows, so with GS | 512 its scale
+// groups are fixed at compile time: the batch's scales (one per lane and
+// group), W (four dwords per thread per chunk: rows 4*(t/16)..+3, columns
+// 4*(t%16)..+3) and x (two 16-byte pieces per thread per chunk) are all
+// issued before the first chunk is consumed, and the partial product of each
+// group is folded into the accumulator at a static point.  Per chunk: W is
+// transposed in registers (v_perm), converted to fp16 and stored [column][k]
+// with 8-byte LDS writes, x is staged with 16-byte writes, then two 32-deep
+// MFMA k-steps per 16-row block.
+template <int GS, bool PACKED>
 __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
-    __shared__ __align__(16) _Float16 xs[kBM * kXPitch];
-    __shared__ __align__(16) _Float16 wt[kWaves][16 * kWPitch];
+    static_assert(GS % 32 == 0 && (kRing * kBK) % GS == 0, "group size");
+    constexpr int SPG = GS / 32;                 // k steps per scale group
+    constexpr int NG = kRing * kBK / GS;         // scale groups per batch
+    // Double-buffered staging: chunk j uses buffer j & 1, so one barrier per
+    // chunk suffices (a buffer is rewritten two chunks later, after every
+    // wave has passed the intervening barrier, i.e. finished reading it).
+    __shared__ __align__(16) _Float16 xs[2][kBM * kXPitch];
+    __shared__ __align__(16) _Float16 wt[2][kBN * kWPitch];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    // tile -> segment, columns
-    int tile = blockIdx.x;
+    const int t = threadIdx.x;
+    // block -> (unit, half); unit -> (pair, split, m tile)
+    const int b = blockIdx.x;
+    const int unit = (b >> 4) * 8 + (b & 7);
+    const int half = (b >> 3) & 1;
+    if (unit >= a.units) return;
+    const int mt = unit % a.mtiles;
+    const int rest = unit / a.mtiles;
+    const int split = rest % a.splits;
+    const int pair = rest / a.splits;
+    int       tile = 2 * pair + half;
+    if (tile >= a.tiles) return;
     int si = 0;
     while (si + 1 < a.nseg && tile >= (a.seg[si].n + kBN - 1) / kBN) {
         tile -= (a.seg[si].n + kBN - 1) / kBN;
         ++si;
     }
     const W8A16Seg &sg = a.seg[si];
-    const int       n0 = tile * kBN + 16 * wave; // this wave's first column in the segment
+    const int       c0 = tile * kBN;     // first column of the workgroup in the segment
+    const int       n0 = c0 + 16 * wave; // this wave's first column
     const bool      wave_live = n0 < sg.n;
-    const int       m0 = blockIdx.y * kBM;
-    const int       split = blockIdx.z;
-    const int       kchunks = a.K / kBK + (a.K % kBK ? 1 : 0);
-    const int       c_begin = split * a.chunks_per_split;
+    const int       m0 = mt * kBM;
+    const int       kchunks = (a.K + kBK - 1) / kBK;
+    const int       c_begin = split * a.chunks_per_split; // a multiple of kRing
     const int       c_end = min(kchunks, c_begin + a.chunks_per_split);
+    const int       ngroups = (a.K + GS - 1) / GS;
 
-    // Global loads of one chunk: x (kXPer x 16 B per thread: 64 rows x 128 B),
-    // W (16 B per lane: row k0 + lane, the wave's 16 columns).
-    constexpr int kXPer = kBM * kBK / 8 / kThreads;
-    auto load_chunk = [&](int c, uint4(&xv)[kXPer], uint4 &wv) __attribute__((always_inline)) {
-        const int k0 = c * kBK;
+    // Loads are never masked: every address is clamped into the operand, and
+    // what a clamped element feeds is either discarded (output columns >= n,
+    // rows >= M) or skipped (k steps >= K, a uniform branch), so no load
+    // ends up in a divergent branch with a wait right behind it.
+    const int     wq = 4 * (t & 15); // W column quad (within the tile)
+    const int     wr = 4 * (t >> 4); // W row quad (within the chunk)
+    const int     wcol = min(c0 + wq, sg.n - 4);
+    const int8_t *wbase = sg.w + (int64_t)wr * sg.n + wcol;
+    const int64_t wchunk = (int64_t)kBK * sg.n;
+    const int     ksteps = a.K >> 5;
+    const int8_t *pbase = sg.w + ((int64_t)(min(n0, sg.n - 16) >> 4) * ksteps * 64 + lane) * 8;
+    const __half *xrow[2];
+    int           xk[2];
 #pragma unroll
-        for (int u = 0; u < kXPer; ++u) {
-            const int q = threadIdx.x + kThreads * u;
-            const int r = q >> 3, kp = q & 7;
-            const int m = m0 + r, k = k0 + 8 * kp;
-            xv[u] = (m < a.M && k < a.K)
-                        ? *reinterpret_cast<const uint4 *>(a.x + (int64_t)m * a.ldx + k)
-                        : make_uint4(0u, 0u, 0u, 0u);
-        }
-        const int k = k0 + lane;
-        wv = (wave_live && k < a.K)
-                 ? *reinterpret_cast<const uint4 *>(sg.w + (int64_t)k * sg.n + n0)
-                 : make_uint4(0u, 0u, 0u, 0u);
-    };
+    for (int u = 0; u < 2; ++u) {
+        const int q = t + kThreads * u;
+        const int r = q >> 3, kp = q & 7;
+        xrow[u] = a.x + (int64_t)min(m0 + r, a.M - 1) * a.ldx;
+        xk[u] = 8 * kp;
+    }
+    const int     ncol = n0 + (lane & 15); // this lane's output column (D layout)
+    const __half *sbase = sg.s + min(ncol, sg.n - 1);
 
     f32x4 acc[4], P[4];
 #pragma unroll
@@ -151,66 +219,112 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
         acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    int   gcur = -1;
-    float scur = 0.0f;
-    const int ncol = n0 + (lane & 15); // this lane's output column (D layout)
-    auto fold = [&]() __attribute__((always_inline)) {
+
+    for (int cb = c_begin; cb < c_end; cb += kRing) {
+        // Every load below is unconditional, from an address that is valid
+        // whether or not the element is (masked elements read element 0 and
+        // are zeroed afterwards), so no load sits in a divergent branch and
+        // the waits are deferred to the first use.
+        const int g0 = cb * kBK / GS; // first scale group of the batch
+        uint16_t  sraw[NG];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int i = 0; i < NG; ++i)
+            sraw[i] = *reinterpret_cast<const uint16_t *>(sbase + (int64_t)min(g0 + i, ngroups - 1) * sg.n);
+        // W of all kRing chunks in flight at once (HBM); x (L2-resident) one
+        // chunk ahead.
+        uint32_t wbuf[kRing][4]; // reference layout: rows wr..wr+3 x columns wq..wq+3
+        uint2    wpk[kRing][2];  // packed layout: the wave's B fragment of k steps 2c, 2c+1
+        uint4    xbuf[2][2];
+        auto     load_x = [&](int j, uint4(&xv)[2]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(P[rb][i], scur, acc[rb][i]);
-            P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    };
-    // Stage chunk c from (xv, wv), prefetch chunk c + 1 into (xn, wn), multiply.
-    auto body = [&](int c, const uint4(&xv)[kXPer], const uint4 &wv, uint4(&xn)[kXPer],
-                    uint4 &wn) __attribute__((always_inline)) {
+            for (int u = 0; u < 2; ++u)
+                xv[u] = *reinterpret_cast<const uint4 *>(xrow[u] + min((cb + j) * kBK + xk[u], a.K - 8));
+        };
 #pragma unroll
-        for (int u = 0; u < kXPer; ++u) {
-            const int q = threadIdx.x + kThreads * u;
-            const int r = q >> 3, kp = q & 7;
-            *reinterpret_cast<uint4 *>(&xs[r * kXPitch + 8 * kp]) = xv[u];
-        }
-        {
-            const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
-            _Float16      *dst = &wt[wave][lane];
+        for (int j = 0; j < kRing; ++j) {
+            const int c = min(cb + j, kchunks - 1);
+            if constexpr (PACKED) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int8_t v = (int8_t)((wd[j >> 2] >> (8 * (j & 3))) & 0xffu);
-                dst[j * kWPitch] = (_Float16)v;
+                for (int ks = 0; ks < 2; ++ks)
+                    wpk[j][ks] = *reinterpret_cast<const uint2 *>(pbase + (int64_t)min(2 * c + ks, ksteps - 1) * 512);
+            } else {
+                const int8_t *wp = wbase + (int64_t)c * wchunk;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    wbuf[j][i] = *reinterpret_cast<const uint32_t *>(
+                        wp + (int64_t)min(i, a.K - 1 - c * kBK - wr) * sg.n); // row <= K - 1
             }
         }
-        __syncthreads();
-        if (c + 1 < c_end) load_chunk(c + 1, xn, wn); // in flight during the MFMAs
+        load_x(0, xbuf[0]);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int k0 = c * kBK + 32 * ks;
-            if (k0 >= a.K) break;
-            const int g = k0 / a.gs;
-            if (g != gcur) {
-                if (gcur >= 0) fold();
-                gcur = g;
-                scur = wave_live ? h2f(sg.s[(int64_t)g * sg.n + ncol]) : 0.0f;
+        for (int j = 0; j < kRing; ++j) {
+            const int c = cb + j;
+            if (c >= c_end) break; // uniform; zero steps add nothing, groups folded below
+            if (j + 1 < kRing) load_x(j + 1, xbuf[(j + 1) & 1]);
+            _Float16 *xsb = xs[j & 1];
+            _Float16 *wtb = wt[j & 1];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int q = t + kThreads * u;
+                const int r = q >> 3, kp = q & 7;
+                *reinterpret_cast<uint4 *>(&xsb[r * kXPitch + 8 * kp]) = xbuf[j & 1][u];
             }
-            const f16x8 bop = *reinterpret_cast<const f16x8 *>(
-                &wt[wave][(lane & 15) * kWPitch + 32 * ks + 8 * (lane >> 4)]);
+            if constexpr (!PACKED) {
+                uint32_t col[4];
+                transpose4x4(wbuf[j], col);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    *reinterpret_cast<uint2 *>(&wtb[(wq + jj) * kWPitch + wr]) = i8x4_to_f16x4(col[jj]);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                if (32 * (2 * c + ks) >= a.K) break; // uniform: the half chunk beyond K (K % 64 == 32)
+                f16x8 bop;
+                if constexpr (PACKED) {
+                    const uint2 lo = i8x4_to_f16x4(wpk[j][ks].x), hi = i8x4_to_f16x4(wpk[j][ks].y);
+                    bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                } else {
+                    bop = *reinterpret_cast<const f16x8 *>(
+                        &wtb[(16 * wave + (lane & 15)) * kWPitch + 32 * ks + 8 * (lane >> 4)]);
+                }
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    const f16x8 aop = *reinterpret_cast<const f16x8 *>(
+                        &xsb[(16 * rb + (lane & 15)) * kXPitch + 32 * ks + 8 * (lane >> 4)]);
+                    P[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, P[rb], 0, 0, 0);
+                }
+                const int step = 2 * j + ks; // static
+                if ((step + 1) % SPG == 0) { // end of scale group step / SPG
+                    const float s_ = h2f(__builtin_bit_cast(__half, sraw[step / SPG])) *
+                                     (g0 + step / SPG < ngroups ? 1.0f : 0.0f);
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(P[rb][i], s_, acc[rb][i]);
+                        P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                }
+            }
+        }
+        __syncthreads(); // the next batch restages both buffers
+        // A batch cut short inside a group (K % GS != 0): fold the rest with
+        // that group's scale.  Steps executed: those of the batch's chunks
+        // that lie below K.
+        const int done_steps = min(2 * min(kRing, c_end - cb), ksteps - 2 * cb);
+        if (done_steps % SPG) {
+            float s_ = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NG; ++i)
+                s_ = (i == done_steps / SPG && g0 + i < ngroups) ? h2f(__builtin_bit_cast(__half, sraw[i])) : s_;
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
-                const f16x8 aop = *reinterpret_cast<const f16x8 *>(
-                    &xs[(16 * rb + (lane & 15)) * kXPitch + 32 * ks + 8 * (lane >> 4)]);
-                P[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, P[rb], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(P[rb][i], s_, acc[rb][i]);
+                P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
         }
-        __syncthreads(); // xs / wt are restaged by the next chunk
-    };
-
-    uint4 xa[kXPer], xb[kXPer], wa, wb;
-    if (c_begin < c_end) load_chunk(c_begin, xa, wa);
-    for (int c = c_begin; c < c_end; c += 2) {
-        body(c, xa, wa, xb, wb);
-        if (c + 1 < c_end) body(c + 1, xb, wb, xa, wa);
     }
-    if (gcur >= 0) fold();
     if (!wave_live) return;
 
     // D layout: lane holds rows 16*rb + 4*(lane/16) + i, column lane%16.
@@ -227,6 +341,29 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
             }
         }
     }
+}
+
+// Repacks W [K][N] int8 (K % 32 == 0, N % 16 == 0) so that the B fragment of
+// v_mfma_f32_16x16x32_f16 for column block nb and k step ks is 512
+// contiguous bytes: packed[((nb * K/32 + ks) * 64 + l) * 8 + j] =
+// W[32 ks + 8 (l / 16) + j][16 nb + l % 16].  One thread per (nb, ks, l).
+__global__ __launch_bounds__(256) void w8a16_pack_kernel(const int8_t *w, int K, int N, int8_t *out) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)(N / 16) * (K / 32) * 64;
+    if (idx >= total) return;
+    const int     l = (int)(idx & 63);
+    const int64_t frag = idx >> 6;
+    const int     ks = (int)(frag % (K / 32));
+    const int     nb = (int)(frag / (K / 32));
+    const int     col = 16 * nb + (l & 15);
+    const int     k0 = 32 * ks + 8 * (l >> 4);
+    uint32_t      lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lo |= (uint32_t)(uint8_t)w[(int64_t)(k0 + j) * N + col] << (8 * j);
+        hi |= (uint32_t)(uint8_t)w[(int64_t)(k0 + 4 + j) * N + col] << (8 * j);
+    }
+    *reinterpret_cast<uint2 *>(out + idx * 8) = make_uint2(lo, hi);
 }
 
 // Sums the split-K partials in split order and applies the epilogue.
@@ -266,7 +403,7 @@ int g_force_generic = -1;
 } // namespace
 
 bool w8a16_mfma_ok(int K, int gs, const W8A16Seg *segs, int nseg) {
-    if (K % 32 != 0 || gs % 32 != 0) return false;
+    if (K % 32 != 0 || (gs != 32 && gs != 64 && gs != 128 && gs != 256 && gs != 512)) return false;
     for (int i = 0; i < nseg; ++i)
         if (segs[i].n % 16 != 0) return false;
     return true;
@@ -277,12 +414,15 @@ namespace {
 // launch -- so that every output element is summed in the same order whether
 // its weight matrix is multiplied alone or fused with others (the fused
 // projection's cache bytes equal the unfused path's).  Decode-sized M splits K
-// into up to 8 ranges of >= 1024 rows for parallelism; larger M has enough
-// row tiles.  Sets the 64-row chunks per split.
+// into up to 8 ranges of >= 512 rows (at most kRing chunks each for K <= 4096,
+// so a split's loads are all in flight together); larger M has enough row
+// tiles.  Sets the 64-row chunks per split.
 int split_plan(int M, int K, int *chunks_per_split) {
     const int kchunks = (K + kBK - 1) / kBK;
-    int       splits = M <= 256 ? std::min(8, std::max(1, K / 1024)) : 1;
-    const int cps = (kchunks + splits - 1) / splits;
+    int       splits = M <= 256 ? std::min(8, std::max(1, K / 512)) : 1;
+    // chunks per split: a multiple of kRing, so that every batch starts on a
+    // 512-row (scale-group) boundary
+    const int cps = ((kchunks + splits - 1) / splits + kRing - 1) / kRing * kRing;
     if (chunks_per_split) *chunks_per_split = cps;
     return (kchunks + cps - 1) / cps;
 }
@@ -297,7 +437,7 @@ size_t w8a16_workspace_floats(int M, int K, int gs, const W8A16Seg *segs, int ns
 }
 
 void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A16Seg *segs, int nseg,
-                  const CacheRows *cache, float *workspace, hipStream_t stream) {
+                  const CacheRows *cache, float *workspace, hipStream_t stream, bool packed) {
     if (nseg < 1 || nseg > kMaxSegs) throw std::invalid_argument("w8a16: 1..3 weight segments");
     GemmArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -320,32 +460,68 @@ void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A1
     if (cache) a.cache = *cache;
     bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && ldx % 8 == 0;
     for (int i = 0; i < nseg; ++i) aligned &= (reinterpret_cast<uintptr_t>(segs[i].w) & 15u) == 0;
-    const bool mfma = g_force_generic != 1 && aligned && w8a16_mfma_ok(K, gs, segs, nseg);
+    const bool mfma = packed || (g_force_generic != 1 && aligned && w8a16_mfma_ok(K, gs, segs, nseg));
+    if (packed && !w8a16_mfma_ok(K, gs, segs, nseg))
+        throw std::invalid_argument("w8a16: packed weights need K % 32 == 0, N % 16 == 0 and a "
+                                    "group size in {32, 64, 128, 256, 512}");
+    if (packed && !aligned) throw std::invalid_argument("w8a16: x and weights must be 16-byte aligned");
     if (!mfma) {
         a.splits = 1;
         const int64_t total = (int64_t)M * a.ntot;
+        profile_begin(KernelId::W8A16, stream);
         hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                            stream, a);
         HIP_CHECK(hipGetLastError());
+        profile_end(KernelId::W8A16, stream);
         return;
     }
     const int mt = (M + kBM - 1) / kBM;
     const int splits = split_plan(M, K, &a.chunks_per_split);
     a.splits = splits;
+    a.tiles = tiles;
+    a.mtiles = mt;
+    a.units = (tiles + 1) / 2 * splits * mt;
     a.partial = splits > 1 ? workspace : nullptr;
     if (splits > 1 && !workspace) throw std::invalid_argument("w8a16: split-K needs a workspace");
-    hipLaunchKernelGGL(w8a16_mfma_kernel, dim3((unsigned)tiles, (unsigned)mt, (unsigned)splits),
-                       dim3(kThreads), 0, stream, a);
+    const unsigned blocks = (unsigned)((a.units + 7) / 8 * 16); // pairs of 8-block groups
+    profile_begin(KernelId::W8A16, stream);
+#define TL_W8_LAUNCH(G)                                                                             \
+    do {                                                                                            \
+        if (packed)                                                                                 \
+            hipLaunchKernelGGL((w8a16_mfma_kernel<G, true>), dim3(blocks), dim3(kThreads), 0, stream, a);  \
+        else                                                                                        \
+            hipLaunchKernelGGL((w8a16_mfma_kernel<G, false>), dim3(blocks), dim3(kThreads), 0, stream, a); \
+    } while (0)
+    switch (gs) {
+    case 32: TL_W8_LAUNCH(32); break;
+    case 64: TL_W8_LAUNCH(64); break;
+    case 128: TL_W8_LAUNCH(128); break;
+    case 256: TL_W8_LAUNCH(256); break;
+    default: TL_W8_LAUNCH(512); break;
+    }
+#undef TL_W8_LAUNCH
     HIP_CHECK(hipGetLastError());
+    profile_end(KernelId::W8A16, stream);
     if (splits > 1) {
         const int64_t total = (int64_t)M * a.ntot;
+        profile_begin(KernelId::W8A16Reduce, stream);
         hipLaunchKernelGGL(w8a16_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                            stream, a);
         HIP_CHECK(hipGetLastError());
+        profile_end(KernelId::W8A16Reduce, stream);
     }
 }
 
 void w8a16_force_generic(int on) { g_force_generic = on; }
+
+void launch_w8a16_pack(const int8_t *w, int K, int N, int8_t *out, hipStream_t stream) {
+    if (K % 32 != 0 || N % 16 != 0 || K <= 0 || N <= 0)
+        throw std::invalid_argument("w8a16_pack: K must be a positive multiple of 32 and N of 16");
+    const int64_t total = (int64_t)(N / 16) * (K / 32) * 64;
+    hipLaunchKernelGGL(w8a16_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, w,
+                       K, N, out);
+    HIP_CHECK(hipGetLastError());
+}
 
 } // namespace detail
 } // namespace tiny_llm

@@ -545,7 +545,7 @@ Result<void> DecodeBatch::gather(int layer_idx, half *k_out, half *v_out, int s_
 Result<void> DecodeBatch::project(int layer_idx, const half *x, int hidden, int group_size,
                                   const int8_t *wk, const half *sk, const int8_t *wv,
                                   const half *sv, const int8_t *wq, const half *sq, half *q_out,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, bool packed) {
     const KVCacheConfig &cfg = mgr_.getConfig();
     if (!appendable_)
         return Result<void>::err("DecodeBatch: project needs a batch made by prepare()");
@@ -586,7 +586,10 @@ Result<void> DecodeBatch::project(int layer_idx, const half *x, int hidden, int 
     float *ws = nullptr;
     if (const size_t f = detail::w8a16_workspace_floats(n_, hidden, group_size, segs, nseg))
         ws = gemm_work_->get(f);
-    detail::launch_w8a16(x, hidden, n_, hidden, group_size, segs, nseg, &rows, ws, stream);
+    if (packed && !detail::w8a16_mfma_ok(hidden, group_size, segs, nseg))
+        return Result<void>::err("DecodeBatch: packed weights need hidden % 32 == 0 and group_size "
+                                 "in {32, 64, 128, 256, 512}");
+    detail::launch_w8a16(x, hidden, n_, hidden, group_size, segs, nseg, &rows, ws, stream, packed);
     return Result<void>::ok();
 }
 

@@ -172,8 +172,8 @@ namespace {
 struct ProfState {
     std::mutex                                          mu;
     std::atomic<bool>                                   on{false};
-    std::array<std::vector<std::pair<hipEvent_t, hipEvent_t>>, 4> done;
-    std::array<hipEvent_t, 4>                           open{};
+    std::array<std::vector<std::pair<hipEvent_t, hipEvent_t>>, static_cast<size_t>(KernelId::Count)> done;
+    std::array<hipEvent_t, static_cast<size_t>(KernelId::Count)> open{};
 };
 ProfState &prof() {
     static ProfState p;
@@ -224,7 +224,7 @@ void profile_reset() {
 }
 
 bool profile_query(int id, double *total_ms, long long *launches) {
-    if (id < 0 || id >= 4) return false;
+    if (id < 0 || id >= static_cast<int>(KernelId::Count)) return false;
     ProfState                  &p = prof();
     std::lock_guard<std::mutex> lk(p.mu);
     double                      tot = 0.0;

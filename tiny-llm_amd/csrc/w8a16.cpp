@@ -17,7 +17,7 @@ namespace tiny_llm {
 namespace detail {
 
 std::string w8a16_call(const __half *x, const int8_t *w, const __half *s, __half *out, int M, int N,
-                       int K, int gs, bool residual, hipStream_t stream) {
+                       int K, int gs, bool residual, hipStream_t stream, bool packed) {
     if (M <= 0 || N <= 0 || K <= 0 || gs <= 0) return ""; // reference: silent no-op
     if (!x || !w || !s || !out) return "w8a16_matmul: null pointer argument";
     W8A16Seg seg;
@@ -33,7 +33,18 @@ std::string w8a16_call(const __half *x, const int8_t *w, const __half *s, __half
     ctx.claim(stream);
     float *ws = nullptr;
     if (const size_t f = w8a16_workspace_floats(M, K, gs, &seg, 1)) ws = ctx.ws.get(f);
-    launch_w8a16(x, K, M, K, gs, &seg, 1, nullptr, ws, stream);
+    if (packed && !w8a16_mfma_ok(K, gs, &seg, 1))
+        return "w8a16_matmul: packed weights need K % 32 == 0, N % 16 == 0 and group_size in "
+               "{32, 64, 128, 256, 512}";
+    launch_w8a16(x, K, M, K, gs, &seg, 1, nullptr, ws, stream, packed);
+    return "";
+}
+
+std::string w8a16_pack_call(const int8_t *w, int K, int N, int8_t *out, hipStream_t stream) {
+    if (!w || !out) return "w8a16_pack: null pointer argument";
+    if (K <= 0 || N <= 0 || K % 32 != 0 || N % 16 != 0)
+        return "w8a16_pack: K must be a positive multiple of 32 and N of 16";
+    launch_w8a16_pack(w, K, N, out, stream);
     return "";
 }
 
@@ -45,7 +56,8 @@ void w8a16_matmul(const half *input, const int8_t *weight, const half *scales, h
                   int N, int K, int group_size, hipStream_t stream) {
     std::string err;
     try {
-        err = detail::w8a16_call(input, weight, scales, output, M, N, K, group_size, false, stream);
+        err = detail::w8a16_call(input, weight, scales, output, M, N, K, group_size, false, stream,
+                                 false);
     } catch (const std::exception &e) {
         err = e.what();
     }
@@ -53,10 +65,21 @@ void w8a16_matmul(const half *input, const int8_t *weight, const half *scales, h
 }
 
 void w8a16_matmul_residual(const half *input, const int8_t *weight, const half *scales, half *hidden,
-                           int M, int N, int K, int group_size, hipStream_t stream) {
+                           int M, int N, int K, int group_size, hipStream_t stream, bool packed) {
     std::string err;
     try {
-        err = detail::w8a16_call(input, weight, scales, hidden, M, N, K, group_size, true, stream);
+        err = detail::w8a16_call(input, weight, scales, hidden, M, N, K, group_size, true, stream,
+                                 packed);
+    } catch (const std::exception &e) {
+        err = e.what();
+    }
+    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+}
+
+void w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, hipStream_t stream) {
+    std::string err;
+    try {
+        err = detail::w8a16_pack_call(weight, K, N, packed, stream);
     } catch (const std::exception &e) {
         err = e.what();
     }

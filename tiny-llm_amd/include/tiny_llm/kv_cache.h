@@ -132,10 +132,11 @@ class DecodeBatch {
     // trip.  x: [n][hidden] fp16; wk/wv: [hidden][num_heads*head_dim] int8;
     // scales [ceil(hidden/group_size)][num_heads*head_dim].  Optionally also
     // q_out[n][num_q_heads*head_dim] = x @ dequant(wq, sq) in the same launch
-    // (wq/sq/q_out all null to skip).
+    // (wq/sq/q_out all null to skip).  packed: the weights are in the layout
+    // of kernels::w8a16_pack.
     Result<void> project(int layer_idx, const half *x, int hidden, int group_size, const int8_t *wk,
                          const half *sk, const int8_t *wv, const half *sv, const int8_t *wq,
-                         const half *sq, half *q_out, hipStream_t stream);
+                         const half *sq, half *q_out, hipStream_t stream, bool packed = false);
     // advanceSeqLen(seq, num_tokens) for every sequence of the last prepare.
     Result<void> commit(int num_tokens);
 

@@ -100,9 +100,10 @@ def _declare(L: C.CDLL) -> None:
         "tl_kv_batch_decode": (i, [vp, i, vp, vp, vp, vp, f, vp]),
         "tl_kv_batch_gather": (i, [vp, i, vp, vp, i, vp]),
         "tl_kv_batch_commit": (i, [vp, i]),
-        "tl_kv_batch_project": (i, [vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, vp, vp]),
+        "tl_kv_batch_project": (i, [vp, i, vp, i, i, vp, vp, vp, vp, vp, vp, vp, i, vp]),
+        "tl_w8a16_pack": (i, [vp, i, i, vp, vp]),
         "tl_w8a16_matmul": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
-        "tl_w8a16_matmul_residual": (i, [vp, vp, vp, vp, i, i, i, i, vp]),
+        "tl_w8a16_matmul_residual": (i, [vp, vp, vp, vp, i, i, i, i, i, vp]),
         "tl_w8a16_set_path": (i, [i]),
         "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
@@ -282,10 +283,10 @@ class DecodeBatch:
         _check(load().tl_kv_batch_gather(self._h, layer, k_out or None, v_out or None, s_max, stream))
 
     def project(self, layer, x, hidden, group_size, wk, sk, wv, sv, wq=None, sq=None, q_out=None,
-                stream=0):
+                stream=0, packed=False):
         """K/V projections with the append fused (tl_kv_batch_project)."""
         _check(load().tl_kv_batch_project(self._h, layer, x, hidden, group_size, wk, sk, wv, sv,
-                                          wq or None, sq or None, q_out or None, stream))
+                                          wq or None, sq or None, q_out or None, int(packed), stream))
 
     def commit(self, num_tokens=1):
         """advanceSeqLen(seq, num_tokens) for every sequence of the last prepare."""
@@ -348,10 +349,16 @@ def w8a16_matmul(input, weight, scales, output, M, N, K, group_size, stream=0):
     _check(load().tl_w8a16_matmul(input, weight, scales, output, M, N, K, group_size, stream))
 
 
-def w8a16_matmul_residual(input, weight, scales, hidden, M, N, K, group_size, stream=0):
+def w8a16_matmul_residual(input, weight, scales, hidden, M, N, K, group_size, stream=0,
+                          packed=False):
     """hidden = fp16(hidden + fp16(input @ dequant(weight, scales))), in place."""
     _check(load().tl_w8a16_matmul_residual(input, weight, scales, hidden, M, N, K, group_size,
-                                           stream))
+                                           int(packed), stream))
+
+
+def w8a16_pack(weight, K, N, packed, stream=0):
+    """Repack weight [K][N] int8 into the MFMA-fragment layout (K*N bytes)."""
+    _check(load().tl_w8a16_pack(weight, K, N, packed, stream))
 
 
 def w8a16_set_path(path: int):
