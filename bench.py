@@ -56,6 +56,12 @@ def parse():
     ap.add_argument("--q-heads", type=int, default=0,
                     help="override the number of query heads of configs 2-4 (64 on config 3 "
                          "gives the group-8 head shape of config 5 at batch 64 / context 8192)")
+    ap.add_argument("--alloc", default="slots", choices=("slots", "blocks"),
+                    help="pool of configs 2, 3 and 5: slots = the reference's full-length slot "
+                         "per sequence; blocks = blocks handed out as sequences grow")
+    ap.add_argument("--block-tokens", type=int, default=16, help="tokens per block of --alloc blocks")
+    ap.add_argument("--kv-gib", type=float, default=0.0,
+                    help="config 5: HBM budget of the KV pool in GiB (default: 1280 full slots)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run one device-to-device copy of this many MiB (HBM counter "
                          "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) and exit")
@@ -166,7 +172,13 @@ def fixed_batch(args, tl, torch, workloads, np):
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream().cuda_stream
 
-    mgr = tl.KVCacheManager(L, Hkv, D, M, B)
+    blocks = args.alloc == "blocks" and not bt
+    if blocks:  # every sequence's blocks, in the order the prefill and steps take them
+        bb = args.block_tokens
+        need = int(((ctx + K + args.warmup + 1 + bb - 1) // bb).sum())
+        mgr = tl.KVCacheManager(L, Hkv, D, M, B, block_tokens=bb, num_blocks=need)
+    else:
+        mgr = tl.KVCacheManager(L, Hkv, D, M, B)
     if bt:  # config 4: 16-token blocks behind a seeded random permutation
         perm = workloads.block_permutation(B * M // bt, workloads.seed(cfg.cfg, 4))
         assert mgr.setBlockMap(bt, perm) is None
@@ -230,14 +242,18 @@ def fixed_batch(args, tl, torch, workloads, np):
     tl.profile_reset()
     lens_k = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int64)
 
-    total_bytes = sum(workloads.step_bytes(lens0 + i, Hq, Hkv, D, layers=L, paged_block=bt)
+    total_bytes = sum(workloads.step_bytes(lens0 + i, Hq, Hkv, D, layers=L,
+                                           paged_block=bt or (args.block_tokens if blocks else 0))
                       for i in range(K))
     attn_bytes = workloads.attention_bytes(lens_k, Hq, Hkv, D)
-    if bt:
-        attn_bytes += 4 * B + 4 * int(((lens_k + 1 + bt - 1) // bt).sum())
+    if bt or blocks:
+        b_ = bt or args.block_tokens
+        attn_bytes += 4 * B + 4 * int(((lens_k + 1 + b_ - 1) // b_).sum())
     conf = {"workload": cfg.name, "layers": L, "batch": B, "q_heads": Hq, "kv_heads": Hkv,
             "head_dim": D, "context_first": int(lens0.min()), "context_max_first": int(lens0.max()),
-            "context_sum_first": int(lens0.sum()), "block_tokens": bt, "kv_std": cfg.kv_std,
+            "context_sum_first": int(lens0.sum()),
+            "block_tokens": args.block_tokens if blocks else bt, "kv_std": cfg.kv_std,
+            "alloc": "blocks" if blocks else ("permuted blocks" if bt else "full-length slots"),
             "chunk_tokens": info["chunk_tokens"], "work_items": info["work_items"],
             "parallelism": "single GPU"}
     data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) (torch.randn, seeded), prefilled "
@@ -255,7 +271,14 @@ def churn(args, tl, torch, workloads, np):
     timed without hooks, once with per-launch hipEvents."""
     K = args.steps or 1000
     sim_args = dict(steps=K)
-    Hq, Hkv, D, M, slots = 64, 8, 128, 5120, 1280
+    Hq, Hkv, D, M, slots, bt = 64, 8, 128, 5120, 1280, args.block_tokens
+    slot_bytes = M * Hkv * D * 2 * 2
+    budget = int(args.kv_gib * (1 << 30)) if args.kv_gib else slots * slot_bytes
+    blocks = args.alloc == "blocks"
+    if blocks:
+        nblocks = budget // (bt * Hkv * D * 2 * 2)
+    else:
+        slots = min(slots, budget // slot_bytes)
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream().cuda_stream
     gen = torch.Generator(device=dev)
@@ -267,7 +290,10 @@ def churn(args, tl, torch, workloads, np):
     nv = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
     out = torch.empty((slots, Hq, D), device=dev, dtype=torch.float16)
     scale = 1.0 / float(np.sqrt(D))
-    mgr = tl.KVCacheManager(1, Hkv, D, M, slots)
+    if blocks:
+        mgr = tl.KVCacheManager(1, Hkv, D, M, slots, block_tokens=bt, num_blocks=nblocks)
+    else:
+        mgr = tl.KVCacheManager(1, Hkv, D, M, slots)
     batch = tl.DecodeBatch(mgr, slots, Hq)
 
     def run(profile):
@@ -275,6 +301,7 @@ def churn(args, tl, torch, workloads, np):
         live = {}    # seq id -> remaining decode steps
         length = {}  # seq id -> getSeqLen, tracked on the host side of the loop
         nbytes, attn_nbytes, rejected, live_sum, peak = 0, 0, 0, 0, 0
+        preempted, used_sum, arrival = 0, 0, {}  # arrival: seq id -> admission order
         if profile:
             tl.profile_reset()
             tl.profile_enable(True)
@@ -285,14 +312,31 @@ def churn(args, tl, torch, workloads, np):
         for ev in sim.events():
             for prompt, life in zip(ev.arrivals, ev.lifetimes):
                 sid, err = mgr.allocateSequence(M)
+                if err is None and blocks and mgr.freeBlocks() < -(-prompt // bt) + len(live):
+                    mgr.releaseSequence(sid)  # admit only with a block of headroom per live seq
+                    err = "exhausted"
                 if err is not None:
                     rejected += 1
                     continue
                 assert mgr.appendKV(sid, 0, src_k.data_ptr(), src_v.data_ptr(), prompt, stream) is None
                 mgr.advanceSeqLen(sid, prompt)
+                arrival[sid] = len(arrival)
                 nbytes += 2 * prompt * Hkv * D * 2 * 2  # read + write of K and V
                 live[sid] = max(1, life)
                 length[sid] = prompt
+            if blocks:
+                # A step opens a block for every sequence at a block boundary;
+                # when the pool cannot back them, the newest sequences are
+                # preempted (released) first.
+                need = sum(1 for s in live if length[s] % bt == 0)
+                while need > mgr.freeBlocks() and live:
+                    s = max(live, key=arrival.__getitem__)
+                    need -= 1 if length[s] % bt == 0 else 0
+                    del live[s]
+                    del length[s]
+                    assert mgr.releaseSequence(s) is None
+                    preempted += 1
+            used_sum += mgr.getUsedMemory()
             ids = list(live)
             if ids:
                 batch.prepare(ids, stream)
@@ -324,6 +368,7 @@ def churn(args, tl, torch, workloads, np):
             ks = kernel_stats(tl)
             tl.profile_reset()
         return dict(ms=ms, wall=wall, nbytes=nbytes, attn_nbytes=attn_nbytes, rejected=rejected,
+                    preempted=preempted, used_avg=used_sum / sim.steps,
                     live_avg=live_sum / sim.steps,
                     live_peak=peak, ks=ks)
 
@@ -337,11 +382,16 @@ def churn(args, tl, torch, workloads, np):
     # algorithmic bytes of the average attention launch (fused append
     # included, prompt appends excluded) over the profiled pass
     launches = max(1, ks["attn_chunk"][1])
-    conf = {"workload": "cfg5_churn_g8", "layers": 1, "q_heads": Hq, "kv_heads": Hkv,
+    conf = {"workload": "cfg5_churn_g8" + ("_blocks" if blocks else ""), "layers": 1, "q_heads": Hq, "kv_heads": Hkv,
             "head_dim": D, "max_seq_len": M, "slots": slots, "arrivals_per_step": 2.0,
             "prompt": "U{256..4096}", "lifetime": "geometric(1/512)",
             "live_avg": round(timed["live_avg"], 1), "live_peak": timed["live_peak"],
-            "rejected": timed["rejected"], "parallelism": "single GPU"}
+            "rejected": timed["rejected"], "parallelism": "single GPU",
+            "alloc": f"blocks of {bt} tokens" if blocks else "full-length slots",
+            "kv_pool_gib": round(budget / (1 << 30), 2),
+            "kv_used_avg_gib": round(timed["used_avg"] / (1 << 30), 2)}
+    if blocks:
+        conf["preempted"] = timed["preempted"]
     return dict(cfg=None, K=K, elapsed_ms=timed["ms"], t_wall=timed["wall"],
                 total_bytes=timed["nbytes"], attn_bytes=prof["attn_nbytes"] / launches, ks=ks,
                 kpass=K, conf=conf,

@@ -102,6 +102,28 @@ int tl_kv_slot_of(const tl_kv_manager *mgr, int seq_id);
  * perm == NULL restores the reference layout. */
 int tl_kv_set_block_map(tl_kv_manager *mgr, int block_tokens, const int32_t *perm, size_t n);
 
+/* Block-granular pool (build addition; replaces the full-slot reservation
+ * of allocateSequence, kv_cache.cpp:91-119).  The pool holds num_blocks
+ * blocks of block_tokens tokens (a power of two >= 16), each with every
+ * layer's K and V of those tokens, plus one spare block that unmapped table
+ * entries point to:
+ *   [layer][K|V][num_blocks + 1][block_tokens][num_heads][head_dim]  fp16.
+ * max_batch_size bounds the live sequences.  tl_kv_append, tl_kv_advance and
+ * tl_kv_batch_prepare map the blocks they need (all or nothing per call) and
+ * fail with "KV cache exhausted" when too few are free; release returns a
+ * sequence's blocks.  Used/total/free memory count blocks of
+ * tl_kv_block_bytes.  tl_kv_get_cache fails (no contiguous region). */
+int tl_kv_create_paged(const tl_kv_config *cfg, int block_tokens, int num_blocks,
+                       tl_kv_manager **out);
+/* Blocks in the pool / free now (0 for other pools). */
+int    tl_kv_num_blocks(const tl_kv_manager *mgr);
+int    tl_kv_free_blocks(const tl_kv_manager *mgr);
+/* Bytes of one block (all layers, K and V); 0 for other pools. */
+size_t tl_kv_block_bytes(const tl_kv_manager *mgr);
+/* Physical blocks of a sequence in token order: writes min(*n, mapped) ids
+ * to out and sets *n to the number mapped. */
+int tl_kv_block_table(const tl_kv_manager *mgr, int seq_id, int32_t *out, int *n);
+
 /* ------------------------------------------------------------------------
  * Batched decode surface (build addition layered on the manager).  The
  * reference decodes one sequence per call: TransformerLayer::attention

@@ -8,6 +8,7 @@
 #include "tiny_llm/kv_cache.h"
 #include "tiny_llm/logger.h"
 
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -158,6 +159,44 @@ int tl_kv_get_config(const tl_kv_manager *mgr, tl_kv_config *out) {
 void  *tl_kv_pool(const tl_kv_manager *mgr) { return mgr ? mgr->m->pool() : nullptr; }
 size_t tl_kv_slot_bytes(const tl_kv_manager *mgr) { return mgr ? mgr->m->slotBytes() : 0; }
 int    tl_kv_slot_of(const tl_kv_manager *mgr, int seq_id) { return mgr ? mgr->m->slotOf(seq_id) : -1; }
+
+int tl_kv_create_paged(const tl_kv_config *cfg, int block_tokens, int num_blocks,
+                       tl_kv_manager **out) {
+    if (!out) return fail(TL_ERR_INVALID, "tl_kv_create_paged: out is null");
+    *out = nullptr;
+    if (!cfg) return fail(TL_ERR_INVALID, "tl_kv_create_paged: cfg is null");
+    return guarded([&] {
+        tiny_llm::KVCacheConfig c;
+        c.num_layers = cfg->num_layers;
+        c.num_heads = cfg->num_heads;
+        c.head_dim = cfg->head_dim;
+        c.max_seq_len = cfg->max_seq_len;
+        c.max_batch_size = cfg->max_batch_size;
+        auto r = KVCacheManager::createPaged(c, block_tokens, num_blocks);
+        if (r.isErr()) return fail(TL_ERR_INVALID, r.error());
+        *out = new tl_kv_manager{std::move(r.value())};
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+int    tl_kv_num_blocks(const tl_kv_manager *mgr) { return mgr ? mgr->m->numBlocks() : 0; }
+int    tl_kv_free_blocks(const tl_kv_manager *mgr) { return mgr ? mgr->m->freeBlocks() : 0; }
+size_t tl_kv_block_bytes(const tl_kv_manager *mgr) { return mgr ? mgr->m->blockBytes() : 0; }
+
+int tl_kv_block_table(const tl_kv_manager *mgr, int seq_id, int32_t *out, int *n) {
+    if (!mgr || !n || (*n > 0 && !out)) return fail(TL_ERR_INVALID, "tl_kv_block_table: null argument");
+    return guarded([&] {
+        auto r = mgr->m->blockTable(seq_id);
+        if (r.isErr()) return fail(TL_ERR_INVALID, r.error());
+        const auto &t = r.value();
+        const int   m = static_cast<int>(t.size());
+        for (int i = 0; i < std::min(*n, m); ++i) out[i] = t[static_cast<size_t>(i)];
+        *n = m;
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
 
 int tl_kv_set_block_map(tl_kv_manager *mgr, int block_tokens, const int32_t *perm, size_t n) {
     if (!mgr) return fail(TL_ERR_INVALID, "tl_kv_set_block_map: null manager");

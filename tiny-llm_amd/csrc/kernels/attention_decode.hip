@@ -137,37 +137,35 @@ struct RowAddr {
             vbase = reinterpret_cast<const char *>(v.v_base) + head + (int64_t)row * blk_bytes;
         }
     }
-    // Block ids of the tokens [t_first, t_last] of one tile (at most
-    // kTile / 16 + 1 blocks): lane i holds the id of block (t_first >> log2)
-    // + i, clamped to the last one.  Loaded one tile ahead, so the address
+    // Block ids of the four 16-token quarters of one tile [t_first, t_last]
+    // (t_first is a multiple of kTile and blocks hold >= 16 tokens, so each
+    // quarter lies in one block): lane k < 4 holds the block of token
+    // min(t_first + 16k, t_last).  Loaded one tile ahead, so the address
     // arithmetic of the loads never waits on the block table.
     __device__ __forceinline__ int tile_blocks(int t_first, int t_last, int lane) const {
+        static_assert(kTile == 64, "four 16-token quarters per tile");
         if constexpr (PAGED) {
-            const int j0 = t_first >> log2_blk, j1 = t_last >> log2_blk;
-            return lane <= kTile / 16 ? bt_row[min(j0 + lane, j1)] : 0;
+            return lane < 4 ? bt_row[min(t_first + 16 * lane, t_last) >> log2_blk] : 0;
         } else {
             return 0;
         }
     }
-    // Base of the block holding token t (t wave-uniform) from the tile's
-    // block ids (j0 = first block of the tile); the <= 16 tokens of one
-    // aligned load step share it (blocks hold >= 16 tokens).
-    __device__ __forceinline__ int64_t block_off(int t, int btv, int j0) const {
-        if constexpr (PAGED) {
-            const int i = __builtin_amdgcn_readfirstlane((t >> log2_blk) - j0);
-            return (int64_t)__builtin_amdgcn_readlane(btv, i) * blk_bytes;
-        } else {
-            return 0;
-        }
+    // Byte offsets of the quarters' blocks, wave-uniform (scalar registers):
+    // four readlanes per tile, after which every load step picks its
+    // quarter's offset by a compile-time index.
+    struct Quarters {
+        int64_t o[4];
+    };
+    __device__ __forceinline__ Quarters quarters(int btv) const {
+        Quarters q;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            q.o[k] = PAGED ? (int64_t)__builtin_amdgcn_readlane(btv, k) * blk_bytes : 0;
+        return q;
     }
     __device__ __forceinline__ uint32_t in_block(int t) const {
         if constexpr (PAGED) return ((uint32_t)t & mask) * tok_bytes;
         else return (uint32_t)t * tok_bytes;
-    }
-    // Per-lane full offset of token t (any block of the tile).
-    __device__ __forceinline__ int64_t lane_off(int t, int btv, int j0) const {
-        if constexpr (PAGED) return (int64_t)__shfl(btv, (t >> log2_blk) - j0) * blk_bytes + in_block(t);
-        else return in_block(t);
     }
     // Per-lane full offset straight from the block table (one-off accesses).
     __device__ __forceinline__ int64_t lane_off(int t) const {
@@ -454,7 +452,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     constexpr int  NKB = NSTEP / KB;
     constexpr int  VB = TL_ATTN_VB < NBLK ? TL_ATTN_VB : NBLK; // pair blocks per V batch
     constexpr int  NVB = NBLK / VB;
-    constexpr bool kUniformPairs = 2 * TPI <= 16; // a pair block sits in one 16-token block
     extern __shared__ __align__(16) char smem[];
 
     const int       lane = threadIdx.x & 63;
@@ -525,39 +522,35 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     const int ntiles = (n + kTile - 1) / kTile;
     uint4     kb[2][KB];
     uint4     va[2][VB], vb[2][VB];
-    // Tile at chunk offset ts; tokens below tend are valid; btv / j0: the
-    // tile's block ids (tile_blocks) and first block.
-    auto kload = [&](int ts, int tend, int bi, uint4(&buf)[KB], int btv, int j0) {
+    // Tile at chunk offset ts; tokens below tend are valid; q: the tile's
+    // quarter block offsets.  A load step's TPI <= 16 tokens lie in one
+    // quarter, known at compile time; tokens past the end are clamped to the
+    // last valid one, which lies in the same quarter or in the block of the
+    // tile's last token, the block that quarters past the end name.
+    using Quarters = typename RowAddr<PAGED>::Quarters;
+    auto kload = [&](int ts, int tend, int bi, uint4(&buf)[KB], const Quarters &q) {
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
             const int   ss = t0 + ts + (bi * KB + u) * TPI; // step start (global token)
             const int   lim = t0 + tend - 1;
-            const int   ssc = ss < lim ? ss : lim;
             const int   t = ss + r < lim ? ss + r : lim;
-            const char *base = ra.kbase + ra.block_off(ssc, btv, j0);
+            const char *base = ra.kbase + q.o[(bi * KB + u) * TPI / 16];
             buf[u] = ld16nt(base + ra.in_block(t) + 16 * p);
         }
     };
-    auto vload = [&](int ts, int tend, int bj, uint4(&bufa)[VB], uint4(&bufb)[VB], int btv, int j0) {
+    auto vload = [&](int ts, int tend, int bj, uint4(&bufa)[VB], uint4(&bufb)[VB], const Quarters &q) {
 #pragma unroll
         for (int u = 0; u < VB; ++u) {
-            const int bs = t0 + ts + (bj * VB + u) * 2 * TPI; // pair block start
+            const int ob = (bj * VB + u) * 2 * TPI; // pair block start in the tile
+            const int bs = t0 + ts + ob;
             const int lim = t0 + tend - 1;
             const int ta = bs + r < lim ? bs + r : lim;
             const int tb = bs + TPI + r < lim ? bs + TPI + r : lim;
-            if constexpr (kUniformPairs) {
-                const int   bsc = bs < lim ? bs : lim;
-                const char *base = ra.vbase + ra.block_off(bsc, btv, j0);
-                bufa[u] = ld16nt(base + ra.in_block(ta) + 16 * p);
-                bufb[u] = ld16nt(base + ra.in_block(tb) + 16 * p);
-            } else {
-                bufa[u] = ld16nt(ra.vbase + ra.lane_off(ta, btv, j0) + 16 * p);
-                bufb[u] = ld16nt(ra.vbase + ra.lane_off(tb, btv, j0) + 16 * p);
-            }
+            bufa[u] = ld16nt(ra.vbase + q.o[ob / 16] + ra.in_block(ta) + 16 * p);
+            bufb[u] = ld16nt(ra.vbase + q.o[(ob + TPI) / 16] + ra.in_block(tb) + 16 * p);
         }
     };
-    // First block and block ids of the wave's tile ti (paged views only).
-    auto tile_j0 = [&](int ti_) { return PAGED ? (t0 + ti_ * kTile) >> ra.log2_blk : 0; };
+    // Quarter block ids of the wave's tile ti (paged views only).
     auto tile_bt = [&](int ti_) {
         return ra.tile_blocks(t0 + ti_ * kTile, t0 + min(n, ti_ * kTile + kTile) - 1, lane);
     };
@@ -566,19 +559,19 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     int bt_cur = 0, bt_next = 0;
     if (ti < ntiles) {
         bt_cur = tile_bt(ti);
-        kload(ti * kTile, min(n, ti * kTile + kTile), 0, kb[0], bt_cur, tile_j0(ti));
+        kload(ti * kTile, min(n, ti * kTile + kTile), 0, kb[0], ra.quarters(bt_cur));
     }
     for (; ti < ntiles; ti += kNW) {
-        const int ts = ti * kTile;
-        const int tend = min(n, ts + kTile);
-        const int nt = tend - ts;
-        const int j0 = tile_j0(ti);
+        const int      ts = ti * kTile;
+        const int      tend = min(n, ts + kTile);
+        const int      nt = tend - ts;
+        const Quarters qc = ra.quarters(bt_cur);
         if (PAGED && ti + kNW < ntiles) bt_next = tile_bt(ti + kNW); // consumed one tile later
         // ---- scores
 #pragma unroll
         for (int bi = 0; bi < NKB; ++bi) {
-            if (bi + 1 < NKB) kload(ts, tend, bi + 1, kb[(bi + 1) & 1], bt_cur, j0);
-            else vload(ts, tend, 0, va[0], vb[0], bt_cur, j0);
+            if (bi + 1 < NKB) kload(ts, tend, bi + 1, kb[(bi + 1) & 1], qc);
+            else vload(ts, tend, 0, va[0], vb[0], qc);
             if constexpr (MFMA) {
 #pragma unroll
                 for (int u = 0; u < KB; u += SPG)
@@ -607,10 +600,10 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 #pragma unroll
         for (int bj = 0; bj < NVB; ++bj) {
             if (bj + 1 < NVB) {
-                vload(ts, tend, bj + 1, va[(bj + 1) & 1], vb[(bj + 1) & 1], bt_cur, j0);
+                vload(ts, tend, bj + 1, va[(bj + 1) & 1], vb[(bj + 1) & 1], qc);
             } else if (ti + kNW < ntiles) {
                 const int tn = (ti + kNW) * kTile;
-                kload(tn, min(n, tn + kTile), 0, kb[0], bt_next, tile_j0(ti + kNW));
+                kload(tn, min(n, tn + kTile), 0, kb[0], ra.quarters(bt_next));
             }
 #pragma unroll
             for (int u = 0; u < VB; ++u) {

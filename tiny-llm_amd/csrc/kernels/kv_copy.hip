@@ -7,6 +7,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 namespace tiny_llm {
 namespace detail {
 
@@ -79,7 +81,35 @@ __global__ __launch_bounds__(kCopyThreads) void kv_gather_kernel(GatherArgs a) {
     *reinterpret_cast<uint4 *>(a.out + dst) = val;
 }
 
+struct TableArgs {
+    int32_t *table;
+    int32_t  n;
+    int32_t  idx[kTableBatch];
+    int32_t  val[kTableBatch];
+};
+
+__global__ __launch_bounds__(256) void table_update_kernel(TableArgs a) {
+    const int i = (int)threadIdx.x;
+    if (i < a.n) a.table[a.idx[i]] = a.val[i];
+}
+
 } // namespace
+
+void launch_table_update(int32_t *table, const std::pair<int32_t, int32_t> *upd, size_t n,
+                         hipStream_t stream) {
+    static_assert(kTableBatch <= 256, "one thread per pair");
+    for (size_t first = 0; first < n; first += kTableBatch) {
+        TableArgs a;
+        a.table = table;
+        a.n = (int32_t)std::min<size_t>(kTableBatch, n - first);
+        for (int i = 0; i < a.n; ++i) {
+            a.idx[i] = upd[first + (size_t)i].first;
+            a.val[i] = upd[first + (size_t)i].second;
+        }
+        hipLaunchKernelGGL(table_update_kernel, dim3(1), dim3(256), 0, stream, a);
+        HIP_CHECK(hipGetLastError());
+    }
+}
 
 void launch_kv_append(const KvView &view, int64_t layer_stride, const int32_t *wpos, int first_pos,
                       int n, int num_layers, int row_elems, const __half *new_k,

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <utility>
 #include <vector>
 
 namespace tiny_llm {
@@ -118,6 +119,14 @@ void launch_kv_append(const KvView &view, int64_t layer_stride, const int32_t *w
 // +0.0 for lens[b] <= t < s_max.  which: 0 = K, 1 = V.
 void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int uniform_len, int n,
                       int Hkv, int D, int s_max, __half *out, hipStream_t stream);
+
+// Writes table[idx[i]] = val[i] for the n (index, value) pairs, in stream
+// order: the device copy of a block table follows its host mirror with only
+// the entries that changed.  Pairs travel in kernel arguments, kTableBatch per
+// launch.
+constexpr int kTableBatch = 240;
+void launch_table_update(int32_t *table, const std::pair<int32_t, int32_t> *upd, size_t n,
+                         hipStream_t stream);
 
 // Score path of the attention kernels: 0 = VALU dot products over the
 // loaded rows, 1 = MFMA over an LDS-transposed K tile, 2 = auto (VALU for

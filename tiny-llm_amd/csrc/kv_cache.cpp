@@ -8,6 +8,7 @@
 // of csrc/kernels/.
 #include "tiny_llm/kv_cache.h"
 
+#include "block_allocator.h"
 #include "kernels/kv_kernels.h"
 #include "kernels/w8a16.h"
 #include "runtime.h"
@@ -24,8 +25,30 @@ namespace tiny_llm {
 
 using detail::KvView;
 
+KVCacheManager::KVCacheManager(const KVCacheConfig &config) : config_(config) {}
+
 // KVCacheManager::create (kv_cache.cpp:8-60).
 Result<std::unique_ptr<KVCacheManager>> KVCacheManager::create(const KVCacheConfig &config) {
+    return build(config, 0, 0);
+}
+
+Result<std::unique_ptr<KVCacheManager>> KVCacheManager::createPaged(const KVCacheConfig &config,
+                                                                    int block_tokens,
+                                                                    int num_blocks) {
+    using R = Result<std::unique_ptr<KVCacheManager>>;
+    if (block_tokens < 16 || (block_tokens & (block_tokens - 1)) != 0)
+        return R::err("KVCacheManager: block_tokens must be a power of two >= 16 (got " +
+                      std::to_string(block_tokens) + ")");
+    if (num_blocks <= 0 || num_blocks == INT32_MAX)
+        return R::err("KVCacheManager: num_blocks must be in [1, 2^31 - 2] (got " +
+                      std::to_string(num_blocks) + ")");
+    return build(config, block_tokens, num_blocks);
+}
+
+// The checks and pool set-up of create (kv_cache.cpp:8-60); with
+// block_tokens > 0 the pool is the block pool of createPaged.
+Result<std::unique_ptr<KVCacheManager>> KVCacheManager::build(const KVCacheConfig &config,
+                                                              int block_tokens, int num_blocks) {
     using R = Result<std::unique_ptr<KVCacheManager>>;
     if (config.num_layers <= 0 || config.num_heads <= 0 || config.head_dim <= 0 ||
         config.max_seq_len <= 0 || config.max_batch_size <= 0) {
@@ -38,9 +61,23 @@ Result<std::unique_ptr<KVCacheManager>> KVCacheManager::create(const KVCacheConf
     const size_t kv_total = kv_per_layer * static_cast<size_t>(config.num_layers) * 2;
     if (kv_total > SIZE_MAX / sizeof(half)) return R::err("KVCacheManager: memory size overflow");
     manager->slot_size_ = kv_total * sizeof(half);
-    if (manager->slot_size_ > SIZE_MAX / static_cast<size_t>(config.max_batch_size))
-        return R::err("KVCacheManager: pool size overflow");
-    manager->pool_size_ = manager->slot_size_ * static_cast<size_t>(config.max_batch_size);
+    if (block_tokens == 0) {
+        if (manager->slot_size_ > SIZE_MAX / static_cast<size_t>(config.max_batch_size))
+            return R::err("KVCacheManager: pool size overflow");
+        manager->pool_size_ = manager->slot_size_ * static_cast<size_t>(config.max_batch_size);
+        manager->layer_stride_ = 2 * static_cast<int64_t>(kv_per_layer);
+    } else {
+        const size_t block_elems =
+            static_cast<size_t>(block_tokens) * config.num_heads * config.head_dim;
+        const size_t per_kv = block_elems * (static_cast<size_t>(num_blocks) + 1);
+        if (per_kv > SIZE_MAX / (2 * sizeof(half) * static_cast<size_t>(config.num_layers)))
+            return R::err("KVCacheManager: pool size overflow");
+        manager->pool_size_ = per_kv * 2 * static_cast<size_t>(config.num_layers) * sizeof(half);
+        manager->layer_stride_ = 2 * static_cast<int64_t>(per_kv);
+        manager->block_tokens_ = block_tokens;
+        const int bpr = (config.max_seq_len + block_tokens - 1) / block_tokens;
+        manager->blocks_.reset(new detail::BlockAllocator(config.max_batch_size, bpr, num_blocks));
+    }
 
     hipError_t err = hipGetDevice(&manager->device_);
     if (err != hipSuccess)
@@ -55,6 +92,16 @@ Result<std::unique_ptr<KVCacheManager>> KVCacheManager::create(const KVCacheConf
         (void)hipFree(manager->memory_pool_);
         manager->memory_pool_ = nullptr;
         return R::err(std::string("KVCacheManager: hipMemset failed: ") + hipGetErrorString(err));
+    }
+    if (manager->blocks_) {
+        // Every entry starts at the spare block.
+        const std::vector<int32_t> &t = manager->blocks_->table();
+        err = hipMalloc(reinterpret_cast<void **>(&manager->block_map_dev_), t.size() * sizeof(int32_t));
+        if (err == hipSuccess)
+            err = hipMemcpy(manager->block_map_dev_, t.data(), t.size() * sizeof(int32_t),
+                            hipMemcpyHostToDevice);
+        if (err != hipSuccess)
+            return R::err(std::string("KVCacheManager: block table: ") + hipGetErrorString(err));
     }
 
     manager->slots_.resize(static_cast<size_t>(config.max_batch_size));
@@ -123,6 +170,7 @@ Result<void> KVCacheManager::releaseSequence(int seq_id) {
         return Result<void>::err("Sequence not found: " + std::to_string(seq_id));
     }
     auto &slot = slots_[static_cast<size_t>(it->second)];
+    if (blocks_) blocks_->release(it->second);
     slot.active = false;
     slot.seq_id = -1;
     slot.current_len = 0;
@@ -199,6 +247,15 @@ Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new
                                  ", max: " + std::to_string(slot.max_len));
     }
     const int row = config_.num_heads * config_.head_dim;
+    if (blocks_) {
+        const int need = (write_pos + num_tokens + block_tokens_ - 1) / block_tokens_;
+        if (!blocks_->ensure(slot_idx, need)) {
+            auto r = exhausted(need - blocks_->mapped(slot_idx));
+            TLLM_ERROR("appendKV: %s", r.error().c_str());
+            return r;
+        }
+        syncTable(stream);
+    }
     if (!isPaged()) {
         half        *k_cache = memory_pool_ + calculateOffset(slot_idx, layer_idx, false);
         half        *v_cache = memory_pool_ + calculateOffset(slot_idx, layer_idx, true);
@@ -207,8 +264,8 @@ Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new
         HIP_CHECK(hipMemcpyAsync(k_cache + pos_offset, new_k, copy_size, hipMemcpyDeviceToDevice, stream));
         HIP_CHECK(hipMemcpyAsync(v_cache + pos_offset, new_v, copy_size, hipMemcpyDeviceToDevice, stream));
     } else {
-        // Paged pool: the tokens cross 16-token blocks, so scatter them with
-        // the append kernel through this slot's row of the block map.
+        // Paged pool: the tokens cross blocks, so scatter them with the
+        // append kernel through this slot's row of the block map.
         KvView v = layerView(layer_idx, nullptr);
         v.block_table = block_map_dev_ + static_cast<size_t>(slot_idx) * v.bt_stride;
         v.bt_stride = 0;
@@ -233,7 +290,18 @@ Result<void> KVCacheManager::advanceSeqLen(int seq_id, int num_tokens) {
     }
     auto     &slot = slots_[static_cast<size_t>(it->second)];
     const int old_len = slot.current_len;
-    slot.current_len = std::min(slot.current_len + num_tokens, slot.max_len);
+    const int new_len = std::min(slot.current_len + num_tokens, slot.max_len);
+    if (blocks_) {
+        // Positions made visible without an append still get blocks, so
+        // that every visible token of a block pool is backed.
+        const int need = (new_len + block_tokens_ - 1) / block_tokens_;
+        if (!blocks_->ensure(it->second, need)) {
+            auto r = exhausted(need - blocks_->mapped(it->second));
+            TLLM_ERROR("advanceSeqLen: %s", r.error().c_str());
+            return r;
+        }
+    }
+    slot.current_len = new_len;
     TLLM_TRACE("advanceSeqLen: seq_id=%d, %d -> %d", seq_id, old_len, slot.current_len);
     (void)old_len;
     return Result<void>::ok();
@@ -248,9 +316,12 @@ bool KVCacheManager::hasSequence(int seq_id) const noexcept {
     return seq_to_slot_.find(seq_id) != seq_to_slot_.end();
 }
 size_t KVCacheManager::getUsedMemory() const noexcept {
+    if (blocks_) return static_cast<size_t>(blocks_->usedBlocks()) * blockBytes();
     return static_cast<size_t>(getActiveSequenceCount()) * slot_size_;
 }
-size_t KVCacheManager::getTotalMemory() const noexcept { return pool_size_; }
+size_t KVCacheManager::getTotalMemory() const noexcept {
+    return blocks_ ? static_cast<size_t>(blocks_->numBlocks()) * blockBytes() : pool_size_;
+}
 size_t KVCacheManager::getFreeMemory() const noexcept { return getTotalMemory() - getUsedMemory(); }
 int    KVCacheManager::getActiveSequenceCount() const noexcept {
     int count = 0;
@@ -268,7 +339,53 @@ const SequenceCache *KVCacheManager::sequence(int seq_id) const noexcept {
     return s < 0 ? nullptr : &slots_[static_cast<size_t>(s)];
 }
 
+int KVCacheManager::numBlocks() const noexcept { return blocks_ ? blocks_->numBlocks() : 0; }
+int KVCacheManager::freeBlocks() const noexcept { return blocks_ ? blocks_->freeBlocks() : 0; }
+size_t KVCacheManager::blockBytes() const noexcept {
+    return blocks_ ? static_cast<size_t>(block_tokens_) * config_.num_heads * config_.head_dim *
+                         config_.num_layers * 2 * sizeof(half)
+                   : 0;
+}
+
+Result<std::vector<int32_t>> KVCacheManager::blockTable(int seq_id) const {
+    using R = Result<std::vector<int32_t>>;
+    if (!blocks_) return R::err("blockTable: not a block pool");
+    const int slot = slotOf(seq_id);
+    if (slot < 0) return R::err("Sequence not found: " + std::to_string(seq_id));
+    const auto  &t = blocks_->table();
+    const size_t base = static_cast<size_t>(slot) * static_cast<size_t>(blocks_->blocksPerRow());
+    return R::ok(std::vector<int32_t>(t.begin() + static_cast<std::ptrdiff_t>(base),
+                                      t.begin() + static_cast<std::ptrdiff_t>(base) + blocks_->mapped(slot)));
+}
+
+Result<void> KVCacheManager::exhausted(int64_t need) const {
+    return Result<void>::err("KV cache exhausted: no free blocks available. Needed: " +
+                             std::to_string(need) + " blocks, free: " +
+                             std::to_string(blocks_->freeBlocks()) + " of " +
+                             std::to_string(blocks_->numBlocks()));
+}
+
+void KVCacheManager::syncTable(hipStream_t stream) {
+    if (!blocks_ || !blocks_->hasUpdates()) return;
+    const auto upd = blocks_->takeUpdates();
+    detail::launch_table_update(block_map_dev_, upd.data(), upd.size(), stream);
+}
+
+Result<void> KVCacheManager::reserveSlots(const int32_t *slots, const int32_t *tokens, int n) {
+    if (!blocks_ || n <= 0) return Result<void>::ok();
+    std::vector<int> rows(static_cast<size_t>(n)), need(static_cast<size_t>(n));
+    for (int i = 0; i < n; ++i) {
+        rows[static_cast<size_t>(i)] = slots[i];
+        need[static_cast<size_t>(i)] = (tokens[i] + block_tokens_ - 1) / block_tokens_;
+    }
+    const int64_t short_by = blocks_->shortfall(rows.data(), need.data(), n);
+    if (short_by > 0) return exhausted(short_by + blocks_->freeBlocks());
+    for (int i = 0; i < n; ++i) blocks_->ensure(rows[static_cast<size_t>(i)], need[static_cast<size_t>(i)]);
+    return Result<void>::ok();
+}
+
 Result<void> KVCacheManager::setBlockMap(int block_tokens, const int32_t *perm, size_t n) {
+    if (blocks_) return Result<void>::err("setBlockMap: a block pool maps its blocks itself");
     if (getActiveSequenceCount() != 0)
         return Result<void>::err("setBlockMap: the block map can only change with no live sequences");
     if (perm == nullptr) {
@@ -315,11 +432,9 @@ Result<void> KVCacheManager::setBlockMap(int block_tokens, const int32_t *perm, 
 }
 
 KvView KVCacheManager::layerView(int layer_idx, const int32_t *seq_row_dev) const {
-    const int64_t kv_per_layer =
-        static_cast<int64_t>(config_.num_heads) * config_.max_seq_len * config_.head_dim;
     KvView v;
-    v.k_base = memory_pool_ + static_cast<int64_t>(layer_idx) * 2 * kv_per_layer;
-    v.v_base = v.k_base + kv_per_layer;
+    v.k_base = memory_pool_ + static_cast<int64_t>(layer_idx) * layer_stride_;
+    v.v_base = v.k_base + layer_stride_ / 2;
     v.seq_row = seq_row_dev;
     v.tok_stride = static_cast<int64_t>(config_.num_heads) * config_.head_dim;
     v.head_stride = config_.head_dim;
@@ -327,7 +442,7 @@ KvView KVCacheManager::layerView(int layer_idx, const int32_t *seq_row_dev) cons
         int lg = 0;
         while ((1 << lg) < block_tokens_) ++lg;
         v.block_table = block_map_dev_;
-        v.bt_stride = config_.max_seq_len / block_tokens_;
+        v.bt_stride = blocks_ ? blocks_->blocksPerRow() : config_.max_seq_len / block_tokens_;
         v.log2_blk = lg;
         v.blk_stride = static_cast<int64_t>(block_tokens_) * v.tok_stride;
     } else {
@@ -372,9 +487,12 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
         return Result<void>::err("DecodeBatch: n=" + std::to_string(n) + " outside [0, " +
                                  std::to_string(max_seqs_) + "]");
     if (n > 0 && seq_ids == nullptr) return Result<void>::err("DecodeBatch: seq_ids is null");
+    // A failed prepare leaves an empty batch.
+    n_ = 0;
+    appendable_ = false;
+    ids_.clear();
     const KVCacheConfig &cfg = mgr_.getConfig();
     std::vector<char>    taken(static_cast<size_t>(cfg.max_batch_size), 0);
-    ids_.assign(seq_ids, seq_ids + n);
     lens_.assign(static_cast<size_t>(n), 0);
     wpos_.assign(static_cast<size_t>(n), 0);
     slot_.assign(static_cast<size_t>(n), 0);
@@ -404,6 +522,15 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
             lens_[static_cast<size_t>(i)] = a;
         }
     }
+    if (mgr_.isBlockPool()) {
+        // Back the decode token's position (and, for attended lengths, what
+        // the kernels read) with blocks before any kernel of the step runs.
+        if (appendable) {
+            auto r = mgr_.reserveSlots(slot_.data(), lens_.data(), n);
+            if (r.isErr()) return r;
+        }
+        mgr_.syncTable(stream);
+    }
     // Split-K plan: work items (entry, chunk), longest first.
     detail::WorkList &wl = *plan_;
     detail::plan_work(lens_.data(), n, cfg.num_heads, cfg.head_dim, wl);
@@ -413,6 +540,7 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
     n_work_ = wl.n_work;
     n_ = n;
     appendable_ = appendable;
+    ids_.assign(seq_ids, seq_ids + n);
     // Small batches carry their metadata in the attention kernel's arguments;
     // the device copy is made only when a kernel that reads it is launched.
     inline_ok_ = detail::pack_inline(lens_.data(), wl, slot_.data(), n, *inl_);
@@ -475,10 +603,8 @@ Result<void> DecodeBatch::append(int layer_begin, int num_layers, const half *ne
                                  std::to_string(cfg.num_layers) + ")");
     if (n_ == 0) return Result<void>::ok();
     upload_device(stream);
-    const KvView  v = mgr_.layerView(layer_begin, d_slot_);
-    const int64_t layer_stride =
-        2 * static_cast<int64_t>(cfg.num_heads) * cfg.max_seq_len * cfg.head_dim;
-    detail::launch_kv_append(v, layer_stride, d_wpos_, 0, n_, num_layers,
+    const KvView v = mgr_.layerView(layer_begin, d_slot_);
+    detail::launch_kv_append(v, mgr_.layerStride(), d_wpos_, 0, n_, num_layers,
                              cfg.num_heads * cfg.head_dim, new_k, new_v, stream);
     return Result<void>::ok();
 }

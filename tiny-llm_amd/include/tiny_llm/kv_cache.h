@@ -5,6 +5,11 @@
 // Pool layout (kv_cache.cpp:69-80, 226-233), one hipMalloc'd block:
 //   [slot][layer][K|V][max_seq_len][num_heads][head_dim]  fp16
 // so a token's K (or V) row of num_heads*head_dim halves is contiguous.
+//
+// A block-granular pool (createPaged) instead holds num_blocks blocks of
+// block_tokens tokens plus one spare block:
+//   [layer][K|V][num_blocks + 1][block_tokens][num_heads][head_dim]  fp16
+// and a sequence is handed blocks as it grows (see BlockAllocator).
 #pragma once
 
 #include "tiny_llm/hip_utils.h"
@@ -25,6 +30,7 @@ namespace tiny_llm {
 namespace detail {
 struct KvView;
 struct WorkList;
+class BlockAllocator;
 struct InlineMeta;
 class MetaRing;
 class Workspace;
@@ -70,6 +76,32 @@ class KVCacheManager {
     const KVCacheConfig &getConfig() const noexcept { return config_; }
 
     // ---- additions of the batched path ----
+    // Block-granular pool: the reference's API over num_blocks blocks of
+    // block_tokens tokens (a power of two >= 16) instead of max_batch_size
+    // full max_seq_len slots.  max_batch_size bounds the live sequences;
+    // memory follows the tokens held.  appendKV, advanceSeqLen and
+    // DecodeBatch::prepare map the blocks they need and fail with "KV cache
+    // exhausted" when the pool has too few free blocks; releaseSequence
+    // returns a sequence's blocks.  getUsedMemory / getTotalMemory count
+    // blocks (num_blocks * blockBytes() in total).
+    static Result<std::unique_ptr<KVCacheManager>> createPaged(const KVCacheConfig &config,
+                                                               int block_tokens, int num_blocks);
+    bool   isBlockPool() const noexcept { return blocks_ != nullptr; }
+    int    numBlocks() const noexcept;
+    int    freeBlocks() const noexcept;
+    size_t blockBytes() const noexcept;
+    // Physical blocks of a sequence of a block pool, in token order.
+    Result<std::vector<int32_t>> blockTable(int seq_id) const;
+    // Patches the device block table with the entries changed since the last
+    // call, on `stream` (no-op for other pools).  Every call that launches a
+    // kernel reading the table calls this first.
+    void syncTable(hipStream_t stream);
+    // Maps blocks so that every listed slot holds tokens[i] tokens: all or
+    // nothing.
+    Result<void> reserveSlots(const int32_t *slots, const int32_t *tokens, int n);
+    // Elements from layer l's K base to layer l+1's.
+    int64_t layerStride() const noexcept { return layer_stride_; }
+
     // Paged addressing over the same pool (see tl_kv_set_block_map).
     Result<void>         setBlockMap(int block_tokens, const int32_t *perm, size_t n);
     bool                 isPaged() const noexcept { return block_tokens_ > 0; }
@@ -83,7 +115,10 @@ class KVCacheManager {
     detail::KvView layerView(int layer_idx, const int32_t *seq_row_dev) const;
 
   private:
-    explicit KVCacheManager(const KVCacheConfig &config) : config_(config) {}
+    explicit KVCacheManager(const KVCacheConfig &config);
+    static Result<std::unique_ptr<KVCacheManager>> build(const KVCacheConfig &config,
+                                                         int block_tokens, int num_blocks);
+    Result<void> exhausted(int64_t need) const;
 
     size_t calculateOffset(int slot_idx, int layer_idx, bool is_value) const;
     int    findFreeSlot() const;
@@ -100,6 +135,8 @@ class KVCacheManager {
     int      block_tokens_ = 0;          // 0: reference layout
     int32_t *block_map_dev_ = nullptr;   // [max_batch][max_seq_len/bt] physical block ids
     std::vector<int32_t> block_map_host_;
+    int64_t  layer_stride_ = 0;          // elements between consecutive layers' K bases
+    std::unique_ptr<detail::BlockAllocator> blocks_;  // block pool only
 };
 
 // A decode step over n sequences of one manager.  prepare() snapshots the

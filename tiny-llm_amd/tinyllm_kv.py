@@ -90,6 +90,11 @@ def _declare(L: C.CDLL) -> None:
         "tl_kv_slot_bytes": (sz, [vp]),
         "tl_kv_slot_of": (i, [vp, i]),
         "tl_kv_set_block_map": (i, [vp, i, vp, sz]),
+        "tl_kv_create_paged": (i, [C.POINTER(KVConfig), i, i, C.POINTER(vp)]),
+        "tl_kv_num_blocks": (i, [vp]),
+        "tl_kv_free_blocks": (i, [vp]),
+        "tl_kv_block_bytes": (sz, [vp]),
+        "tl_kv_block_table": (i, [vp, i, vp, ip]),
         "tl_kv_batch_create": (i, [vp, i, i, C.POINTER(vp)]),
         "tl_kv_batch_destroy": (None, [vp]),
         "tl_kv_batch_prepare": (i, [vp, vp, i, vp]),
@@ -146,11 +151,17 @@ class KVCacheManager:
     """tiny_llm::KVCacheManager over HIP (same method names as the reference)."""
 
     def __init__(self, num_layers=32, num_heads=32, head_dim=128, max_seq_len=2048,
-                 max_batch_size=1):
+                 max_batch_size=1, block_tokens=0, num_blocks=0):
+        """block_tokens > 0: a block-granular pool of num_blocks blocks
+        (tl_kv_create_paged); otherwise the reference's slot pool."""
         L = load()
         self.config = KVConfig(num_layers, num_heads, head_dim, max_seq_len, max_batch_size)
         self._h = C.c_void_p()
-        _check(L.tl_kv_create(C.byref(self.config), C.byref(self._h)))
+        if block_tokens:
+            _check(L.tl_kv_create_paged(C.byref(self.config), block_tokens, num_blocks,
+                                        C.byref(self._h)))
+        else:
+            _check(L.tl_kv_create(C.byref(self.config), C.byref(self._h)))
 
     @classmethod
     def create(cls, **cfg):
@@ -186,6 +197,25 @@ class KVCacheManager:
     def getCache(self, seq_id, layer_idx):
         r, _ = self.getCacheChecked(seq_id, layer_idx)
         return r if r is not None else (0, 0)
+
+    def numBlocks(self):
+        return load().tl_kv_num_blocks(self._h)
+
+    def freeBlocks(self):
+        return load().tl_kv_free_blocks(self._h)
+
+    def blockBytes(self):
+        return load().tl_kv_block_bytes(self._h)
+
+    def blockTable(self, seq_id):
+        """(physical block ids in token order, None) or (None, error)."""
+        n = C.c_int(0)
+        rc = load().tl_kv_block_table(self._h, seq_id, None, C.byref(n))
+        if rc != TL_OK:
+            return None, last_error()
+        out = (C.c_int32 * max(1, n.value))()
+        rc = load().tl_kv_block_table(self._h, seq_id, out, C.byref(n))
+        return (list(out)[:n.value], None) if rc == TL_OK else (None, last_error())
 
     def appendKV(self, seq_id, layer_idx, new_k, new_v, num_tokens, stream=0):
         rc = load().tl_kv_append(self._h, seq_id, layer_idx, new_k, new_v, num_tokens, stream)
