@@ -45,10 +45,15 @@ def parse():
                     help="timed steps (default: 100 for configs 2-4, 1000 for config 5)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5))
-    ap.add_argument("--path", default="decode", choices=("decode", "project", "oproj"),
+    ap.add_argument("--path", default="decode", choices=("decode", "project", "oproj", "prefill"),
                     help="decode: append + attention (the headline); project: the decode step's "
                          "fused QKV W8A16 projection writing K/V into the cache; oproj: the W8A16 "
-                         "o_proj + residual (Llama-3-8B layer shapes, batch 64)")
+                         "o_proj + residual (Llama-3-8B layer shapes, batch 64); prefill: prompt "
+                         "tokens appended and attended causally over the cache")
+    ap.add_argument("--prefill-seqs", type=int, default=4, help="prefill: prompts per step")
+    ap.add_argument("--prefill-tokens", type=int, default=2048, help="prefill: new tokens per prompt")
+    ap.add_argument("--prefill-prefix", type=int, default=0,
+                    help="prefill: tokens already cached per prompt (chunked continuation)")
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -400,6 +405,86 @@ def churn(args, tl, torch, workloads, np):
                 kpass_desc=f"second run of the same {K}-step event sequence")
 
 
+def prefill_bench(args, tl, torch, np):
+    """Prefill into the cache at Llama-3-8B attention shapes (32 q / 8 kv
+    heads, head_dim 128): --prefill-seqs prompts of --prefill-tokens new tokens
+    on top of --prefill-prefix cached ones, one layer.  A step is
+    PrefillBatch.prepare + run (append of the new K/V rows, then causal GQA
+    attention of every new token over its sequence's cache).  The cache is
+    rewound after each step (lengths are not committed), so every step
+    repeats the same work."""
+    Hq, Hkv, D = 32, 8, 128
+    nseq, n, p0 = args.prefill_seqs, args.prefill_tokens, args.prefill_prefix
+    K = args.steps or 20
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261201 + 11)
+    M = ((p0 + n + 63) // 64) * 64
+    mgr = tl.KVCacheManager(1, Hkv, D, M, nseq)
+    ids = [mgr.allocateSequence(M)[0] for _ in range(nseq)]
+    if p0:
+        pk = torch.randn((p0, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+        for sid in ids:
+            assert mgr.appendKV(sid, 0, pk.data_ptr(), pk.data_ptr(), p0, stream) is None
+            mgr.advanceSeqLen(sid, p0)
+    T = nseq * n
+    q = torch.randn((T, Hq, D), generator=gen, device=dev, dtype=torch.float16)
+    nk = torch.randn((T, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    nv = torch.randn((T, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    out = torch.empty((T, Hq, D), device=dev, dtype=torch.float16)
+    pb = tl.PrefillBatch(mgr, nseq, Hq)
+    scale = 1.0 / float(np.sqrt(D))
+
+    def call():
+        pb.prepare(ids, [n] * nseq, stream)
+        pb.run(0, q.data_ptr(), nk.data_ptr(), nv.data_ptr(), out.data_ptr(), scale, stream)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    ev0.record()
+    for _ in range(K):
+        call()
+    ev1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms = ev0.elapsed_time(ev1) / K
+    tl.profile_reset()
+    tl.profile_enable(True)
+    for _ in range(min(K, 10)):
+        call()
+    torch.cuda.synchronize()
+    tl.profile_enable(False)
+    a_ms, a_n = tl.profile_query("attn_prefill")
+    c_ms, c_n = tl.profile_query("kv_append")
+    tl.profile_reset()
+    a_avg, c_avg = a_ms / max(1, a_n), c_ms / max(1, c_n)
+    # causal attention FLOPs: QK^T and PV, 2 flops per multiply-add, query j
+    # of a prompt attending p0 + j + 1 keys
+    keys = nseq * (n * p0 + n * (n + 1) // 2)
+    flops = 4.0 * D * Hq * keys
+    tflops = flops / (a_avg * 1e-3) / 1e12
+    peak = 2500.0
+    return {
+        "metric": "prefill attention TFLOP/s (causal GQA over the cache), Llama-3-8B heads",
+        "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: Q/K/V ~ N(0,1) (torch.randn, seeded)",
+        "config": {"workload": f"llama3_8b_prefill_{nseq}x{n}" + (f"_prefix{p0}" if p0 else ""),
+                   "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "prompts": nseq,
+                   "new_tokens": n, "cached_prefix": p0, "attended_keys": keys},
+        "kernels_us": {"attn_prefill": round(a_avg * 1e3, 2), "kv_append": round(c_avg * 1e3, 2)},
+        "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
+        "roofline": {"kernel": "attn_prefill_kernel<128,4,contiguous>", "bound": "mfma",
+                     "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+
+
 def gemm_bench(args, tl, torch, np):
     """W8A16 projection kernels at Llama-3-8B layer shapes (hidden 4096, 32 q /
     8 kv heads, head_dim 128, group 128) for a decode batch of 64.  Weights of
@@ -520,6 +605,9 @@ def main():
     import workloads
 
     torch.cuda.set_device(0)
+    if args.path == "prefill":
+        print(json.dumps(prefill_bench(args, tl, torch, np)), flush=True)
+        return
     if args.path != "decode":
         print(json.dumps(gemm_bench(args, tl, torch, np)), flush=True)
         return

@@ -228,6 +228,51 @@ int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_l
 void tl_attention_decode(const void *q, const void *k, const void *v, void *out, float scale,
                          int batch, int num_heads, int seq_len, int head_dim, void *stream);
 
+/* attention_prefill (kernels/attention.cuh:20-26, attention.cu:131-237):
+ * q/k/v/out [B][H][S][D] fp16 device pointers, causal (query i attends to
+ * keys 0..i), softmax with 1/(sum+1e-6), MFMA with fp32 accumulation.
+ * Silently returns on non-positive dimensions; head_dim in {32,64,128,256}. */
+void tl_attention_prefill(const void *q, const void *k, const void *v, void *out, float scale,
+                          int batch, int num_heads, int seq_len, int head_dim, void *stream);
+/* softmax (kernels/attention.cuh:28-30, attention.cu:288-354): rows of
+ * seq_len fp16 values, [batch][seq_len] in and out. */
+void tl_softmax(const void *input, void *output, int batch, int seq_len, void *stream);
+/* get_attention_weights (kernels/attention.cuh:32-36, attention.cu:240-286):
+ * weights [B][H][query_len][key_len] = fp16(scale * q.k), 0 above the
+ * diagonal when causal != 0; no softmax. */
+void tl_get_attention_weights(const void *q, const void *k, void *weights, float scale, int batch,
+                              int num_heads, int query_len, int key_len, int head_dim, int causal,
+                              void *stream);
+
+/* ------------------------------------------------------------------------
+ * Prefill into the cache (build addition).  The reference's prefill branch
+ * (src/transformer.cpp:214-241, inference_engine.cpp:233-272) appends the
+ * prompt's K/V with appendKV(n) and runs attention_prefill over k_buf_/v_buf_;
+ * this batch appends the new tokens of several sequences and runs causal
+ * GQA attention of each new token over its sequence's cache (positions
+ * 0 .. getSeqLen + j), so a prompt can also continue chunk by chunk.
+ *   prepare: seq_ids[i] brings num_tokens[i] >= 1 new tokens (same checks and
+ *            error texts as appendKV; block pools map the blocks needed);
+ *   append:  new_k/new_v [T][num_heads*head_dim], sequences back to back,
+ *            T = sum of num_tokens (bytes identical to appendKV per sequence);
+ *   attention: q/out [T][num_q_heads][head_dim];
+ *   run:     append + attention;
+ *   commit:  advanceSeqLen(seq_ids[i], num_tokens[i]).
+ * num_q_heads / num_heads in {1,2,4,8}; head_dim in {32,64,128,256}. */
+typedef struct tl_kv_prefill tl_kv_prefill;
+int  tl_kv_prefill_create(tl_kv_manager *mgr, int max_seqs, int num_q_heads, tl_kv_prefill **out);
+void tl_kv_prefill_destroy(tl_kv_prefill *p);
+int  tl_kv_prefill_prepare(tl_kv_prefill *p, const int *seq_ids, const int *num_tokens, int n,
+                           void *stream);
+int  tl_kv_prefill_info(const tl_kv_prefill *p, int *n, int *tokens);
+int  tl_kv_prefill_append(tl_kv_prefill *p, int layer, const void *new_k, const void *new_v,
+                          void *stream);
+int  tl_kv_prefill_attention(tl_kv_prefill *p, int layer, const void *q, void *out, float scale,
+                             void *stream);
+int  tl_kv_prefill_run(tl_kv_prefill *p, int layer, const void *q, const void *new_k,
+                       const void *new_v, void *out, float scale, void *stream);
+int  tl_kv_prefill_commit(tl_kv_prefill *p);
+
 /* w8a16_matmul (kernels/w8a16_matmul.cuh:22-26, w8a16_matmul.cu:219-236):
  * output[M][N] = fp16(input[M][K] @ dequant(weight[K][N] int8,
  * scales[ceil(K/group_size)][N] fp16)), fp32 accumulation.  Returns TL_OK

@@ -28,6 +28,15 @@
  *                          invariance; GQA sharing; decode == last row of
  *                          causal full attention (test_transformer.cu:222-300)
  *                          (tests/test_oracle_attention.py).
+ *   orc_attention_prefill  row i == orc_attention_decode over the first i+1
+ *                          keys, bit for bit (masked keys add exact zeros);
+ *                          float64 causal softmax attention by numpy; row 0
+ *                          == v_0 / (1 + 1e-6) (tests/test_oracle_prefill.py).
+ *   orc_softmax            float64 softmax by numpy; rows sum to 1; order
+ *                          kept (test_kernels.cu:505-530, :664-740).
+ *   orc_get_attention_weights  float64 scale * q.k by numpy within one fp16
+ *                          rounding; exact zeros above the diagonal
+ *                          (test_kernels.cu:558-662).
  *   orc_kv_gather          brute-force element loop in numpy over the same
  *                          view parameters plus the identity
  *                          gather(cache layout) == reshaped reference pool.
@@ -518,6 +527,125 @@ void orc_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *
     for (int b = 0; b < B; ++b) lens[b] = S;
     orc_attn_decode_gqa(q, &view, lens, B, H, H, D, scale, out_f32, out_f16, 1);
     free(lens);
+}
+
+/* ------------------------------------------------------------------------ */
+/* prefill attention, softmax, attention weights (attention.cu:131-354)      */
+/* ------------------------------------------------------------------------ */
+
+/* One (b, h, i) row of attention_prefill_kernel (attention.cu:131-222), in
+ * order:
+ *   s_p = (sum_d fmaf(q_d, k_pd)) * scale for p <= i, -FLT_MAX for p > i (:149-162)
+ *   m = max_p s_p; e_p = expf(s_p - m); sum = sum_p e_p            (:165-204)
+ *   w_p = e_p * (1 / (sum + 1e-6f))                                 (:207-210)
+ *   o_d = sum_{p<S} fmaf(w_p, v_pd), p in order                     (:214-220)
+ * Masked keys give e_p = expf(-FLT_MAX - m) = 0 and add fmaf(0, v, o) = o,
+ * so row i equals decode attention over the first i + 1 keys. */
+void orc_attention_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                           float *out_f32, uint16_t *out_f16, float scale, int B, int H, int S,
+                           int D, int nthreads) {
+    if (B <= 0 || H <= 0 || S <= 0 || D <= 0) return;
+    h2f_table_init();
+    const long rows = (long)B * H * S;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = 1;
+#pragma omp parallel num_threads(nthreads)
+#else
+    (void)nthreads;
+#endif
+    {
+        float *scores = (float *)malloc(sizeof(float) * (size_t)S);
+        float *acc = (float *)malloc(sizeof(float) * (size_t)D);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+        for (long r = 0; r < rows; ++r) {
+            const long      bh = r / S;
+            const int       i = (int)(r % S);
+            const uint16_t *qr = q + r * D;
+            const uint16_t *kb = k + bh * S * D;
+            const uint16_t *vb = v + bh * S * D;
+            for (int p = 0; p < S; ++p) {
+                if (p <= i) {
+                    float score = 0.0f;
+                    for (int d = 0; d < D; ++d)
+                        score = fmaf(g_h2f_table[qr[d]], g_h2f_table[kb[(size_t)p * D + d]], score);
+                    scores[p] = score * scale;
+                } else {
+                    scores[p] = -FLT_MAX;
+                }
+            }
+            float m = -FLT_MAX;
+            for (int p = 0; p < S; ++p) m = fmaxf(m, scores[p]);
+            float sum = 0.0f;
+            for (int p = 0; p < S; ++p) {
+                const float e = expf(scores[p] - m);
+                scores[p] = e;
+                sum += e;
+            }
+            const float inv = 1.0f / (sum + 1e-6f);
+            for (int p = 0; p < S; ++p) scores[p] *= inv;
+            for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+            for (int p = 0; p < S; ++p)
+                for (int d = 0; d < D; ++d)
+                    acc[d] = fmaf(scores[p], g_h2f_table[vb[(size_t)p * D + d]], acc[d]);
+            for (int d = 0; d < D; ++d) {
+                if (out_f32) out_f32[r * D + d] = acc[d];
+                out_f16[r * D + d] = orc_f2h(acc[d]);
+            }
+        }
+        free(scores);
+        free(acc);
+    }
+}
+
+/* softmax_kernel (attention.cu:288-343): max, e_i = expf(x_i - max),
+ * sum, y_i = half(e_i * (1 / (sum + 1e-6f))). */
+void orc_softmax(const uint16_t *in, float *out_f32, uint16_t *out_f16, int rows, int S) {
+    if (rows <= 0 || S <= 0) return;
+    h2f_table_init();
+    float *e = (float *)malloc(sizeof(float) * (size_t)S);
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *x = in + (size_t)r * S;
+        float           m = -FLT_MAX;
+        for (int i = 0; i < S; ++i) m = fmaxf(m, g_h2f_table[x[i]]);
+        float sum = 0.0f;
+        for (int i = 0; i < S; ++i) {
+            e[i] = expf(g_h2f_table[x[i]] - m);
+            sum += e[i];
+        }
+        const float inv = 1.0f / (sum + 1e-6f);
+        for (int i = 0; i < S; ++i) {
+            const float y = e[i] * inv;
+            if (out_f32) out_f32[(size_t)r * S + i] = y;
+            out_f16[(size_t)r * S + i] = orc_f2h(y);
+        }
+    }
+    free(e);
+}
+
+/* get_attention_weights_kernel (attention.cu:240-268). */
+void orc_get_attention_weights(const uint16_t *q, const uint16_t *k, float *out_f32,
+                               uint16_t *out_f16, float scale, int B, int H, int Lq, int Lk, int D,
+                               int causal) {
+    if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D <= 0) return;
+    h2f_table_init();
+    for (long bh = 0; bh < (long)B * H; ++bh)
+        for (int i = 0; i < Lq; ++i) {
+            const uint16_t *qr = q + (bh * Lq + i) * D;
+            for (int p = 0; p < Lk; ++p) {
+                const size_t o = (size_t)(bh * Lq + i) * Lk + p;
+                float        w = 0.0f;
+                if (!(causal && p > i)) {
+                    float score = 0.0f;
+                    for (int d = 0; d < D; ++d)
+                        score = fmaf(g_h2f_table[qr[d]], g_h2f_table[k[(bh * Lk + p) * D + d]], score);
+                    w = score * scale;
+                }
+                if (out_f32) out_f32[o] = w;
+                out_f16[o] = orc_f2h(w);
+            }
+        }
 }
 
 void orc_kv_gather(const orc_kv_view *kv, int which, const int32_t *seq_lens, int B, int Hkv,

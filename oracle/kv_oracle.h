@@ -111,6 +111,25 @@ void orc_attn_decode_gqa(const uint16_t *q, const orc_kv_view *kv, const int32_t
 void orc_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out_f32,
                           uint16_t *out_f16, float scale, int B, int H, int S, int D);
 
+/* attention_prefill (attention.cu:131-237): compact [B][H][S][D] Q/K/V/out,
+ * MHA; row (b, h, i) scores every key p < S, masked to -FLT_MAX for p > i,
+ * then softmax with 1/(sum+1e-6) and o_d = sum over all S keys of w_p v_pd.
+ * Silent no-op on non-positive dimensions (:228-230).  out_f32 may be NULL. */
+void orc_attention_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                           float *out_f32, uint16_t *out_f16, float scale, int B, int H, int S,
+                           int D, int nthreads);
+
+/* softmax (attention.cu:288-354): rows of S fp16 values, softmax with
+ * 1/(sum+1e-6), fp16 output.  out_f32 may be NULL. */
+void orc_softmax(const uint16_t *in, float *out_f32, uint16_t *out_f16, int rows, int S);
+
+/* get_attention_weights (attention.cu:240-286): fp16(scale * q.k) for every
+ * (b, h, query i, key p) of [B][H][Lq][Lk]; 0 where causal and p > i.  No
+ * softmax.  out_f32 (may be NULL) holds the value before rounding. */
+void orc_get_attention_weights(const uint16_t *q, const uint16_t *k, float *out_f32,
+                               uint16_t *out_f16, float scale, int B, int H, int Lq, int Lk, int D,
+                               int causal);
+
 /* Gather: out[b][g][t][d] = cache(b,g,t,d) for t < seq_lens[b], 0 otherwise.
  * out is [B][Hkv][S_max][D]; which = 0 gathers K, 1 gathers V.             */
 /* ---- W8A16 matmul (kernels/w8a16_matmul.cu:71-98, the reference kernel

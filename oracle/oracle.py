@@ -21,11 +21,11 @@ _lib = None
 
 
 def build(force: bool = False) -> str:
-    """Compile the oracle with its Makefile (gcc, no GPU)."""
-    if force or not os.path.exists(_LIB_PATH):
-        if force and os.path.exists(_LIB_PATH):
-            os.remove(_LIB_PATH)
-        subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    """Compile the oracle with its Makefile (gcc, no GPU); make rebuilds it
+    when a source is newer than the library."""
+    if force and os.path.exists(_LIB_PATH):
+        os.remove(_LIB_PATH)
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
     return _LIB_PATH
 
 
@@ -74,6 +74,12 @@ def _declare(L: C.CDLL) -> None:
     L.orc_attn_decode_gqa.argtypes = [vp, C.POINTER(_View), vp, i, i, i, i, C.c_float, vp, vp, i]
     L.orc_attention_decode.argtypes = [vp, vp, vp, vp, vp, C.c_float, i, i, i, i]
     L.orc_kv_gather.argtypes = [C.POINTER(_View), i, vp, i, i, i, i, vp]
+    L.orc_attention_prefill.argtypes = [vp, vp, vp, vp, vp, C.c_float, i, i, i, i, i]
+    L.orc_attention_prefill.restype = None
+    L.orc_softmax.argtypes = [vp, vp, vp, i, i]
+    L.orc_softmax.restype = None
+    L.orc_get_attention_weights.argtypes = [vp, vp, vp, vp, C.c_float, i, i, i, i, i, i]
+    L.orc_get_attention_weights.restype = None
     L.orc_w8a16_matmul.argtypes = [vp, vp, vp, vp, vp, i, i, i, i]
     L.orc_w8a16_matmul.restype = None
     L.orc_add_inplace.argtypes = [vp, vp, C.c_size_t]
@@ -268,6 +274,37 @@ def attention_decode(q, k, v, scale, B, H, S, D):
     o32 = np.zeros((B, H, D), dtype=np.float32)
     o16 = np.zeros((B, H, D), dtype=np.uint16)
     lib().orc_attention_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(o32), _ptr(o16), scale, B, H, S, D)
+    return o32, o16
+
+
+def attention_prefill(q, k, v, scale, B, H, S, D, nthreads=1):
+    """Literal attention_prefill contract: compact [B][H][S][D], causal, MHA.
+    Returns (out_f32, out_f16 bits), each [B][H][S][D]."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k, v))
+    o32 = np.zeros((B, H, S, D), dtype=np.float32)
+    o16 = np.zeros((B, H, S, D), dtype=np.uint16)
+    lib().orc_attention_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(o32), _ptr(o16), scale, B, H, S, D,
+                                nthreads)
+    return o32, o16
+
+
+def softmax(x, rows, S):
+    """softmax over rows of S fp16 bit patterns -> (f32, f16 bits)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    o32 = np.zeros((rows, S), dtype=np.float32)
+    o16 = np.zeros((rows, S), dtype=np.uint16)
+    lib().orc_softmax(_ptr(x), _ptr(o32), _ptr(o16), rows, S)
+    return o32, o16
+
+
+def get_attention_weights(q, k, scale, B, H, Lq, Lk, D, causal):
+    """Scaled scores [B][H][Lq][Lk] (no softmax), zero above the diagonal when
+    causal -> (f32, f16 bits)."""
+    q, k = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k))
+    o32 = np.zeros((B, H, Lq, Lk), dtype=np.float32)
+    o16 = np.zeros((B, H, Lq, Lk), dtype=np.uint16)
+    lib().orc_get_attention_weights(_ptr(q), _ptr(k), _ptr(o32), _ptr(o16), scale, B, H, Lq, Lk, D,
+                                    int(causal))
     return o32, o16
 
 

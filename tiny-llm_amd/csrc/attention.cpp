@@ -5,6 +5,7 @@
 #include "tiny_llm/kernels/attention.h"
 
 #include "kernels/kv_kernels.h"
+#include "kernels/prefill.h"
 #include "runtime.h"
 #include "tiny_llm/hip_utils.h"
 #include "tiny_llm/logger.h"
@@ -117,9 +118,71 @@ std::string attn_decode_compact(const __half *q, const __half *k, const __half *
     return "";
 }
 
+std::string attn_prefill_compact(const __half *q, const __half *k, const __half *v, __half *out,
+                                float scale, int B, int H, int S, int D, hipStream_t stream) {
+    if (!prefill_shape_supported(D, 1))
+        return "attention_prefill: unsupported head_dim " + std::to_string(D) +
+               " (supported: 32, 64, 128, 256)";
+    if (!q || !k || !v || !out) return "attention_prefill: null pointer argument";
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return "attention_prefill: query, key, value and output must be 16-byte aligned";
+    KvView kv;
+    kv.k_base = k;
+    kv.v_base = v;
+    kv.log2_blk = 30;
+    kv.blk_stride = static_cast<int64_t>(H) * S * D;
+    kv.tok_stride = D;
+    kv.head_stride = static_cast<int64_t>(S) * D;
+    PrefillLaunch p;
+    p.q = q;
+    p.out = out;
+    p.q_tok_stride = D;
+    p.q_head_stride = static_cast<int64_t>(S) * D;
+    p.q_entry_stride = static_cast<int64_t>(H) * S * D;
+    p.uniform_b = B;
+    p.uniform_n = S;
+    launch_attn_prefill(p, kv, H, H, D, scale, stream);
+    return "";
+}
+
 } // namespace detail
 
 namespace kernels {
+
+void attention_prefill(const half *query, const half *key, const half *value, half *output,
+                       float scale, int batch_size, int num_heads, int seq_len, int head_dim,
+                       hipStream_t stream) {
+    if (batch_size <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return;
+    std::string err;
+    try {
+        err = detail::attn_prefill_compact(query, key, value, output, scale, batch_size, num_heads,
+                                           seq_len, head_dim, stream);
+    } catch (const std::exception &e) {
+        err = e.what();
+    }
+    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+}
+
+void softmax(const half *input, half *output, int batch_size, int seq_len, hipStream_t stream) {
+    if (batch_size <= 0 || seq_len <= 0) return;
+    try {
+        detail::launch_softmax(input, output, batch_size, seq_len, stream);
+    } catch (const std::exception &e) {
+        TLLM_ERROR("softmax: %s", e.what());
+    }
+}
+
+void get_attention_weights(const half *query, const half *key, half *weights, float scale,
+                           int batch_size, int num_heads, int query_len, int key_len, int head_dim,
+                           bool apply_causal_mask, hipStream_t stream) {
+    if (batch_size <= 0 || num_heads <= 0 || query_len <= 0 || key_len <= 0 || head_dim <= 0) return;
+    try {
+        detail::launch_attention_weights(query, key, weights, scale, batch_size, num_heads,
+                                         query_len, key_len, head_dim, apply_causal_mask, stream);
+    } catch (const std::exception &e) {
+        TLLM_ERROR("get_attention_weights: %s", e.what());
+    }
+}
 
 void attention_decode(const half *query, const half *k_cache, const half *v_cache, half *output,
                       float scale, int batch_size, int num_heads, int seq_len, int head_dim,

@@ -19,6 +19,8 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
                              int Hq, int Hkv, int D, float scale, __half *out, hipStream_t stream);
 std::string attn_decode_compact(const __half *q, const __half *k, const __half *v, __half *out,
                                 float scale, int B, int H, int S, int D, hipStream_t stream);
+std::string attn_prefill_compact(const __half *q, const __half *k, const __half *v, __half *out,
+                                 float scale, int B, int H, int S, int D, hipStream_t stream);
 std::string w8a16_call(const __half *x, const int8_t *w, const __half *s, __half *out, int M, int N,
                        int K, int gs, bool residual, hipStream_t stream, bool packed);
 std::string w8a16_pack_call(const int8_t *w, int K, int N, int8_t *out, hipStream_t stream);
@@ -27,6 +29,7 @@ void        w8a16_force_generic(int on);
 } // namespace tiny_llm
 
 using tiny_llm::DecodeBatch;
+using tiny_llm::PrefillBatch;
 using tiny_llm::KVCacheManager;
 using tiny_llm::Result;
 
@@ -35,6 +38,10 @@ struct tl_kv_manager {
 };
 struct tl_kv_batch {
     std::unique_ptr<DecodeBatch> b;
+};
+
+struct tl_kv_prefill {
+    std::unique_ptr<PrefillBatch> b;
 };
 
 namespace {
@@ -367,6 +374,91 @@ void tl_attention_decode(const void *q, const void *k, const void *v, void *out,
     });
 }
 
+int tl_kv_prefill_create(tl_kv_manager *mgr, int max_seqs, int num_q_heads, tl_kv_prefill **out) {
+    if (!mgr || !out) return fail(TL_ERR_INVALID, "tl_kv_prefill_create: null argument");
+    *out = nullptr;
+    return guarded([&] {
+        auto r = PrefillBatch::create(*mgr->m, max_seqs, num_q_heads);
+        if (r.isErr()) return fail(TL_ERR_INVALID, r.error());
+        *out = new tl_kv_prefill{std::move(r.value())};
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+void tl_kv_prefill_destroy(tl_kv_prefill *p) { delete p; }
+
+int tl_kv_prefill_prepare(tl_kv_prefill *p, const int *seq_ids, const int *num_tokens, int n,
+                          void *stream) {
+    if (!p) return fail(TL_ERR_INVALID, "tl_kv_prefill_prepare: null batch");
+    return guarded([&] { return status(p->b->prepare(seq_ids, num_tokens, n, as_stream(stream))); });
+}
+
+int tl_kv_prefill_info(const tl_kv_prefill *p, int *n, int *tokens) {
+    if (!p || !n || !tokens) return fail(TL_ERR_INVALID, "tl_kv_prefill_info: null argument");
+    *n = p->b->size();
+    *tokens = p->b->tokens();
+    return TL_OK;
+}
+
+int tl_kv_prefill_append(tl_kv_prefill *p, int layer, const void *new_k, const void *new_v,
+                         void *stream) {
+    if (!p) return fail(TL_ERR_INVALID, "tl_kv_prefill_append: null batch");
+    return guarded([&] {
+        return status(p->b->append(layer, as_half(new_k), as_half(new_v), as_stream(stream)));
+    });
+}
+
+int tl_kv_prefill_attention(tl_kv_prefill *p, int layer, const void *q, void *out, float scale,
+                            void *stream) {
+    if (!p) return fail(TL_ERR_INVALID, "tl_kv_prefill_attention: null batch");
+    return guarded([&] {
+        return status(p->b->attention(layer, as_half(q), as_half(out), scale, as_stream(stream)));
+    });
+}
+
+int tl_kv_prefill_run(tl_kv_prefill *p, int layer, const void *q, const void *new_k,
+                      const void *new_v, void *out, float scale, void *stream) {
+    if (!p) return fail(TL_ERR_INVALID, "tl_kv_prefill_run: null batch");
+    return guarded([&] {
+        return status(p->b->prefill(layer, as_half(q), as_half(new_k), as_half(new_v), as_half(out),
+                                    scale, as_stream(stream)));
+    });
+}
+
+int tl_kv_prefill_commit(tl_kv_prefill *p) {
+    if (!p) return fail(TL_ERR_INVALID, "tl_kv_prefill_commit: null batch");
+    return guarded([&] { return status(p->b->commit()); });
+}
+
+void tl_attention_prefill(const void *q, const void *k, const void *v, void *out, float scale,
+                          int batch, int num_heads, int seq_len, int head_dim, void *stream) {
+    if (batch <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return;
+    (void)guarded([&] {
+        const std::string err = tiny_llm::detail::attn_prefill_compact(
+            as_half(q), as_half(k), as_half(v), as_half(out), scale, batch, num_heads, seq_len,
+            head_dim, as_stream(stream));
+        if (!err.empty()) {
+            TLLM_ERROR("%s", err.c_str());
+            return fail(TL_ERR_INVALID, err);
+        }
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+void tl_softmax(const void *input, void *output, int batch, int seq_len, void *stream) {
+    tiny_llm::kernels::softmax(as_half(input), as_half(output), batch, seq_len, as_stream(stream));
+}
+
+void tl_get_attention_weights(const void *q, const void *k, void *weights, float scale, int batch,
+                              int num_heads, int query_len, int key_len, int head_dim, int causal,
+                              void *stream) {
+    tiny_llm::kernels::get_attention_weights(as_half(q), as_half(k), as_half(weights), scale, batch,
+                                             num_heads, query_len, key_len, head_dim, causal != 0,
+                                             as_stream(stream));
+}
+
 int tl_attn_set_score_path(int path) {
     if (path < 0 || path > 2)
         return fail(TL_ERR_INVALID, "tl_attn_set_score_path: path must be 0 (valu), 1 (mfma) or 2 (auto)");
@@ -389,10 +481,12 @@ void tl_profile_enable(int on) { tiny_llm::detail::profile_set(on != 0); }
 void tl_profile_reset(void) { tiny_llm::detail::profile_reset(); }
 
 int tl_profile_query(const char *kernel, double *total_ms, long long *launches) {
-    static const char *names[] = {"attn_chunk", "attn_merge", "kv_append", "kv_gather", "w8a16",
-                                  "w8a16_reduce"};
+    static const char *names[] = {"attn_chunk", "attn_merge",   "kv_append",   "kv_gather",
+                                  "w8a16",      "w8a16_reduce", "attn_prefill"};
+    constexpr int      kNames = static_cast<int>(sizeof(names) / sizeof(names[0]));
+    static_assert(kNames == static_cast<int>(tiny_llm::detail::KernelId::Count), "profile names");
     if (!kernel || !total_ms || !launches) return fail(TL_ERR_INVALID, "tl_profile_query: null argument");
-    for (int i = 0; i < 6; ++i)
+    for (int i = 0; i < kNames; ++i)
         if (std::strcmp(kernel, names[i]) == 0)
             return guarded([&] {
                 tiny_llm::detail::profile_query(i, total_ms, launches);

@@ -1,0 +1,449 @@
+// Prefill attention for gfx950: causal attention of a block of new query
+// tokens over a KV view, GQA, on MFMA; plus the reference's softmax and
+// attention-weights kernels.
+//
+// Per query token i of a sequence whose new tokens start at position p0 and
+// query head h (kv head g = h / G):
+//   o_h = (sum_{p <= p0+i} e_p v_{g,p}) / (sum_{p <= p0+i} e_p + 1e-6),
+//   e_p = 2^(s_p - m),  s_p = (q_h . k_{g,p}) * scale * log2(e),  m = max_p s_p
+// which is the arithmetic of attention_prefill_kernel (attention.cu:131-222:
+// masked keys get -FLT_MAX and contribute exp(...) = 0), reading the keys
+// from the cache instead of the current token batch, and equal to decode
+// attention over the first p0+i+1 keys.
+//
+// Workgroup: 4 waves, one kv head g, 64 query rows = 64/G tokens x G heads;
+// wave w owns rows 16w..16w+15.  Keys stream in tiles of 64 tokens through
+// LDS: K row-major, V transposed ([d][token]).  Per wave and tile:
+//   S^T = K Q^T        v_mfma_f32_16x16x32_f16: A = K rows (token l%16,
+//                      dims 8(l/16)..+7), B = Q (query l%16, same dims),
+//                      D = S^T (tokens 4(l/16)+i, query l%16)
+//   online softmax     per query column, over the lane's 16 scores and the
+//                      4 lanes sharing the column (xor 16, 32)
+//   O^T += V^T P^T     v_mfma_f32_16x16x16_f16: A = V^T (dim l%16, tokens
+//                      4(l/16)..+3) from the transposed tile, B = P^T,
+//                      which is the fp16 S^T fragment as it stands (tokens
+//                      4(l/16)+j, query l%16); D = O^T (dims 4(l/16)+i,
+//                      query l%16), so the rescale by the running max is
+//                      lane-local.
+// The next tile's K/V rows are loaded into registers while the current one
+// is computed.  Grid: work items x Hkv, kv head fastest, so with 8 kv heads
+// every workgroup of head g runs on XCD g and the tiles it re-reads stay in
+// that XCD's L2.
+#include "prefill.h"
+
+#include "tiny_llm/hip_utils.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cfloat>
+
+namespace tiny_llm {
+namespace detail {
+
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float    f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPThreads = 256;
+constexpr int kKeyTile = 64;
+
+struct PrefillArgs {
+    const __half       *q;
+    __half             *out;
+    KvView              kv;
+    const PrefillEntry *entries;
+    const int32_t      *work;
+    int64_t             q_tok;
+    int64_t             q_head;
+    int64_t             q_entry;
+    int                 uniform_b;
+    int                 uniform_n;
+    int                 Hkv;
+    float               scale_log2;
+};
+
+// Byte offsets of the token rows of one (cache row, kv head).
+template <bool PAGED>
+struct KeyRows {
+    const char    *kbase;
+    const char    *vbase;
+    const int32_t *bt_row;
+    int64_t        blk_bytes;
+    int64_t        tok_bytes;
+    int            log2_blk;
+    int            mask;
+
+    __device__ __forceinline__ KeyRows(const KvView &v, int row, int g) {
+        const int64_t head = (int64_t)g * v.head_stride * 2;
+        blk_bytes = v.blk_stride * 2;
+        tok_bytes = v.tok_stride * 2;
+        log2_blk = v.log2_blk;
+        mask = (1 << v.log2_blk) - 1;
+        if constexpr (PAGED) {
+            bt_row = v.block_table + (int64_t)row * v.bt_stride;
+            kbase = reinterpret_cast<const char *>(v.k_base) + head;
+            vbase = reinterpret_cast<const char *>(v.v_base) + head;
+        } else {
+            bt_row = nullptr;
+            kbase = reinterpret_cast<const char *>(v.k_base) + head + (int64_t)row * blk_bytes;
+            vbase = reinterpret_cast<const char *>(v.v_base) + head + (int64_t)row * blk_bytes;
+        }
+    }
+    __device__ __forceinline__ int64_t off(int t) const {
+        if constexpr (PAGED) return (int64_t)bt_row[t >> log2_blk] * blk_bytes + (int64_t)(t & mask) * tok_bytes;
+        else return (int64_t)t * tok_bytes;
+    }
+};
+
+__device__ __forceinline__ uint4 ld16(const char *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// Rounds x to fp32 in a register before whatever consumes it: keeps the
+// compiler from folding a multiply into the fp16 conversion that follows
+// (v_fma_mixlo_f16 rounds once, the reference's __float2half(a * b) twice).
+__device__ __forceinline__ float materialize(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+template <int D, int G, bool PAGED>
+__global__ __launch_bounds__(kPThreads) void attn_prefill_kernel(PrefillArgs a) {
+    static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
+    constexpr int BQ = 64 / G;         // query tokens per workgroup
+    constexpr int KS = D / 32;         // k steps of S^T
+    constexpr int DT = D / 16;         // dim tiles of O^T
+    constexpr int KP = D / 8;          // 16-byte pieces per row
+    constexpr int KPITCH = D + 8;      // halves per LDS K row
+    constexpr int VPITCH = kKeyTile + 8; // halves per LDS V^T row
+    constexpr int NKI = kKeyTile * KP / kPThreads;               // K pieces per thread
+    constexpr int VITEMS = (kKeyTile / 4) * KP;                  // (4-token group, piece) items
+    constexpr int NVI = (VITEMS + kPThreads - 1) / kPThreads;    // per thread
+    __shared__ __align__(16) uint16_t ks[kKeyTile * KPITCH];
+    __shared__ __align__(16) uint16_t vt[D * VPITCH];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int item = blockIdx.x / a.Hkv;
+    const int g = blockIdx.x - item * a.Hkv;
+    int64_t   q_off;
+    int       p0, n, row, qt;
+    if (a.entries) {
+        const int e = a.work[2 * item];
+        qt = a.work[2 * item + 1];
+        const PrefillEntry E = a.entries[e];
+        q_off = E.q_off;
+        p0 = E.p0;
+        n = E.n;
+        row = E.row;
+    } else { // uniform entries, the query tiles with the most keys first
+        const int nqt = (a.uniform_n + BQ - 1) / BQ;
+        const int b = item % a.uniform_b;
+        qt = nqt - 1 - item / a.uniform_b;
+        q_off = (int64_t)b * a.q_entry;
+        p0 = 0;
+        n = a.uniform_n;
+        row = b;
+    }
+    const int c = lane & 15, qg = lane >> 4;
+    const int r = wave * 16 + c;          // query row of this lane's column
+    const int qi = qt * BQ + r / G;       // query token within the entry
+    const int h = g * G + r % G;
+    const bool valid = qi < n;
+    const int qic = valid ? qi : n - 1;
+    const int pos = p0 + qic;             // keys 0 .. pos are attended
+    const int kend = p0 + min(n, (qt + 1) * BQ);
+    const int ntile = (kend + kKeyTile - 1) / kKeyTile;
+
+    const KeyRows<PAGED> kr(a.kv, row, g);
+
+    // Q fragments (B operand of S^T): query column c, dims 32ks + 8qg .. +7.
+    f16x8 qb[KS];
+    {
+        const char *qp = reinterpret_cast<const char *>(a.q + q_off + (int64_t)qic * a.q_tok +
+                                                        (int64_t)h * a.q_head);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qb[s] = __builtin_bit_cast(f16x8, ld16(qp + 2 * (32 * s + 8 * qg)));
+    }
+
+    uint4 kreg[NKI];
+    uint4 vreg[NVI][4];
+    auto load_tile = [&](int kt) {
+        const int t0 = kt * kKeyTile;
+#pragma unroll
+        for (int u = 0; u < NKI; ++u) {
+            const int it = tid + u * kPThreads;
+            const int tk = it / KP, pc = it - tk * KP;
+            const int t = min(t0 + tk, kend - 1);
+            kreg[u] = ld16(kr.kbase + kr.off(t) + 16 * pc);
+        }
+#pragma unroll
+        for (int u = 0; u < NVI; ++u) {
+            const int it = tid + u * kPThreads;
+            if (VITEMS % kPThreads == 0 || it < VITEMS) {
+                const int tg = it / KP, pc = it - tg * KP;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = min(t0 + 4 * tg + j, kend - 1);
+                    vreg[u][j] = ld16(kr.vbase + kr.off(t) + 16 * pc);
+                }
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int u = 0; u < NKI; ++u) {
+            const int it = tid + u * kPThreads;
+            const int tk = it / KP, pc = it - tk * KP;
+            *reinterpret_cast<uint4 *>(&ks[tk * KPITCH + 8 * pc]) = kreg[u];
+        }
+#pragma unroll
+        for (int u = 0; u < NVI; ++u) {
+            const int it = tid + u * kPThreads;
+            if (VITEMS % kPThreads == 0 || it < VITEMS) {
+                const int      tg = it / KP, pc = it - tg * KP;
+                const uint32_t w0[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
+                const uint32_t w1[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
+                const uint32_t w2[4] = {vreg[u][2].x, vreg[u][2].y, vreg[u][2].z, vreg[u][2].w};
+                const uint32_t w3[4] = {vreg[u][3].x, vreg[u][3].y, vreg[u][3].z, vreg[u][3].w};
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    // dims 8pc+2w (low halves) and 8pc+2w+1 (high halves) of tokens 4tg..4tg+3
+                    const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u),
+                                                __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u));
+                    const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u),
+                                                __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u));
+                    *reinterpret_cast<uint2 *>(&vt[(8 * pc + 2 * w) * VPITCH + 4 * tg]) = lo;
+                    *reinterpret_cast<uint2 *>(&vt[(8 * pc + 2 * w + 1) * VPITCH + 4 * tg]) = hi;
+                }
+            }
+        }
+    };
+
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    load_tile(0);
+    for (int kt = 0; kt < ntile; ++kt) {
+        store_tile();
+        __syncthreads();
+        if (kt + 1 < ntile) load_tile(kt + 1); // in flight during this tile's math
+
+        // ---- S^T = K Q^T, 16 keys x 16 queries per fragment
+        f32x4 s[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            s[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < KS; ++st) {
+                const f16x8 kf = *reinterpret_cast<const f16x8 *>(&ks[(16 * tt + c) * KPITCH + 32 * st + 8 * qg]);
+                s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qb[st], s[tt], 0, 0, 0);
+            }
+        }
+        // ---- causal mask, online softmax of the query column
+        const int tb = kt * kKeyTile + 4 * qg;
+        float     mloc = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x = tb + 16 * tt + i <= pos ? s[tt][i] * a.scale_log2 : -INFINITY;
+                s[tt][i] = x;
+                mloc = fmaxf(mloc, x);
+            }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        // Key 0 lies in tile 0 and is attended by every query, so m_new is finite.
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.0f;
+        f16x4 pf[4];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = __builtin_amdgcn_exp2f(s[tt][i] - m_new);
+                psum += p;
+                pf[tt][i] = (_Float16)p;
+            }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        // ---- O^T += V^T P^T
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const f16x4 vf = *reinterpret_cast<const f16x4 *>(&vt[(16 * dt + c) * VPITCH + 16 * tt + 4 * qg]);
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pf[tt], acc[dt], 0, 0, 0);
+            }
+        __syncthreads(); // the tile's LDS is rewritten next
+    }
+
+    float l = l_run + __shfl_xor(l_run, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / (l + 1e-6f);
+    if (valid) {
+        __half *op = a.out + q_off + (int64_t)qi * a.q_tok + (int64_t)h * a.q_head + 4 * qg;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const __half2 lo = __floats2half2_rn(acc[dt][0] * inv, acc[dt][1] * inv);
+            const __half2 hi = __floats2half2_rn(acc[dt][2] * inv, acc[dt][3] * inv);
+            uint2         w;
+            w.x = __builtin_bit_cast(uint32_t, lo);
+            w.y = __builtin_bit_cast(uint32_t, hi);
+            *reinterpret_cast<uint2 *>(op + 16 * dt) = w;
+        }
+    }
+}
+
+// softmax_kernel (attention.cu:288-343): one workgroup per row.
+__global__ __launch_bounds__(256) void softmax_kernel(const __half *in, __half *out, int S) {
+    __shared__ float red[8];
+    const __half *x = in + (int64_t)blockIdx.x * S;
+    __half       *y = out + (int64_t)blockIdx.x * S;
+    const int     tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float         m = -FLT_MAX;
+    for (int i = tid; i < S; i += 256) m = fmaxf(m, __half2float(x[i]));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    constexpr float kLog2e = 1.4426950408889634f;
+    float           sum = 0.0f;
+    for (int i = tid; i < S; i += 256) sum += exp2f((__half2float(x[i]) - m) * kLog2e);
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    if (lane == 0) red[4 + wave] = sum;
+    __syncthreads();
+    sum = (red[4] + red[5]) + (red[6] + red[7]);
+    const float inv = 1.0f / (sum + 1e-6f);
+    for (int i = tid; i < S; i += 256)
+        y[i] = __float2half(materialize(exp2f((__half2float(x[i]) - m) * kLog2e) * inv));
+}
+
+// get_attention_weights_kernel (attention.cu:240-268): one thread per
+// (query, key) score, the reference's sequential fmaf order over d, then
+// score * scale rounded to fp32 and to fp16.
+__global__ __launch_bounds__(256) void attention_weights_kernel(const __half *q, const __half *k,
+                                                                __half *w, float scale, int H,
+                                                                int Lq, int Lk, int D, int causal) {
+    const int     i = blockIdx.y, bh = blockIdx.z;
+    const int     p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= Lk) return;
+    const __half *qr = q + ((int64_t)bh * Lq + i) * D;
+    const __half *kr = k + ((int64_t)bh * Lk + p) * D;
+    float         v = 0.0f;
+    if (!(causal && p > i)) {
+        float score = 0.0f;
+        for (int d = 0; d < D; ++d) score = fmaf(__half2float(qr[d]), __half2float(kr[d]), score);
+        v = materialize(score * scale);
+    }
+    w[((int64_t)bh * Lq + i) * Lk + p] = __float2half(v);
+    (void)H;
+}
+
+template <int D, int G>
+void launch_dg(const PrefillArgs &a, int grid, bool paged, hipStream_t stream) {
+    if (paged)
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true>), dim3(grid), dim3(kPThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false>), dim3(grid), dim3(kPThreads), 0, stream, a);
+}
+
+template <int D>
+void launch_d(const PrefillArgs &a, int grid, int G, bool paged, hipStream_t stream) {
+    switch (G) {
+    case 1: launch_dg<D, 1>(a, grid, paged, stream); break;
+    case 2: launch_dg<D, 2>(a, grid, paged, stream); break;
+    case 4: launch_dg<D, 4>(a, grid, paged, stream); break;
+    case 8: launch_dg<D, 8>(a, grid, paged, stream); break;
+    default: break;
+    }
+}
+
+} // namespace
+
+bool prefill_shape_supported(int D, int G) {
+    return (D == 32 || D == 64 || D == 128 || D == 256) && (G == 1 || G == 2 || G == 4 || G == 8);
+}
+
+void plan_prefill(const PrefillEntry *entries, int n, int G, std::vector<int32_t> &work) {
+    const int BQ = prefill_block_tokens(G);
+    struct It {
+        int64_t keys;
+        int32_t e, qt;
+    };
+    std::vector<It> items;
+    for (int e = 0; e < n; ++e) {
+        const int nqt = (entries[e].n + BQ - 1) / BQ;
+        for (int qt = 0; qt < nqt; ++qt)
+            items.push_back({(int64_t)entries[e].p0 + std::min(entries[e].n, (qt + 1) * BQ), e, qt});
+    }
+    std::stable_sort(items.begin(), items.end(), [](const It &x, const It &y) { return x.keys > y.keys; });
+    work.resize(2 * items.size());
+    for (size_t i = 0; i < items.size(); ++i) {
+        work[2 * i] = items[i].e;
+        work[2 * i + 1] = items[i].qt;
+    }
+}
+
+void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int Hkv, int D,
+                         float scale, hipStream_t stream) {
+    const int G = Hq / Hkv;
+    int       items;
+    if (p.entries) {
+        items = p.n_items;
+    } else {
+        const int BQ = prefill_block_tokens(G);
+        items = p.uniform_b * ((p.uniform_n + BQ - 1) / BQ);
+    }
+    if (items <= 0) return;
+    PrefillArgs a;
+    a.q = p.q;
+    a.out = p.out;
+    a.kv = kv;
+    a.entries = p.entries;
+    a.work = p.work;
+    a.q_tok = p.q_tok_stride;
+    a.q_head = p.q_head_stride;
+    a.q_entry = p.q_entry_stride;
+    a.uniform_b = p.uniform_b;
+    a.uniform_n = p.uniform_n;
+    a.Hkv = Hkv;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    const int64_t grid = (int64_t)items * Hkv;
+    if (grid > INT32_MAX) throw std::invalid_argument("attention_prefill: too many work items");
+    const bool paged = kv.block_table != nullptr;
+    profile_begin(KernelId::AttnPrefill, stream);
+    switch (D) {
+    case 32: launch_d<32>(a, (int)grid, G, paged, stream); break;
+    case 64: launch_d<64>(a, (int)grid, G, paged, stream); break;
+    case 128: launch_d<128>(a, (int)grid, G, paged, stream); break;
+    case 256: launch_d<256>(a, (int)grid, G, paged, stream); break;
+    default: break;
+    }
+    HIP_CHECK(hipGetLastError());
+    profile_end(KernelId::AttnPrefill, stream);
+}
+
+void launch_softmax(const __half *in, __half *out, int rows, int S, hipStream_t stream) {
+    if (rows <= 0 || S <= 0) return;
+    hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(256), 0, stream, in, out, S);
+    HIP_CHECK(hipGetLastError());
+}
+
+void launch_attention_weights(const __half *q, const __half *k, __half *w, float scale, int B,
+                              int H, int Lq, int Lk, int D, bool causal, hipStream_t stream) {
+    if (B <= 0 || H <= 0 || Lq <= 0 || Lk <= 0 || D <= 0) return;
+    dim3 grid((unsigned)((Lk + 255) / 256), (unsigned)Lq, (unsigned)(B * H));
+    hipLaunchKernelGGL(attention_weights_kernel, grid, dim3(256), 0, stream, q, k, w, scale, H, Lq,
+                       Lk, D, causal ? 1 : 0);
+    HIP_CHECK(hipGetLastError());
+}
+
+} // namespace detail
+} // namespace tiny_llm

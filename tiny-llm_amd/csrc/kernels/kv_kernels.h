@@ -149,7 +149,8 @@ enum class KernelId {
     KvGather = 3,
     W8A16 = 4,       // main GEMM kernel (either path)
     W8A16Reduce = 5, // split-K reduction + epilogue
-    Count = 6
+    AttnPrefill = 6,
+    Count = 7
 };
 void profile_begin(KernelId id, hipStream_t stream);
 void profile_end(KernelId id, hipStream_t stream);

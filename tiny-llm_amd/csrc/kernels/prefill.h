@@ -1,0 +1,72 @@
+// Launch interface of the prefill-side attention kernels (gfx950):
+// causal attention of new query tokens over a KV view (the cache-native
+// prefill, and the reference's compact attention_prefill), plus the
+// reference's test-side softmax and attention-weights kernels.
+#pragma once
+
+#include "kv_kernels.h"
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <vector>
+
+namespace tiny_llm {
+namespace detail {
+
+// One sequence of a prefill call: its n new query tokens sit at positions
+// p0 .. p0+n-1 of cache row `row`; query token i, head h is at
+// q + q_off + i * q_tok_stride + h * q_head_stride (out likewise), and it
+// attends to the keys at positions 0 .. p0+i of that row.
+struct PrefillEntry {
+    int64_t q_off;
+    int32_t p0;
+    int32_t n;
+    int32_t row;
+    int32_t pad;
+};
+
+static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
+
+// Query tokens per workgroup: 64 query rows of (token, head) pairs, G heads
+// of one kv group per token.
+inline int prefill_block_tokens(int G) { return 64 / G; }
+
+// Work items (entry, query tile), most keys first (LPT order for the
+// hardware dispatcher): work[2i], work[2i+1].
+void plan_prefill(const PrefillEntry *entries, int n, int G, std::vector<int32_t> &work);
+
+struct PrefillLaunch {
+    const __half       *q = nullptr;
+    __half             *out = nullptr;
+    int64_t             q_tok_stride = 0;
+    int64_t             q_head_stride = 0;
+    // Either a device entry table and work list (n_items items) ...
+    const PrefillEntry *entries = nullptr;
+    const int32_t      *work = nullptr;
+    int                 n_items = 0;
+    // ... or, with entries == NULL, `uniform_b` entries b with p0 = 0,
+    // n = uniform_n, row = b and q_off = b * q_entry_stride.
+    int                 uniform_b = 0;
+    int                 uniform_n = 0;
+    int64_t             q_entry_stride = 0;
+};
+
+// True when (D, G) has a prefill kernel (D in {32,64,128,256}, G in {1,2,4,8}).
+bool prefill_shape_supported(int D, int G);
+
+// Throws HipException on launch failure.
+void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int Hkv, int D,
+                         float scale, hipStream_t stream);
+
+// softmax (attention.cu:288-354): rows of S fp16 values.
+void launch_softmax(const __half *in, __half *out, int rows, int S, hipStream_t stream);
+
+// get_attention_weights (attention.cu:240-286): [B][H][Lq][Lk] = fp16(scale * q.k),
+// zero above the diagonal when causal.
+void launch_attention_weights(const __half *q, const __half *k, __half *w, float scale, int B,
+                              int H, int Lq, int Lk, int D, bool causal, hipStream_t stream);
+
+} // namespace detail
+} // namespace tiny_llm

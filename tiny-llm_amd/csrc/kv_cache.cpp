@@ -10,6 +10,7 @@
 
 #include "block_allocator.h"
 #include "kernels/kv_kernels.h"
+#include "kernels/prefill.h"
 #include "kernels/w8a16.h"
 #include "runtime.h"
 #include "tiny_llm/logger.h"
@@ -716,6 +717,162 @@ Result<void> DecodeBatch::project(int layer_idx, const half *x, int hidden, int 
         return Result<void>::err("DecodeBatch: packed weights need hidden % 32 == 0 and group_size "
                                  "in {32, 64, 128, 256, 512}");
     detail::launch_w8a16(x, hidden, n_, hidden, group_size, segs, nseg, &rows, ws, stream, packed);
+    return Result<void>::ok();
+}
+
+// ======================================================================
+// PrefillBatch
+// ======================================================================
+
+PrefillBatch::PrefillBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads)
+    : mgr_(mgr), max_seqs_(max_seqs), num_q_heads_(num_q_heads), meta_(new detail::MetaRing(4)) {}
+
+PrefillBatch::~PrefillBatch() = default;
+
+Result<std::unique_ptr<PrefillBatch>> PrefillBatch::create(KVCacheManager &mgr, int max_seqs,
+                                                           int num_q_heads) {
+    using R = Result<std::unique_ptr<PrefillBatch>>;
+    const KVCacheConfig &cfg = mgr.getConfig();
+    if (max_seqs <= 0) return R::err("PrefillBatch: max_seqs must be positive");
+    if (num_q_heads <= 0 || num_q_heads % cfg.num_heads != 0)
+        return R::err("PrefillBatch: num_q_heads (" + std::to_string(num_q_heads) +
+                      ") must be a positive multiple of num_heads (" +
+                      std::to_string(cfg.num_heads) + ")");
+    if (!detail::prefill_shape_supported(cfg.head_dim, num_q_heads / cfg.num_heads))
+        return R::err("PrefillBatch: unsupported head_dim/group (head_dim in {32,64,128,256}, "
+                      "num_q_heads/num_heads in {1,2,4,8})");
+    return R::ok(std::unique_ptr<PrefillBatch>(new PrefillBatch(mgr, max_seqs, num_q_heads)));
+}
+
+Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, int n,
+                                   hipStream_t stream) {
+    n_ = 0;
+    tokens_ = 0;
+    ids_.clear();
+    counts_.clear();
+    if (n < 0 || n > max_seqs_)
+        return Result<void>::err("PrefillBatch: n=" + std::to_string(n) + " outside [0, " +
+                                 std::to_string(max_seqs_) + "]");
+    if (n > 0 && (seq_ids == nullptr || num_tokens == nullptr))
+        return Result<void>::err("PrefillBatch: seq_ids / num_tokens is null");
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    std::vector<char>    taken(static_cast<size_t>(cfg.max_batch_size), 0);
+    std::vector<int32_t> slots(static_cast<size_t>(n)), ends(static_cast<size_t>(n));
+    std::vector<detail::PrefillEntry> entries(static_cast<size_t>(n));
+    int64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        const int            id = seq_ids[i];
+        const SequenceCache *sc = mgr_.sequence(id);
+        if (!sc) return Result<void>::err("PrefillBatch: sequence not found: " + std::to_string(id));
+        const int slot = mgr_.slotOf(id);
+        if (taken[static_cast<size_t>(slot)])
+            return Result<void>::err("PrefillBatch: duplicate sequence in batch: " + std::to_string(id));
+        taken[static_cast<size_t>(slot)] = 1;
+        const int nt = num_tokens[i];
+        if (nt <= 0)
+            return Result<void>::err("appendKV: num_tokens must be positive: " + std::to_string(nt));
+        if (sc->current_len + nt > sc->max_len)
+            return Result<void>::err("appendKV: cache overflow. Current: " +
+                                     std::to_string(sc->current_len) + ", appending: " +
+                                     std::to_string(nt) + ", max: " + std::to_string(sc->max_len));
+        slots[static_cast<size_t>(i)] = slot;
+        ends[static_cast<size_t>(i)] = sc->current_len + nt;
+        entries[static_cast<size_t>(i)] = {total * num_q_heads_ * cfg.head_dim, sc->current_len, nt,
+                                           slot, 0};
+        total += nt;
+    }
+    if (total > INT32_MAX / 2)
+        return Result<void>::err("PrefillBatch: too many tokens in one prefill step");
+    if (mgr_.isBlockPool()) {
+        auto r = mgr_.reserveSlots(slots.data(), ends.data(), n);
+        if (r.isErr()) return r;
+        mgr_.syncTable(stream);
+    }
+    std::vector<int32_t> work;
+    detail::plan_prefill(entries.data(), n, num_q_heads_ / cfg.num_heads, work);
+    // Device copy: [entries (6 words each) | token rows T | token positions T | work].
+    const size_t T = static_cast<size_t>(total);
+    const size_t words = 6 * static_cast<size_t>(n) + 2 * T + work.size();
+    int32_t     *h = static_cast<int32_t *>(meta_->begin(words * 4));
+    std::memcpy(h, entries.data(), static_cast<size_t>(n) * sizeof(detail::PrefillEntry));
+    int32_t *rows = h + 6 * static_cast<size_t>(n), *pos = rows + T;
+    size_t   k = 0;
+    for (int i = 0; i < n; ++i)
+        for (int j = 0; j < num_tokens[i]; ++j, ++k) {
+            rows[k] = slots[static_cast<size_t>(i)];
+            pos[k] = entries[static_cast<size_t>(i)].p0 + j;
+        }
+    if (!work.empty()) std::memcpy(pos + T, work.data(), work.size() * 4);
+    const int32_t *d = static_cast<const int32_t *>(meta_->commit(stream));
+    d_entries_ = reinterpret_cast<const detail::PrefillEntry *>(d);
+    d_tok_row_ = d + 6 * static_cast<size_t>(n);
+    d_tok_pos_ = d_tok_row_ + T;
+    d_work_ = d_tok_pos_ + T;
+    n_items_ = static_cast<int>(work.size() / 2);
+    ids_.assign(seq_ids, seq_ids + n);
+    counts_.assign(num_tokens, num_tokens + n);
+    n_ = n;
+    tokens_ = static_cast<int>(total);
+    return Result<void>::ok();
+}
+
+Result<void> PrefillBatch::append(int layer_idx, const half *new_k, const half *new_v,
+                                  hipStream_t stream) {
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    if (new_k == nullptr) return Result<void>::err("new_k is null");
+    if (new_v == nullptr) return Result<void>::err("new_v is null");
+    if (layer_idx < 0 || layer_idx >= cfg.num_layers)
+        return Result<void>::err("PrefillBatch: Invalid layer_idx: " + std::to_string(layer_idx));
+    if (tokens_ == 0) return Result<void>::ok();
+    const int row = cfg.num_heads * cfg.head_dim;
+    // The append kernel's grid holds one token per y index (< 65536).
+    constexpr int kMaxY = 32768;
+    for (int t0 = 0; t0 < tokens_; t0 += kMaxY) {
+        const int nt = std::min(kMaxY, tokens_ - t0);
+        KvView    v = mgr_.layerView(layer_idx, d_tok_row_ + t0);
+        detail::launch_kv_append(v, 0, d_tok_pos_ + t0, 0, nt, 1, row,
+                                 new_k + static_cast<size_t>(t0) * row,
+                                 new_v + static_cast<size_t>(t0) * row, stream);
+    }
+    return Result<void>::ok();
+}
+
+Result<void> PrefillBatch::attention(int layer_idx, const half *q, half *out, float scale,
+                                     hipStream_t stream) {
+    const KVCacheConfig &cfg = mgr_.getConfig();
+    if (q == nullptr || out == nullptr) return Result<void>::err("PrefillBatch: q/out is null");
+    if (layer_idx < 0 || layer_idx >= cfg.num_layers)
+        return Result<void>::err("PrefillBatch: Invalid layer_idx: " + std::to_string(layer_idx));
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15u)
+        return Result<void>::err("PrefillBatch: q and out must be 16-byte aligned");
+    if (n_items_ == 0) return Result<void>::ok();
+    detail::PrefillLaunch p;
+    p.q = q;
+    p.out = out;
+    p.q_tok_stride = static_cast<int64_t>(num_q_heads_) * cfg.head_dim;
+    p.q_head_stride = cfg.head_dim;
+    p.entries = d_entries_;
+    p.work = d_work_;
+    p.n_items = n_items_;
+    detail::launch_attn_prefill(p, mgr_.layerView(layer_idx, nullptr), num_q_heads_, cfg.num_heads,
+                                cfg.head_dim, scale, stream);
+    return Result<void>::ok();
+}
+
+Result<void> PrefillBatch::prefill(int layer_idx, const half *q, const half *new_k,
+                                   const half *new_v, half *out, float scale, hipStream_t stream) {
+    auto r = append(layer_idx, new_k, new_v, stream);
+    if (r.isErr()) return r;
+    return attention(layer_idx, q, out, scale, stream);
+}
+
+// InferenceEngine::prefill's commit (inference_engine.cpp:272):
+// advanceSeqLen(seq, prompt tokens) once after all layers.
+Result<void> PrefillBatch::commit() {
+    for (size_t i = 0; i < ids_.size(); ++i) {
+        auto r = mgr_.advanceSeqLen(ids_[i], counts_[i]);
+        if (r.isErr()) return r;
+    }
     return Result<void>::ok();
 }
 

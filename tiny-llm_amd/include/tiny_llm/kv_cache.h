@@ -32,6 +32,7 @@ struct KvView;
 struct WorkList;
 class BlockAllocator;
 struct InlineMeta;
+struct PrefillEntry;
 class MetaRing;
 class Workspace;
 } // namespace detail
@@ -209,6 +210,55 @@ class DecodeBatch {
     bool                               uploaded_ = false;  // device copy of this prepare made
     const int32_t  *d_lens_ = nullptr, *d_wpos_ = nullptr, *d_slot_ = nullptr;
     const int32_t  *d_part_base_ = nullptr, *d_work_ = nullptr;
+};
+
+// A prefill step over n sequences of one manager: sequence i brings
+// num_tokens[i] new tokens at positions getSeqLen .. getSeqLen+num_tokens-1.
+// prepare() snapshots the write positions (and, for a block pool, maps the
+// blocks they need); every layer's append / attention then reads that
+// snapshot; commit() advances each sequence by its token count.  New tokens
+// are token-major and sequences back to back: K/V rows [T][num_heads *
+// head_dim], queries and outputs [T][num_q_heads][head_dim], T = the sum of
+// num_tokens.  Query token j of sequence i attends to the sequence's cache
+// positions 0 .. getSeqLen + j (causal, the new tokens included), which is
+// the prefill branch of TransformerLayer::attention (transformer.cpp:
+// 222-241) reading the cache instead of k_buf_/v_buf_; with getSeqLen > 0 it
+// continues a prompt chunk by chunk.
+class PrefillBatch {
+  public:
+    static Result<std::unique_ptr<PrefillBatch>> create(KVCacheManager &mgr, int max_seqs,
+                                                        int num_q_heads);
+    ~PrefillBatch();
+    PrefillBatch(const PrefillBatch &) = delete;
+    PrefillBatch &operator=(const PrefillBatch &) = delete;
+
+    Result<void> prepare(const int *seq_ids, const int *num_tokens, int n, hipStream_t stream);
+    // appendKV of every sequence's new tokens for one layer.
+    Result<void> append(int layer_idx, const half *new_k, const half *new_v, hipStream_t stream);
+    // Causal attention of the new tokens over the cache (after append).
+    Result<void> attention(int layer_idx, const half *q, half *out, float scale, hipStream_t stream);
+    // append + attention.
+    Result<void> prefill(int layer_idx, const half *q, const half *new_k, const half *new_v,
+                         half *out, float scale, hipStream_t stream);
+    // advanceSeqLen(seq, num_tokens[i]) for every sequence of the last prepare.
+    Result<void> commit();
+
+    int size() const noexcept { return n_; }
+    int tokens() const noexcept { return tokens_; }
+
+  private:
+    PrefillBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads);
+
+    KVCacheManager      &mgr_;
+    int                  max_seqs_;
+    int                  num_q_heads_;
+    int                  n_ = 0;
+    int                  tokens_ = 0;
+    int                  n_items_ = 0;
+    std::vector<int32_t> ids_, counts_;
+    std::unique_ptr<detail::MetaRing> meta_;
+    const int32_t       *d_tok_row_ = nullptr, *d_tok_pos_ = nullptr, *d_work_ = nullptr;
+    const detail::PrefillEntry *d_entries_ = nullptr;
 };
 
 } // namespace tiny_llm

@@ -112,6 +112,17 @@ def _declare(L: C.CDLL) -> None:
         "tl_w8a16_set_path": (i, [i]),
         "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
+        "tl_attention_prefill": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
+        "tl_softmax": (None, [vp, vp, i, i, vp]),
+        "tl_get_attention_weights": (None, [vp, vp, vp, f, i, i, i, i, i, i, vp]),
+        "tl_kv_prefill_create": (i, [vp, i, i, C.POINTER(vp)]),
+        "tl_kv_prefill_destroy": (None, [vp]),
+        "tl_kv_prefill_prepare": (i, [vp, vp, vp, i, vp]),
+        "tl_kv_prefill_info": (i, [vp, ip, ip]),
+        "tl_kv_prefill_append": (i, [vp, i, vp, vp, vp]),
+        "tl_kv_prefill_attention": (i, [vp, i, vp, vp, f, vp]),
+        "tl_kv_prefill_run": (i, [vp, i, vp, vp, vp, vp, f, vp]),
+        "tl_kv_prefill_commit": (i, [vp]),
         "tl_attn_set_score_path": (i, [i]),
         "tl_attn_get_score_path": (i, []),
         "tl_attn_set_waves": (i, [i]),
@@ -321,6 +332,62 @@ class DecodeBatch:
     def commit(self, num_tokens=1):
         """advanceSeqLen(seq, num_tokens) for every sequence of the last prepare."""
         _check(load().tl_kv_batch_commit(self._h, num_tokens))
+
+
+class PrefillBatch:
+    """tiny_llm::PrefillBatch: new tokens of several sequences appended and
+    attended causally over the cache (tl_kv_prefill_*)."""
+
+    def __init__(self, mgr: KVCacheManager, max_seqs: int, num_q_heads: int):
+        self.mgr = mgr
+        self._h = C.c_void_p()
+        _check(load().tl_kv_prefill_create(mgr._h, max_seqs, num_q_heads, C.byref(self._h)))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            load().tl_kv_prefill_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def prepare(self, seq_ids, num_tokens, stream=0):
+        n = len(seq_ids)
+        ids = (C.c_int * max(1, n))(*seq_ids)
+        cnt = (C.c_int * max(1, n))(*num_tokens)
+        _check(load().tl_kv_prefill_prepare(self._h, ids, cnt, n, stream))
+
+    def info(self):
+        n, t = C.c_int(), C.c_int()
+        _check(load().tl_kv_prefill_info(self._h, C.byref(n), C.byref(t)))
+        return {"n": n.value, "tokens": t.value}
+
+    def append(self, layer, new_k, new_v, stream=0):
+        _check(load().tl_kv_prefill_append(self._h, layer, new_k, new_v, stream))
+
+    def attention(self, layer, q, out, scale, stream=0):
+        _check(load().tl_kv_prefill_attention(self._h, layer, q, out, scale, stream))
+
+    def run(self, layer, q, new_k, new_v, out, scale, stream=0):
+        _check(load().tl_kv_prefill_run(self._h, layer, q, new_k, new_v, out, scale, stream))
+
+    def commit(self):
+        _check(load().tl_kv_prefill_commit(self._h))
+
+
+def attention_prefill(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, stream=0):
+    """kernels::attention_prefill: compact [B][H][S][D], causal."""
+    load().tl_attention_prefill(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, stream)
+
+
+def softmax(inp, out, batch, seq_len, stream=0):
+    load().tl_softmax(inp, out, batch, seq_len, stream)
+
+
+def get_attention_weights(q, k, w, scale, batch, num_heads, query_len, key_len, head_dim, causal,
+                          stream=0):
+    load().tl_get_attention_weights(q, k, w, scale, batch, num_heads, query_len, key_len, head_dim,
+                                    int(causal), stream)
 
 
 def attn_decode_gqa(q, view: KVView, seq_lens, Hq, Hkv, D, scale, out, stream=0):
