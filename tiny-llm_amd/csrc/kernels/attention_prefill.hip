@@ -11,20 +11,22 @@
 // from the cache instead of the current token batch, and equal to decode
 // attention over the first p0+i+1 keys.
 //
-// Workgroup: 4 waves, one kv head g, 64 query rows = 64/G tokens x G heads;
-// wave w owns rows 16w..16w+15.  Keys stream in tiles of 64 tokens through
-// LDS: K row-major, V transposed ([d][token]).  Per wave and tile:
+// Workgroup: 4 waves, one kv head g, 128 query rows = 128/G tokens x G heads
+// (64 rows for head_dim 256); each wave owns two (one) 16-row query column
+// groups.  Keys stream in tiles of 64 tokens through double-buffered LDS:
+// K row-major, V transposed ([d][token]).  Per wave, group and tile:
 //   S^T = K Q^T        v_mfma_f32_16x16x32_f16: A = K rows (token l%16,
 //                      dims 8(l/16)..+7), B = Q (query l%16, same dims),
 //                      D = S^T (tokens 4(l/16)+i, query l%16)
 //   online softmax     per query column, over the lane's 16 scores and the
 //                      4 lanes sharing the column (xor 16, 32)
-//   O^T += V^T P^T     v_mfma_f32_16x16x16_f16: A = V^T (dim l%16, tokens
-//                      4(l/16)..+3) from the transposed tile, B = P^T,
-//                      which is the fp16 S^T fragment as it stands (tokens
-//                      4(l/16)+j, query l%16); D = O^T (dims 4(l/16)+i,
-//                      query l%16), so the rescale by the running max is
-//                      lane-local.
+//   O^T += V^T P^T     v_mfma_f32_16x16x32_f16 over 32 keys: B = P^T is the
+//                      fp16 S^T fragments of two key tiles as they stand
+//                      (k index 8(l/16)+j names key 4(l/16)+j of the first
+//                      tile for j < 4, of the second for j >= 4); A = V^T
+//                      (dim l%16) read from the transposed tile in that key
+//                      order; D = O^T (dims 4(l/16)+i, query l%16), so the
+//                      rescale by the running max is lane-local.
 // The next tile's K/V rows are loaded into registers while the current one
 // is computed.  Grid: work items x Hkv, kv head fastest, so with 8 kv heads
 // every workgroup of head g runs on XCD g and the tiles it re-reads stay in
@@ -100,6 +102,12 @@ struct KeyRows {
 
 __device__ __forceinline__ uint4 ld16(const char *p) { return *reinterpret_cast<const uint4 *>(p); }
 
+// 16-query column groups per wave: two share every K and V^T fragment read
+// from LDS (half the LDS traffic per flop); head_dim 256 keeps one to fit
+// the register file.
+template <int D>
+constexpr int kQueryGroups = D <= 128 ? 2 : 1;
+
 // Rounds x to fp32 in a register before whatever consumes it: keeps the
 // compiler from folding a multiply into the fp16 conversion that follows
 // (v_fma_mixlo_f16 rounds once, the reference's __float2half(a * b) twice).
@@ -109,20 +117,26 @@ __device__ __forceinline__ float materialize(float x) {
 }
 
 template <int D, int G, bool PAGED>
-__global__ __launch_bounds__(kPThreads) void attn_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel(PrefillArgs a) {
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
-    constexpr int BQ = 64 / G;         // query tokens per workgroup
-    constexpr int KS = D / 32;         // k steps of S^T
-    constexpr int DT = D / 16;         // dim tiles of O^T
-    constexpr int KP = D / 8;          // 16-byte pieces per row
-    constexpr int KPITCH = D + 8;      // halves per LDS K row
-    constexpr int VPITCH = kKeyTile + 8; // halves per LDS V^T row
-    constexpr int NKI = kKeyTile * KP / kPThreads;               // K pieces per thread
-    constexpr int VITEMS = (kKeyTile / 4) * KP;                  // (4-token group, piece) items
-    constexpr int NVI = (VITEMS + kPThreads - 1) / kPThreads;    // per thread
-    __shared__ __align__(16) uint16_t ks[kKeyTile * KPITCH];
-    __shared__ __align__(16) uint16_t vt[D * VPITCH];
+    constexpr int NQG = kQueryGroups<D>;    // 16-query column groups per wave
+    constexpr int ROWS = 4 * 16 * NQG;      // query rows per workgroup
+    constexpr int BQ = ROWS / G;            // query tokens per workgroup
+    constexpr int KS = D / 32;              // k steps of S^T
+    constexpr int DT = D / 16;              // dim tiles of O^T
+    constexpr int KP = D / 8;               // 16-byte pieces per row
+    constexpr int KPITCH = D + 8;           // halves per LDS K row
+    constexpr int VPITCH = kKeyTile + 8;    // halves per LDS V^T row
+    constexpr int NKI = kKeyTile * KP / kPThreads;            // K pieces per thread
+    constexpr int VITEMS = (kKeyTile / 4) * KP;               // (4-token group, piece) items
+    constexpr int NVI = (VITEMS + kPThreads - 1) / kPThreads; // per thread
+    __shared__ __align__(16) uint16_t ks[2][kKeyTile * KPITCH];
+    __shared__ __align__(16) uint16_t vt[2][D * VPITCH];
+    // Column of key t in V^T row d: rotated by 4 * ((d / 8) % 16) keys, so the
+    // 16 lanes that store rows 8pc + 2w (pc = 0..15) hit distinct banks;
+    // 4-key chunks stay contiguous and aligned.
+    auto vcol = [](int d, int t) { return (t + 4 * ((d >> 3) & 15)) & (kKeyTile - 1); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int item = blockIdx.x / a.Hkv;
@@ -147,56 +161,71 @@ __global__ __launch_bounds__(kPThreads) void attn_prefill_kernel(PrefillArgs a) 
         row = b;
     }
     const int c = lane & 15, qg = lane >> 4;
-    const int r = wave * 16 + c;          // query row of this lane's column
-    const int qi = qt * BQ + r / G;       // query token within the entry
-    const int h = g * G + r % G;
-    const bool valid = qi < n;
-    const int qic = valid ? qi : n - 1;
-    const int pos = p0 + qic;             // keys 0 .. pos are attended
     const int kend = p0 + min(n, (qt + 1) * BQ);
     const int ntile = (kend + kKeyTile - 1) / kKeyTile;
-
-    const KeyRows<PAGED> kr(a.kv, row, g);
-
-    // Q fragments (B operand of S^T): query column c, dims 32ks + 8qg .. +7.
-    f16x8 qb[KS];
-    {
-        const char *qp = reinterpret_cast<const char *>(a.q + q_off + (int64_t)qic * a.q_tok +
-                                                        (int64_t)h * a.q_head);
+    int       pos[NQG];  // keys 0 .. pos are attended by the lane's query column
+    bool      valid[NQG];
+    int64_t   qrow[NQG]; // element offset of the column's query row
+    f16x8     qb[NQG][KS];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) qb[s] = __builtin_bit_cast(f16x8, ld16(qp + 2 * (32 * s + 8 * qg)));
+    for (int j = 0; j < NQG; ++j) {
+        const int r = wave * 16 * NQG + j * 16 + c;
+        const int qi = qt * BQ + r / G;
+        const int h = g * G + r % G;
+        valid[j] = qi < n;
+        const int qic = valid[j] ? qi : n - 1;
+        pos[j] = p0 + qic;
+        qrow[j] = q_off + (int64_t)qic * a.q_tok + (int64_t)h * a.q_head;
+        // B operand of S^T: query column c, dims 32s + 8qg .. +7
+        const char *qp = reinterpret_cast<const char *>(a.q + qrow[j]);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qb[j][s] = __builtin_bit_cast(f16x8, ld16(qp + 2 * (32 * s + 8 * qg)));
     }
 
+    // Smallest attended position of the wave's queries: tiles ending at or
+    // below it need no causal mask.
+    int wave_min_pos = pos[0];
+#pragma unroll
+    for (int j = 1; j < NQG; ++j) wave_min_pos = min(wave_min_pos, pos[j]);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) wave_min_pos = min(wave_min_pos, __shfl_xor(wave_min_pos, o));
+    wave_min_pos = __builtin_amdgcn_readfirstlane(wave_min_pos);
+
+    const KeyRows<PAGED> kr(a.kv, row, g);
     uint4 kreg[NKI];
     uint4 vreg[NVI][4];
+    // Token and piece of every row piece this thread stages (fixed per tile).
+    auto k_tok = [&](int u) { return (tid + u * kPThreads) / KP; };
+    auto k_pc = [&](int u) { return (tid + u * kPThreads) % KP; };
+    auto v_tg = [&](int u) { return (tid + u * kPThreads) / KP; };
+    // Byte offset of token t's row piece pc: 32 bits for a contiguous row
+    // (the host checks that the rows of one cache row span < 4 GiB).
+    auto roff = [&](int t, int pc) -> int64_t {
+        if constexpr (PAGED) return kr.off(t) + 16 * pc;
+        else return (uint32_t)t * (uint32_t)kr.tok_bytes + (uint32_t)(16 * pc);
+    };
     auto load_tile = [&](int kt) {
         const int t0 = kt * kKeyTile;
 #pragma unroll
-        for (int u = 0; u < NKI; ++u) {
-            const int it = tid + u * kPThreads;
-            const int tk = it / KP, pc = it - tk * KP;
-            const int t = min(t0 + tk, kend - 1);
-            kreg[u] = ld16(kr.kbase + kr.off(t) + 16 * pc);
-        }
+        for (int u = 0; u < NKI; ++u)
+            kreg[u] = ld16(kr.kbase + roff(min(t0 + k_tok(u), kend - 1), k_pc(u)));
 #pragma unroll
         for (int u = 0; u < NVI; ++u) {
-            const int it = tid + u * kPThreads;
-            if (VITEMS % kPThreads == 0 || it < VITEMS) {
-                const int tg = it / KP, pc = it - tg * KP;
+            if (VITEMS % kPThreads == 0 || tid + u * kPThreads < VITEMS) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int t = min(t0 + 4 * tg + j, kend - 1);
-                    vreg[u][j] = ld16(kr.vbase + kr.off(t) + 16 * pc);
-                }
+                for (int j = 0; j < 4; ++j)
+                    vreg[u][j] = ld16(kr.vbase + roff(min(t0 + 4 * v_tg(u) + j, kend - 1), k_pc(u)));
             }
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
+        uint16_t *kd = ks[buf];
+        uint16_t *vd = vt[buf];
 #pragma unroll
         for (int u = 0; u < NKI; ++u) {
             const int it = tid + u * kPThreads;
             const int tk = it / KP, pc = it - tk * KP;
-            *reinterpret_cast<uint4 *>(&ks[tk * KPITCH + 8 * pc]) = kreg[u];
+            *reinterpret_cast<uint4 *>(&kd[tk * KPITCH + 8 * pc]) = kreg[u];
         }
 #pragma unroll
         for (int u = 0; u < NVI; ++u) {
@@ -214,89 +243,151 @@ __global__ __launch_bounds__(kPThreads) void attn_prefill_kernel(PrefillArgs a) 
                                                 __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u));
                     const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u),
                                                 __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u));
-                    *reinterpret_cast<uint2 *>(&vt[(8 * pc + 2 * w) * VPITCH + 4 * tg]) = lo;
-                    *reinterpret_cast<uint2 *>(&vt[(8 * pc + 2 * w + 1) * VPITCH + 4 * tg]) = hi;
+                    const int r0 = 8 * pc + 2 * w;
+                    *reinterpret_cast<uint2 *>(&vd[r0 * VPITCH + vcol(r0, 4 * tg)]) = lo;
+                    *reinterpret_cast<uint2 *>(&vd[(r0 + 1) * VPITCH + vcol(r0 + 1, 4 * tg)]) = hi;
                 }
             }
         }
     };
 
-    f32x4 acc[DT];
+    f32x4 acc[NQG][DT];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -INFINITY, l_run = 0.0f;
+    for (int j = 0; j < NQG; ++j)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[j][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run[NQG], l_run[NQG];
+#pragma unroll
+    for (int j = 0; j < NQG; ++j) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.0f;
+    }
 
     load_tile(0);
+    store_tile(0);
+    __syncthreads();
     for (int kt = 0; kt < ntile; ++kt) {
-        store_tile();
-        __syncthreads();
+        const int       buf = kt & 1;
+        const uint16_t *kd = ks[buf];
+        const uint16_t *vd = vt[buf];
         if (kt + 1 < ntile) load_tile(kt + 1); // in flight during this tile's math
 
-        // ---- S^T = K Q^T, 16 keys x 16 queries per fragment
-        f32x4 s[4];
+        // ---- S^T = K Q^T: 16 keys x 16 queries per fragment; one K
+        // fragment serves every query group of the wave
+        // (two key tiles at a time: 2 x NQG independent accumulators per k
+        // step keep the MFMA pipeline busy within the register budget)
+        f32x4 s[NQG][4];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            s[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int j = 0; j < NQG; ++j) s[j][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int th = 0; th < 4; th += 2)
 #pragma unroll
             for (int st = 0; st < KS; ++st) {
-                const f16x8 kf = *reinterpret_cast<const f16x8 *>(&ks[(16 * tt + c) * KPITCH + 32 * st + 8 * qg]);
-                s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qb[st], s[tt], 0, 0, 0);
+                f16x8 kf[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    kf[u] = *reinterpret_cast<const f16x8 *>(&kd[(16 * (th + u) + c) * KPITCH + 32 * st + 8 * qg]);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int j = 0; j < NQG; ++j)
+                        s[j][th + u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u], qb[j][st], s[j][th + u], 0, 0, 0);
             }
-        }
-        // ---- causal mask, online softmax of the query column
+        // ---- causal mask (only tiles that reach past a query of the wave),
+        // online softmax per query column in the log2 domain:
+        // m = scale_log2 * max s, p = 2^(s * scale_log2 - m) by one FMA.
         const int tb = kt * kKeyTile + 4 * qg;
-        float     mloc = -INFINITY;
+        f16x8     pf[NQG][2]; // P^T as the B operand of a 32-key step (see below)
+        if (kt * kKeyTile + kKeyTile - 1 > wave_min_pos) {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+            for (int j = 0; j < NQG; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x = tb + 16 * tt + i <= pos ? s[tt][i] * a.scale_log2 : -INFINITY;
-                s[tt][i] = x;
-                mloc = fmaxf(mloc, x);
+                for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (tb + 16 * tt + i > pos[j]) s[j][tt][i] = -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < NQG; ++j) {
+            float mloc = fmaxf(fmaxf(fmaxf(s[j][0][0], s[j][0][1]), fmaxf(s[j][0][2], s[j][0][3])),
+                               fmaxf(fmaxf(s[j][1][0], s[j][1][1]), fmaxf(s[j][1][2], s[j][1][3])));
+            mloc = fmaxf(mloc, fmaxf(fmaxf(fmaxf(s[j][2][0], s[j][2][1]), fmaxf(s[j][2][2], s[j][2][3])),
+                                     fmaxf(fmaxf(s[j][3][0], s[j][3][1]), fmaxf(s[j][3][2], s[j][3][3]))));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            // Key 0 lies in tile 0 and every query attends it, so m_new is finite.
+            const float m_new = fmaxf(m_run[j], mloc * a.scale_log2);
+            const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+            // The running sums need rescaling only when some column's max moved.
+            if (__any(m_new != m_run[j])) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) acc[j][dt] *= alpha;
+                l_run[j] *= alpha;
             }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        // Key 0 lies in tile 0 and is attended by every query, so m_new is finite.
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        float psum = 0.0f;
-        f16x4 pf[4];
+            m_run[j] = m_new;
+            float psum = 0.0f;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+            for (int tt = 0; tt < 4; ++tt) {
+                float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(s[tt][i] - m_new);
-                psum += p;
-                pf[tt][i] = (_Float16)p;
+                for (int i = 0; i < 4; ++i) {
+                    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][tt][i], a.scale_log2, -m_new));
+                    psum += p[i];
+                }
+                const uint32_t lo = __builtin_bit_cast(uint32_t, __floats2half2_rn(p[0], p[1]));
+                const uint32_t hi = __builtin_bit_cast(uint32_t, __floats2half2_rn(p[2], p[3]));
+                uint4 w = __builtin_bit_cast(uint4, pf[j][tt >> 1]);
+                if (tt & 1) {
+                    w.z = lo;
+                    w.w = hi;
+                } else {
+                    w.x = lo;
+                    w.y = hi;
+                }
+                pf[j][tt >> 1] = __builtin_bit_cast(f16x8, w);
             }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-        // ---- O^T += V^T P^T
+            l_run[j] += psum;
+        }
+        // ---- O^T += V^T P^T on v_mfma_f32_16x16x32_f16 over 32 keys per
+        // step.  Lane group qg's k index 8qg+j stands for key 32tp + 4qg + j
+        // (j < 4) or 32tp + 16 + 4qg + j - 4 (j >= 4): the keys its S^T
+        // fragments of tiles 2tp and 2tp+1 hold, so P^T needs no data
+        // movement; the V^T fragment is read with the same key order.
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const f16x4 vf = *reinterpret_cast<const f16x4 *>(&vt[(16 * dt + c) * VPITCH + 16 * tt + 4 * qg]);
-                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pf[tt], acc[dt], 0, 0, 0);
+            for (int tp = 0; tp < 2; ++tp) {
+                const int       vrow = 16 * dt + c;
+                const uint16_t *vr = &vd[vrow * VPITCH];
+                const uint2     v0 = *reinterpret_cast<const uint2 *>(vr + vcol(vrow, 32 * tp + 4 * qg));
+                const uint2     v1 = *reinterpret_cast<const uint2 *>(vr + vcol(vrow, 32 * tp + 16 + 4 * qg));
+                const f16x8     vf = __builtin_bit_cast(f16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+#pragma unroll
+                for (int j = 0; j < NQG; ++j)
+                    acc[j][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][tp], acc[j][dt], 0, 0, 0);
             }
-        __syncthreads(); // the tile's LDS is rewritten next
+        if (kt + 1 < ntile) store_tile(buf ^ 1);
+        __syncthreads(); // the next tile is in LDS; this tile's buffer is free
     }
 
-    float l = l_run + __shfl_xor(l_run, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / (l + 1e-6f);
-    if (valid) {
-        __half *op = a.out + q_off + (int64_t)qi * a.q_tok + (int64_t)h * a.q_head + 4 * qg;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const __half2 lo = __floats2half2_rn(acc[dt][0] * inv, acc[dt][1] * inv);
-            const __half2 hi = __floats2half2_rn(acc[dt][2] * inv, acc[dt][3] * inv);
-            uint2         w;
-            w.x = __builtin_bit_cast(uint32_t, lo);
-            w.y = __builtin_bit_cast(uint32_t, hi);
-            *reinterpret_cast<uint2 *>(op + 16 * dt) = w;
+    for (int j = 0; j < NQG; ++j) {
+        float l = l_run[j] + __shfl_xor(l_run[j], 16);
+        l += __shfl_xor(l, 32);
+        const float inv = 1.0f / (l + 1e-6f);
+        if (valid[j]) {
+            __half *op = a.out + qrow[j] + 4 * qg;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const __half2 lo = __floats2half2_rn(acc[j][dt][0] * inv, acc[j][dt][1] * inv);
+                const __half2 hi = __floats2half2_rn(acc[j][dt][2] * inv, acc[j][dt][3] * inv);
+                uint2         w;
+                w.x = __builtin_bit_cast(uint32_t, lo);
+                w.y = __builtin_bit_cast(uint32_t, hi);
+                *reinterpret_cast<uint2 *>(op + 16 * dt) = w;
+            }
         }
     }
 }
@@ -371,8 +462,8 @@ bool prefill_shape_supported(int D, int G) {
     return (D == 32 || D == 64 || D == 128 || D == 256) && (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
-void plan_prefill(const PrefillEntry *entries, int n, int G, std::vector<int32_t> &work) {
-    const int BQ = prefill_block_tokens(G);
+void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<int32_t> &work) {
+    const int BQ = prefill_block_tokens(D, G);
     struct It {
         int64_t keys;
         int32_t e, qt;
@@ -398,7 +489,7 @@ void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int H
     if (p.entries) {
         items = p.n_items;
     } else {
-        const int BQ = prefill_block_tokens(G);
+        const int BQ = prefill_block_tokens(D, G);
         items = p.uniform_b * ((p.uniform_n + BQ - 1) / BQ);
     }
     if (items <= 0) return;

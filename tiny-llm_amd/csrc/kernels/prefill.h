@@ -29,13 +29,13 @@ struct PrefillEntry {
 
 static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
 
-// Query tokens per workgroup: 64 query rows of (token, head) pairs, G heads
-// of one kv group per token.
-inline int prefill_block_tokens(int G) { return 64 / G; }
+// Query tokens per workgroup: 128 query rows (64 for head_dim 256) of
+// (token, head) pairs, G heads of one kv group per token.
+inline int prefill_block_tokens(int D, int G) { return (D <= 128 ? 128 : 64) / G; }
 
 // Work items (entry, query tile), most keys first (LPT order for the
 // hardware dispatcher): work[2i], work[2i+1].
-void plan_prefill(const PrefillEntry *entries, int n, int G, std::vector<int32_t> &work);
+void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<int32_t> &work);
 
 struct PrefillLaunch {
     const __half       *q = nullptr;

@@ -789,7 +789,7 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
         mgr_.syncTable(stream);
     }
     std::vector<int32_t> work;
-    detail::plan_prefill(entries.data(), n, num_q_heads_ / cfg.num_heads, work);
+    detail::plan_prefill(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads, work);
     // Device copy: [entries (6 words each) | token rows T | token positions T | work].
     const size_t T = static_cast<size_t>(total);
     const size_t words = 6 * static_cast<size_t>(n) + 2 * T + work.size();
