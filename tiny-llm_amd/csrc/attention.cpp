@@ -141,6 +141,7 @@ std::string attn_prefill_compact(const __half *q, const __half *k, const __half 
     p.q_entry_stride = static_cast<int64_t>(H) * S * D;
     p.uniform_b = B;
     p.uniform_n = S;
+    p.max_keys = S;
     launch_attn_prefill(p, kv, H, H, D, scale, stream);
     return "";
 }

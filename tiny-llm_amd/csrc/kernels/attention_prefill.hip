@@ -39,6 +39,8 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <climits>
+#include <stdexcept>
 
 namespace tiny_llm {
 namespace detail {
@@ -509,6 +511,8 @@ void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int H
     const int64_t grid = (int64_t)items * Hkv;
     if (grid > INT32_MAX) throw std::invalid_argument("attention_prefill: too many work items");
     const bool paged = kv.block_table != nullptr;
+    if (!paged && (int64_t)p.max_keys * kv.tok_stride * 2 > (int64_t)UINT32_MAX)
+        throw std::invalid_argument("attention_prefill: token offsets exceed 32 bits (keys * row bytes)");
     profile_begin(KernelId::AttnPrefill, stream);
     switch (D) {
     case 32: launch_d<32>(a, (int)grid, G, paged, stream); break;

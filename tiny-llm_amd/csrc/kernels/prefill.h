@@ -51,12 +51,16 @@ struct PrefillLaunch {
     int                 uniform_b = 0;
     int                 uniform_n = 0;
     int64_t             q_entry_stride = 0;
+    // Largest p0 + n over the entries (the offset-width check of
+    // contiguous rows).
+    int                 max_keys = 0;
 };
 
 // True when (D, G) has a prefill kernel (D in {32,64,128,256}, G in {1,2,4,8}).
 bool prefill_shape_supported(int D, int G);
 
-// Throws HipException on launch failure.
+// Throws HipException on launch failure, std::invalid_argument when the
+// token offsets of a contiguous (non-paged) view do not fit in 32 bits.
 void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int Hkv, int D,
                          float scale, hipStream_t stream);
 

@@ -760,6 +760,7 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
     std::vector<int32_t> slots(static_cast<size_t>(n)), ends(static_cast<size_t>(n));
     std::vector<detail::PrefillEntry> entries(static_cast<size_t>(n));
     int64_t total = 0;
+    int     max_keys = 0;
     for (int i = 0; i < n; ++i) {
         const int            id = seq_ids[i];
         const SequenceCache *sc = mgr_.sequence(id);
@@ -777,6 +778,7 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
                                      std::to_string(nt) + ", max: " + std::to_string(sc->max_len));
         slots[static_cast<size_t>(i)] = slot;
         ends[static_cast<size_t>(i)] = sc->current_len + nt;
+        max_keys = std::max(max_keys, sc->current_len + nt);
         entries[static_cast<size_t>(i)] = {total * num_q_heads_ * cfg.head_dim, sc->current_len, nt,
                                            slot, 0};
         total += nt;
@@ -813,6 +815,7 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
     counts_.assign(num_tokens, num_tokens + n);
     n_ = n;
     tokens_ = static_cast<int>(total);
+    max_keys_ = max_keys;
     return Result<void>::ok();
 }
 
@@ -854,6 +857,7 @@ Result<void> PrefillBatch::attention(int layer_idx, const half *q, half *out, fl
     p.entries = d_entries_;
     p.work = d_work_;
     p.n_items = n_items_;
+    p.max_keys = max_keys_;
     detail::launch_attn_prefill(p, mgr_.layerView(layer_idx, nullptr), num_q_heads_, cfg.num_heads,
                                 cfg.head_dim, scale, stream);
     return Result<void>::ok();

@@ -255,6 +255,7 @@ class PrefillBatch {
     int                  n_ = 0;
     int                  tokens_ = 0;
     int                  n_items_ = 0;
+    int                  max_keys_ = 0;
     std::vector<int32_t> ids_, counts_;
     std::unique_ptr<detail::MetaRing> meta_;
     const int32_t       *d_tok_row_ = nullptr, *d_tok_pos_ = nullptr, *d_work_ = nullptr;
