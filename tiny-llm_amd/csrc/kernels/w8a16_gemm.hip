@@ -366,17 +366,58 @@ __global__ __launch_bounds__(256) void w8a16_pack_kernel(const int8_t *w, int K,
     *reinterpret_cast<uint2 *>(out + idx * 8) = make_uint2(lo, hi);
 }
 
-// Sums the split-K partials in split order and applies the epilogue.
+// The epilogue of four consecutive columns n..n+3 of one segment (n % 4 ==
+// 0; every segment of the MFMA path has n % 16 == 0): one 8-byte store, and
+// one cache-row lookup, per thread.
+__device__ __forceinline__ void epilogue4(const GemmArgs &a, int si, int m, int n, const float4 &v) {
+    const W8A16Seg &sg = a.seg[si];
+    const __half2   lo = __floats2half2_rn(v.x, v.y), hi = __floats2half2_rn(v.z, v.w);
+    __half         *dst;
+    if (sg.kind == kEpiCache) {
+        const CacheRows &c = a.cache;
+        const int        row = c.seq_row[m];
+        const int        t = c.wpos[m];
+        int64_t          off;
+        if (c.block_table) {
+            const int blk = c.block_table[(int64_t)row * c.bt_stride + (t >> c.log2_blk)];
+            off = (int64_t)blk * c.blk_stride + (int64_t)(t & ((1 << c.log2_blk) - 1)) * c.tok_stride;
+        } else {
+            off = (int64_t)row * c.blk_stride + (int64_t)t * c.tok_stride;
+        }
+        dst = sg.out + off + n;
+    } else {
+        dst = sg.out + (int64_t)m * sg.ld + n;
+    }
+    uint2 w = make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+    if (sg.kind == kEpiResidual) { // fp16(f(res) + f(fp16(acc))), element by element
+        const uint2   r = *reinterpret_cast<const uint2 *>(sg.res + (int64_t)m * sg.ld + n);
+        const __half2 rl = __builtin_bit_cast(__half2, r.x), rh = __builtin_bit_cast(__half2, r.y);
+        const __half2 sl = __floats2half2_rn(__low2float(rl) + __low2float(lo), __high2float(rl) + __high2float(lo));
+        const __half2 sh = __floats2half2_rn(__low2float(rh) + __low2float(hi), __high2float(rh) + __high2float(hi));
+        w = make_uint2(__builtin_bit_cast(uint32_t, sl), __builtin_bit_cast(uint32_t, sh));
+    }
+    *reinterpret_cast<uint2 *>(dst) = w;
+}
+
+// Sums the split-K partials in split order and applies the epilogue, four
+// consecutive columns per thread (16-byte partial loads).
 __global__ __launch_bounds__(256) void w8a16_reduce_kernel(GemmArgs a) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)a.M * a.ntot) return;
-    const int m = (int)(idx / a.ntot);
-    const int c = (int)(idx - (int64_t)m * a.ntot);
+    const int     q = a.ntot >> 2;
+    if (idx >= (int64_t)a.M * q) return;
+    const int m = (int)(idx / q);
+    const int c = 4 * (int)(idx - (int64_t)m * q);
     int       si = 0;
     while (si + 1 < a.nseg && c >= a.col0[si + 1]) ++si;
-    float v = 0.0f;
-    for (int s = 0; s < a.splits; ++s) v += a.partial[((int64_t)s * a.M + m) * a.ntot + c];
-    epilogue(a, si, m, c - a.col0[si], v);
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s = 0; s < a.splits; ++s) {
+        const float4 p = *reinterpret_cast<const float4 *>(a.partial + ((int64_t)s * a.M + m) * a.ntot + c);
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    epilogue4(a, si, m, c - a.col0[si], v);
 }
 
 // Reference-order fallback: one thread per (m, column), sequential k.
@@ -503,7 +544,7 @@ void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A1
     HIP_CHECK(hipGetLastError());
     profile_end(KernelId::W8A16, stream);
     if (splits > 1) {
-        const int64_t total = (int64_t)M * a.ntot;
+        const int64_t total = (int64_t)M * (a.ntot / 4);
         profile_begin(KernelId::W8A16Reduce, stream);
         hipLaunchKernelGGL(w8a16_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                            stream, a);
