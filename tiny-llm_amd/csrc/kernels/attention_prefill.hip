@@ -13,8 +13,8 @@
 //
 // Workgroup: 4 waves, one kv head g, 128 query rows = 128/G tokens x G heads
 // (64 rows for head_dim 256); each wave owns two (one) 16-row query column
-// groups.  Keys stream in tiles of 64 tokens through double-buffered LDS:
-// K row-major, V transposed ([d][token]).  Per wave, group and tile:
+// groups.  Keys stream in tiles of 64 tokens through double-buffered LDS,
+// K and V both row-major (16-byte stores).  Per wave, group and tile:
 //   S^T = K Q^T        v_mfma_f32_16x16x32_f16: A = K rows (token l%16,
 //                      dims 8(l/16)..+7), B = Q (query l%16, same dims),
 //                      D = S^T (tokens 4(l/16)+i, query l%16)
@@ -24,9 +24,10 @@
 //                      fp16 S^T fragments of two key tiles as they stand
 //                      (k index 8(l/16)+j names key 4(l/16)+j of the first
 //                      tile for j < 4, of the second for j >= 4); A = V^T
-//                      (dim l%16) read from the transposed tile in that key
-//                      order; D = O^T (dims 4(l/16)+i, query l%16), so the
-//                      rescale by the running max is lane-local.
+//                      (dim l%16) in that key order, read from the row-major
+//                      V tile with ds_read_b64_tr_b16 (gfx950's transposing
+//                      LDS read); D = O^T (dims 4(l/16)+i, query l%16), so
+//                      the rescale by the running max is lane-local.
 // The next tile's K/V rows are loaded into registers while the current one
 // is computed.  Grid: work items x Hkv, kv head fastest, so with 8 kv heads
 // every workgroup of head g runs on XCD g and the tiles it re-reads stay in
@@ -50,6 +51,13 @@ namespace {
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef short    s16x4 __attribute__((ext_vector_type(4)));
+
+// LDS (address space 3) view of a pointer into a __shared__ array, the
+// operand type of the transposing LDS read.
+__device__ __forceinline__ __attribute__((address_space(3))) s16x4 *lds_ptr(const uint16_t *p) {
+    return (__attribute__((address_space(3))) s16x4 *)(p);
+}
 
 constexpr int kPThreads = 256;
 constexpr int kKeyTile = 64;
@@ -129,16 +137,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     constexpr int DT = D / 16;              // dim tiles of O^T
     constexpr int KP = D / 8;               // 16-byte pieces per row
     constexpr int KPITCH = D + 8;           // halves per LDS K row
-    constexpr int VPITCH = kKeyTile + 8;    // halves per LDS V^T row
+    constexpr int VPITCH = D + 16;          // halves per LDS V row (8 banks between rows)
     constexpr int NKI = kKeyTile * KP / kPThreads;            // K pieces per thread
-    constexpr int VITEMS = (kKeyTile / 4) * KP;               // (4-token group, piece) items
-    constexpr int NVI = (VITEMS + kPThreads - 1) / kPThreads; // per thread
     __shared__ __align__(16) uint16_t ks[2][kKeyTile * KPITCH];
-    __shared__ __align__(16) uint16_t vt[2][D * VPITCH];
-    // Column of key t in V^T row d: rotated by 4 * ((d / 8) % 16) keys, so the
-    // 16 lanes that store rows 8pc + 2w (pc = 0..15) hit distinct banks;
-    // 4-key chunks stay contiguous and aligned.
-    auto vcol = [](int d, int t) { return (t + 4 * ((d >> 3) & 15)) & (kKeyTile - 1); };
+    __shared__ __align__(16) uint16_t vt[2][kKeyTile * VPITCH];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int item = blockIdx.x / a.Hkv;
@@ -195,11 +197,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
 
     const KeyRows<PAGED> kr(a.kv, row, g);
     uint4 kreg[NKI];
-    uint4 vreg[NVI][4];
+    uint4 vreg[NKI];
     // Token and piece of every row piece this thread stages (fixed per tile).
     auto k_tok = [&](int u) { return (tid + u * kPThreads) / KP; };
     auto k_pc = [&](int u) { return (tid + u * kPThreads) % KP; };
-    auto v_tg = [&](int u) { return (tid + u * kPThreads) / KP; };
     // Byte offset of token t's row piece pc: 32 bits for a contiguous row
     // (the host checks that the rows of one cache row span < 4 GiB).
     auto roff = [&](int t, int pc) -> int64_t {
@@ -212,13 +213,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
         for (int u = 0; u < NKI; ++u)
             kreg[u] = ld16(kr.kbase + roff(min(t0 + k_tok(u), kend - 1), k_pc(u)));
 #pragma unroll
-        for (int u = 0; u < NVI; ++u) {
-            if (VITEMS % kPThreads == 0 || tid + u * kPThreads < VITEMS) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    vreg[u][j] = ld16(kr.vbase + roff(min(t0 + 4 * v_tg(u) + j, kend - 1), k_pc(u)));
-            }
-        }
+        for (int u = 0; u < NKI; ++u)
+            vreg[u] = ld16(kr.vbase + roff(min(t0 + k_tok(u), kend - 1), k_pc(u)));
     };
     auto store_tile = [&](int buf) {
         uint16_t *kd = ks[buf];
@@ -230,27 +226,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
             *reinterpret_cast<uint4 *>(&kd[tk * KPITCH + 8 * pc]) = kreg[u];
         }
 #pragma unroll
-        for (int u = 0; u < NVI; ++u) {
-            const int it = tid + u * kPThreads;
-            if (VITEMS % kPThreads == 0 || it < VITEMS) {
-                const int      tg = it / KP, pc = it - tg * KP;
-                const uint32_t w0[4] = {vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w};
-                const uint32_t w1[4] = {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w};
-                const uint32_t w2[4] = {vreg[u][2].x, vreg[u][2].y, vreg[u][2].z, vreg[u][2].w};
-                const uint32_t w3[4] = {vreg[u][3].x, vreg[u][3].y, vreg[u][3].z, vreg[u][3].w};
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    // dims 8pc+2w (low halves) and 8pc+2w+1 (high halves) of tokens 4tg..4tg+3
-                    const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[w], w0[w], 0x05040100u),
-                                                __builtin_amdgcn_perm(w3[w], w2[w], 0x05040100u));
-                    const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[w], w0[w], 0x07060302u),
-                                                __builtin_amdgcn_perm(w3[w], w2[w], 0x07060302u));
-                    const int r0 = 8 * pc + 2 * w;
-                    *reinterpret_cast<uint2 *>(&vd[r0 * VPITCH + vcol(r0, 4 * tg)]) = lo;
-                    *reinterpret_cast<uint2 *>(&vd[(r0 + 1) * VPITCH + vcol(r0 + 1, 4 * tg)]) = hi;
-                }
-            }
-        }
+        for (int u = 0; u < NKI; ++u)
+            *reinterpret_cast<uint4 *>(&vd[k_tok(u) * VPITCH + 8 * k_pc(u)]) = vreg[u];
     };
 
     f32x4 acc[NQG][DT];
@@ -361,11 +338,17 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp) {
-                const int       vrow = 16 * dt + c;
-                const uint16_t *vr = &vd[vrow * VPITCH];
-                const uint2     v0 = *reinterpret_cast<const uint2 *>(vr + vcol(vrow, 32 * tp + 4 * qg));
-                const uint2     v1 = *reinterpret_cast<const uint2 *>(vr + vcol(vrow, 32 * tp + 16 + 4 * qg));
-                const f16x8     vf = __builtin_bit_cast(f16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+                // Transposing LDS reads: lane s of each 16-lane group names
+                // the 4 dims 16dt + 4(s%4) .. +3 of key row 32tp + 4qg + s/4
+                // (+16 for the second read); lane i then holds dim 16dt + i
+                // of keys 32tp + 4qg + j (j = 0..3), the A fragment in the key
+                // order above.
+                const uint16_t *vr = &vd[(32 * tp + 4 * qg + (c >> 2)) * VPITCH + 16 * dt + 4 * (c & 3)];
+                const s16x4     v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(vr));
+                const s16x4     v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(vr + 16 * VPITCH));
+                const f16x8     vf = __builtin_bit_cast(
+                    f16x8, make_uint4(__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
+                                      __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y));
 #pragma unroll
                 for (int j = 0; j < NQG; ++j)
                     acc[j][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][tp], acc[j][dt], 0, 0, 0);
