@@ -19,7 +19,9 @@
 //                      dims 8(l/16)..+7), B = Q (query l%16, same dims),
 //                      D = S^T (tokens 4(l/16)+i, query l%16)
 //   online softmax     per query column, over the lane's 16 scores and the
-//                      4 lanes sharing the column (xor 16, 32)
+//                      4 lanes sharing the column (xor 16, 32); the reference
+//                      max moves only on jumps > 8 (log2), so the running
+//                      sums are rarely rescaled
 //   O^T += V^T P^T     v_mfma_f32_16x16x32_f16 over 32 keys: B = P^T is the
 //                      fp16 S^T fragments of two key tiles as they stand
 //                      (k index 8(l/16)+j names key 4(l/16)+j of the first
@@ -60,6 +62,10 @@ __device__ __forceinline__ __attribute__((address_space(3))) s16x4 *lds_ptr(cons
 }
 
 constexpr int kPThreads = 256;
+// Lazy rescaling threshold of the online softmax, in log2 units.
+constexpr float kLazyMax = 8.0f;
+// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt == 0 only.
+constexpr int kVmcnt0 = 0x0F70;
 constexpr int kKeyTile = 64;
 
 struct PrefillArgs {
@@ -136,11 +142,17 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     constexpr int KS = D / 32;              // k steps of S^T
     constexpr int DT = D / 16;              // dim tiles of O^T
     constexpr int KP = D / 8;               // 16-byte pieces per row
-    constexpr int KPITCH = D + 8;           // halves per LDS K row
-    constexpr int VPITCH = D + 16;          // halves per LDS V row (8 banks between rows)
+    constexpr int ROWH = D;                 // halves per LDS row (unpadded, swizzled)
     constexpr int NKI = kKeyTile * KP / kPThreads;            // K pieces per thread
-    __shared__ __align__(16) uint16_t ks[2][kKeyTile * KPITCH];
-    __shared__ __align__(16) uint16_t vt[2][kKeyTile * VPITCH];
+    // Two buffers per operand as distinct arrays, so the compiler can tell
+    // that the DMA into one does not alias the reads of the other and does
+    // not wait for it before computing.
+    __shared__ __align__(16) uint16_t ks0[kKeyTile * ROWH], ks1[kKeyTile * ROWH];
+    __shared__ __align__(16) uint16_t vt0[kKeyTile * ROWH], vt1[kKeyTile * ROWH];
+    // 16-byte piece x of key row r sits at slot x ^ (r % KP) of the row: the
+    // 16 rows a fragment read touches then fall on distinct banks without
+    // padding, so each wave's DMA of 1 KB lands contiguous.
+    auto slot = [](int r, int x) { return r * KP + (x ^ (r & (KP - 1))); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int item = blockIdx.x / a.Hkv;
@@ -196,38 +208,32 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     wave_min_pos = __builtin_amdgcn_readfirstlane(wave_min_pos);
 
     const KeyRows<PAGED> kr(a.kv, row, g);
-    uint4 kreg[NKI];
-    uint4 vreg[NKI];
-    // Token and piece of every row piece this thread stages (fixed per tile).
-    auto k_tok = [&](int u) { return (tid + u * kPThreads) / KP; };
-    auto k_pc = [&](int u) { return (tid + u * kPThreads) % KP; };
     // Byte offset of token t's row piece pc: 32 bits for a contiguous row
     // (the host checks that the rows of one cache row span < 4 GiB).
     auto roff = [&](int t, int pc) -> int64_t {
         if constexpr (PAGED) return kr.off(t) + 16 * pc;
         else return (uint32_t)t * (uint32_t)kr.tok_bytes + (uint32_t)(16 * pc);
     };
-    auto load_tile = [&](int kt) {
+    // Tile kt of K and V straight from global memory into LDS buffer buf
+    // (global_load_lds, 16 bytes per lane): thread t fills slots
+    // u*256 + t, i.e. every wave instruction one contiguous 1 KB of the tile;
+    // slot s holds row s / KP, piece (s % KP) ^ (row % KP).  Completion is
+    // tracked by vmcnt.
+    auto issue_tile = [&](int kt, uint16_t *kdst, uint16_t *vdst) {
         const int t0 = kt * kKeyTile;
 #pragma unroll
-        for (int u = 0; u < NKI; ++u)
-            kreg[u] = ld16(kr.kbase + roff(min(t0 + k_tok(u), kend - 1), k_pc(u)));
-#pragma unroll
-        for (int u = 0; u < NKI; ++u)
-            vreg[u] = ld16(kr.vbase + roff(min(t0 + k_tok(u), kend - 1), k_pc(u)));
-    };
-    auto store_tile = [&](int buf) {
-        uint16_t *kd = ks[buf];
-        uint16_t *vd = vt[buf];
-#pragma unroll
         for (int u = 0; u < NKI; ++u) {
-            const int it = tid + u * kPThreads;
-            const int tk = it / KP, pc = it - tk * KP;
-            *reinterpret_cast<uint4 *>(&kd[tk * KPITCH + 8 * pc]) = kreg[u];
+            const int sl = u * kPThreads + tid;
+            const int r = sl / KP, x = (sl % KP) ^ (r & (KP - 1));
+            const int64_t off = roff(min(t0 + r, kend - 1), x);
+            const int lbase = (u * kPThreads + wave * 64) * 8; // halves, wave-uniform
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(kr.kbase + off),
+                (__attribute__((address_space(3))) void *)(&kdst[lbase]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(kr.vbase + off),
+                (__attribute__((address_space(3))) void *)(&vdst[lbase]), 16, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < NKI; ++u)
-            *reinterpret_cast<uint4 *>(&vd[k_tok(u) * VPITCH + 8 * k_pc(u)]) = vreg[u];
     };
 
     f32x4 acc[NQG][DT];
@@ -242,14 +248,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
         l_run[j] = 0.0f;
     }
 
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < ntile; ++kt) {
-        const int       buf = kt & 1;
-        const uint16_t *kd = ks[buf];
-        const uint16_t *vd = vt[buf];
-        if (kt + 1 < ntile) load_tile(kt + 1); // in flight during this tile's math
+    // One tile: issue the next tile's DMA into the other buffers, compute on
+    // kd/vd, wait for the DMA, barrier.
+    auto tile_step = [&](int kt, const uint16_t *kd, const uint16_t *vd, uint16_t *kn, uint16_t *vn)
+                         __attribute__((always_inline)) {
+        // the next tile lands in the other buffer during this tile's math
+        if (kt + 1 < ntile) issue_tile(kt + 1, kn, vn);
 
         // ---- S^T = K Q^T: 16 keys x 16 queries per fragment; one K
         // fragment serves every query group of the wave
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
                 f16x8 kf[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
-                    kf[u] = *reinterpret_cast<const f16x8 *>(&kd[(16 * (th + u) + c) * KPITCH + 32 * st + 8 * qg]);
+                    kf[u] = *reinterpret_cast<const f16x8 *>(&kd[slot(16 * (th + u) + c, 4 * st + qg) * 8]);
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -296,16 +300,23 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
                                      fmaxf(fmaxf(s[j][3][0], s[j][3][1]), fmaxf(s[j][3][2], s[j][3][3]))));
             mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-            // Key 0 lies in tile 0 and every query attends it, so m_new is finite.
-            const float m_new = fmaxf(m_run[j], mloc * a.scale_log2);
-            const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
-            // The running sums need rescaling only when some column's max moved.
-            if (__any(m_new != m_run[j])) {
+            // Key 0 lies in tile 0 and every query attends it, so the max is
+            // finite from the first tile on.  The reference point m_run only
+            // moves when the max passes it by more than kLazyMax (log2
+            // units): until then p = 2^(x - m_run) <= 2^kLazyMax, exact in
+            // fp32 and fp16 range, and the final division by l cancels the
+            // shift, so the running sums are rescaled only on such jumps
+            // (once or twice per row instead of on most tiles).
+            const float m_tile = mloc * a.scale_log2;
+            if (__any(m_tile > m_run[j] + kLazyMax)) {
+                const float m_new = fmaxf(m_run[j], m_tile);
+                const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) acc[j][dt] *= alpha;
                 l_run[j] *= alpha;
+                m_run[j] = m_new;
             }
-            m_run[j] = m_new;
+            const float m_new = m_run[j];
             float psum = 0.0f;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -343,9 +354,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
                 // (+16 for the second read); lane i then holds dim 16dt + i
                 // of keys 32tp + 4qg + j (j = 0..3), the A fragment in the key
                 // order above.
-                const uint16_t *vr = &vd[(32 * tp + 4 * qg + (c >> 2)) * VPITCH + 16 * dt + 4 * (c & 3)];
-                const s16x4     v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(vr));
-                const s16x4     v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(vr + 16 * VPITCH));
+                const int       vr0 = 32 * tp + 4 * qg + (c >> 2), vx = 2 * dt + ((c & 3) >> 1);
+                const int       vh = 4 * (c & 1); // half offset within the 16-byte piece
+                const s16x4     v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(&vd[slot(vr0, vx) * 8 + vh]));
+                const s16x4     v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(&vd[slot(vr0 + 16, vx) * 8 + vh]));
                 const f16x8     vf = __builtin_bit_cast(
                     f16x8, make_uint4(__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
                                       __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y));
@@ -353,8 +365,15 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
                 for (int j = 0; j < NQG; ++j)
                     acc[j][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][tp], acc[j][dt], 0, 0, 0);
             }
-        if (kt + 1 < ntile) store_tile(buf ^ 1);
-        __syncthreads(); // the next tile is in LDS; this tile's buffer is free
+        __builtin_amdgcn_s_waitcnt(kVmcnt0); // this wave's part of the next tile has landed
+        __syncthreads();                      // ... every wave's, and this tile's buffer is free
+    };
+    issue_tile(0, ks0, vt0);
+    __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __syncthreads();
+    for (int kt = 0; kt < ntile; kt += 2) {
+        tile_step(kt, ks0, vt0, ks1, vt1);
+        if (kt + 1 < ntile) tile_step(kt + 1, ks1, vt1, ks0, vt0);
     }
 
 #pragma unroll
