@@ -575,7 +575,7 @@ def gemm_bench(args, tl, torch, np):
                    "out_columns": n_out, "group_size": gs, "weight_sets": sets, "what": desc},
         "kernels_us": {"w8a16": round(g_avg * 1e3, 2), "w8a16_reduce": round(r_avg * 1e3, 2)},
         "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
-        "roofline": {"kernel": "w8a16_mfma_kernel + w8a16_reduce_kernel", "bound": "hbm",
+        "roofline": {"kernel": "w8a16_sk_kernel + w8a16_reduce_kernel", "bound": "hbm",
                      "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "tflops": round(flops / (kern_ms * 1e-3) / 1e12, 2),

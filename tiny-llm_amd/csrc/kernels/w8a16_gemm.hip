@@ -4,8 +4,20 @@
 // with an fp32 accumulator, W [K][N] int8 row-major, scales
 // [ceil(K/gs)][N] fp16.
 //
-// MFMA path (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
-// N % 16 == 0):
+// MFMA paths (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
+// N % 16 == 0).  Both split K across workgroups for decode-sized M (the split
+// count depends on (M, K) only, so an output element's value does not depend
+// on which other weight matrices share the launch) and sum the splits in a
+// fixed order, so results are deterministic.
+//
+// Packed weights (w8a16_sk_kernel, the fast path; layout of
+// launch_w8a16_pack): one workgroup = 4 waves = a 64x64 output tile over one
+// split; wave w takes every fourth group of 4 k steps for the whole tile,
+// with W fragments (8 bytes per lane) and x fragments (16 bytes per lane)
+// loaded straight into MFMA operands -- no staging, no barrier until the
+// waves' tiles are summed through LDS.
+//
+// Reference layout (w8a16_mfma_kernel):
 //   One workgroup = 4 waves = a 64-row x 64-column output tile over one split
 //   of K (split-K across workgroups when the tiles alone would leave CUs
 //   idle).  Per 64-row K chunk:
@@ -22,11 +34,10 @@
 //       accumulator with its scale: acc += P_g * s[g][n] (a k step never
 //       straddles groups, and the fold points are compile-time constants).
 //   The loads of up to 8 chunks are issued before the first is consumed.
-//   With one split the workgroup applies the epilogue directly; otherwise it
-//   writes fp32 partials and w8a16_reduce_kernel sums the splits in a fixed
-//   order (deterministic) and applies the epilogue.  The split count depends
-//   on (M, K) only, so an output element's value does not depend on which
-//   other weight matrices share the launch.
+// With one split the GEMM kernel applies the epilogue directly; otherwise it
+// writes fp32 partials and w8a16_reduce_kernel sums the splits in split order
+// and applies the epilogue.  The two MFMA kernels sum in different orders, so
+// their results agree to within rounding, not bit for bit.
 // Generic path (any shape): one thread per output, the reference formula
 // sum = fma(x, w * s, sum) over k in order.
 //
@@ -150,7 +161,7 @@ __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t v) {
 // transposed in registers (v_perm), converted to fp16 and stored [column][k]
 // with 8-byte LDS writes, x is staged with 16-byte writes, then two 32-deep
 // MFMA k-steps per 16-row block.
-template <int GS, bool PACKED>
+template <int GS>
 __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
     static_assert(GS % 32 == 0 && (kRing * kBK) % GS == 0, "group size");
     constexpr int SPG = GS / 32;                 // k steps per scale group
@@ -200,7 +211,6 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
     const int8_t *wbase = sg.w + (int64_t)wr * sg.n + wcol;
     const int64_t wchunk = (int64_t)kBK * sg.n;
     const int     ksteps = a.K >> 5;
-    const int8_t *pbase = sg.w + ((int64_t)(min(n0, sg.n - 16) >> 4) * ksteps * 64 + lane) * 8;
     const __half *xrow[2];
     int           xk[2];
 #pragma unroll
@@ -233,7 +243,6 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
         // W of all kRing chunks in flight at once (HBM); x (L2-resident) one
         // chunk ahead.
         uint32_t wbuf[kRing][4]; // reference layout: rows wr..wr+3 x columns wq..wq+3
-        uint2    wpk[kRing][2];  // packed layout: the wave's B fragment of k steps 2c, 2c+1
         uint4    xbuf[2][2];
         auto     load_x = [&](int j, uint4(&xv)[2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -243,17 +252,11 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < kRing; ++j) {
             const int c = min(cb + j, kchunks - 1);
-            if constexpr (PACKED) {
+            const int8_t *wp = wbase + (int64_t)c * wchunk;
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    wpk[j][ks] = *reinterpret_cast<const uint2 *>(pbase + (int64_t)min(2 * c + ks, ksteps - 1) * 512);
-            } else {
-                const int8_t *wp = wbase + (int64_t)c * wchunk;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    wbuf[j][i] = *reinterpret_cast<const uint32_t *>(
-                        wp + (int64_t)min(i, a.K - 1 - c * kBK - wr) * sg.n); // row <= K - 1
-            }
+            for (int i = 0; i < 4; ++i)
+                wbuf[j][i] = *reinterpret_cast<const uint32_t *>(
+                    wp + (int64_t)min(i, a.K - 1 - c * kBK - wr) * sg.n); // row <= K - 1
         }
         load_x(0, xbuf[0]);
 #pragma unroll
@@ -269,7 +272,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
                 const int r = q >> 3, kp = q & 7;
                 *reinterpret_cast<uint4 *>(&xsb[r * kXPitch + 8 * kp]) = xbuf[j & 1][u];
             }
-            if constexpr (!PACKED) {
+            {
                 uint32_t col[4];
                 transpose4x4(wbuf[j], col);
 #pragma unroll
@@ -280,14 +283,8 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 if (32 * (2 * c + ks) >= a.K) break; // uniform: the half chunk beyond K (K % 64 == 32)
-                f16x8 bop;
-                if constexpr (PACKED) {
-                    const uint2 lo = i8x4_to_f16x4(wpk[j][ks].x), hi = i8x4_to_f16x4(wpk[j][ks].y);
-                    bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                } else {
-                    bop = *reinterpret_cast<const f16x8 *>(
-                        &wtb[(16 * wave + (lane & 15)) * kWPitch + 32 * ks + 8 * (lane >> 4)]);
-                }
+                const f16x8 bop = *reinterpret_cast<const f16x8 *>(
+                    &wtb[(16 * wave + (lane & 15)) * kWPitch + 32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
                     const f16x8 aop = *reinterpret_cast<const f16x8 *>(
@@ -340,6 +337,211 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
                 epilogue(a, si, m, ncol, acc[rb][i]);
             }
         }
+    }
+}
+
+// Packed-weight kernel, split-K inside the workgroup: one workgroup (4 waves)
+// per unit (64-row tile, 64-column tile, K split); wave w takes k steps
+// 4w..4w+3 of every 16-step (512-row) batch of the split for the whole 64x64
+// tile, with its operands straight from global memory (W: 8 bytes per lane
+// per fragment, packed; x: 16 bytes per lane per fragment, two steps ahead),
+// 16 MFMAs per step.  Scale groups are folded in step order.  The four
+// waves' tiles are summed through LDS in wave order, wave w finishing row
+// block w (each wave passes on the three row blocks it does not finish: 48
+// KB of LDS, three workgroups per CU).  ACC: a second accumulator for
+// several scale groups per wave (group size < 128, or more than one batch);
+// without it the wave's result is P * s.
+template <int GS, bool ACC>
+__global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) {
+    static_assert(GS % 32 == 0 && 512 % GS == 0, "group size");
+    constexpr int SPG = GS / 32;
+    constexpr int BS = 16;
+    constexpr int NS = SPG >= 4 ? 1 : 4 / SPG; // scale groups per wave and batch
+    static_assert(ACC || NS == 1, "several groups per wave need the accumulator");
+    __shared__ __align__(16) float red[4 * 3 * 4 * 64 * 4]; // [src wave][rb != src][cb][lane][4]
+    const int     lane = threadIdx.x & 63;
+    const int     wave = threadIdx.x >> 6;
+    const int     unit = blockIdx.x;
+    const int     split = unit % a.splits;
+    const int     rest = unit / a.splits;
+    int           tile = rest % a.tiles;
+    const int     mt = rest / a.tiles;
+    if (mt >= a.mtiles) return;
+    int si = 0;
+    while (si + 1 < a.nseg && tile >= (a.seg[si].n + kBN - 1) / kBN) {
+        tile -= (a.seg[si].n + kBN - 1) / kBN;
+        ++si;
+    }
+    const W8A16Seg &sg = a.seg[si];
+    const int       c0 = tile * kBN;
+    const int       nblk = sg.n >> 4;
+    const int       ksteps = a.K >> 5;
+    const int       s_begin = split * 2 * a.chunks_per_split;
+    const int       s_end = min(ksteps, s_begin + 2 * a.chunks_per_split);
+    const int       ngroups = (a.K + GS - 1) / GS;
+    const int       m0 = mt * kBM;
+
+    const int8_t *wp[4];
+    const __half *sp[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const int nb = min((c0 >> 4) + cb, nblk - 1);
+        wp[cb] = sg.w + ((int64_t)nb * ksteps * 64 + lane) * 8;
+        sp[cb] = sg.s + 16 * nb + (lane & 15);
+    }
+    const __half *xp[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+        xp[rb] = a.x + (int64_t)min(m0 + 16 * rb + (lane & 15), a.M - 1) * a.ldx + 8 * (lane >> 4);
+
+    f32x4 P[4][4], acc[4][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            P[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            acc[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    float s_last[4] = {0.0f, 0.0f, 0.0f, 0.0f}; // scale of the wave's last group (no ACC)
+
+    for (int sb = s_begin; sb < s_end; sb += BS) {
+        const int first = sb + 4 * wave; // this wave's 4 steps
+        const int nsteps = max(0, min(4, s_end - first));
+        if (nsteps == 0) continue;
+        uint2 wv[4][4];
+        f16x8 xv[2][4];
+        auto  load_x = [&](int j, f16x8(&dst)[4]) __attribute__((always_inline)) {
+            const int st = min(first + j, ksteps - 1);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) dst[rb] = *reinterpret_cast<const f16x8 *>(xp[rb] + 32 * st);
+        };
+        load_x(0, xv[0]); // x first (L2 hits), then W (HBM)
+        load_x(1, xv[1]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int st = min(first + j, ksteps - 1);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + (int64_t)st * 512);
+        }
+        uint16_t sraw[NS][4];
+#pragma unroll
+        for (int g = 0; g < NS; ++g)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                sraw[g][cb] = *reinterpret_cast<const uint16_t *>(
+                    sp[cb] + (int64_t)min((first + g * SPG) * 32 / GS, ngroups - 1) * sg.n);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j >= nsteps) continue; // uniform
+            f16x8 xa[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) xa[rb] = xv[j & 1][rb];
+            if (j + 2 < 4) load_x(j + 2, xv[j & 1]);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const uint2 lo = i8x4_to_f16x4(wv[j][cb].x), hi = i8x4_to_f16x4(wv[j][cb].y);
+                const f16x8 bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    P[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rb], bop, P[rb][cb], 0, 0, 0);
+            }
+            if constexpr (ACC) {
+                if ((j + 1) % SPG == 0 || j + 1 == nsteps) { // end of a group or of the wave's steps
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        const float s_ = h2f(__builtin_bit_cast(__half, sraw[j / SPG % NS][cb]));
+#pragma unroll
+                        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc[rb][cb][i] = fmaf(P[rb][cb][i], s_, acc[rb][cb][i]);
+                            P[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                        }
+                    }
+                }
+            }
+        }
+        if constexpr (!ACC) {
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) s_last[cb] = h2f(__builtin_bit_cast(__half, sraw[0][cb]));
+        }
+    }
+    // The wave's result r = acc, or P * s.
+    if constexpr (!ACC) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[rb][cb][i] = P[rb][cb][i] * s_last[cb];
+    }
+
+    // Pass on the three row blocks this wave does not finish.
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        if (rb == wave) continue;
+        const int k = rb - (rb > wave);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            *reinterpret_cast<f32x4 *>(&red[(((wave * 3 + k) * 4 + cb) * 64 + lane) * 4]) = acc[rb][cb];
+    }
+    __syncthreads();
+    // Sum row block w over the waves in wave order.
+    const int rb = wave;
+    f32x4     v[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        v[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int src = 0; src < 4; ++src) {
+            f32x4 u;
+            if (src == wave) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) u = q == wave ? acc[q][cb] : u; // static indices
+            } else {
+                const int k = rb - (rb > src);
+                u = *reinterpret_cast<const f32x4 *>(&red[(((src * 3 + k) * 4 + cb) * 64 + lane) * 4]);
+            }
+            if (src == 0) {
+                v[cb] = u;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[cb][i] += u[i];
+            }
+        }
+    }
+    if (a.splits == 1) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            if (c0 + 16 * cb >= sg.n) continue; // uniform
+            const int n = c0 + 16 * cb + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + 16 * rb + 4 * (lane >> 4) + i;
+                if (m < a.M) epilogue(a, si, m, n, v[cb][i]);
+            }
+        }
+        return;
+    }
+    // Partials: the row block is transposed through LDS (rows of 64 floats,
+    // pitch 68) so that every lane stores 16 contiguous bytes and each group
+    // of 16 lanes one row's 256 bytes.
+    __syncthreads(); // every wave has read the passed-on blocks
+    constexpr int TP = 68;
+    float        *t = &red[wave * 16 * TP];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[(4 * (lane >> 4) + i) * TP + 16 * cb + (lane & 15)] = v[cb][i];
+    const int cw = min(kBN, sg.n - c0); // live columns of the tile (a multiple of 16)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int   r = 4 * q + (lane >> 4);
+        const int   c = 4 * (lane & 15);
+        const int   m = m0 + 16 * rb + r;
+        const f32x4 u = *reinterpret_cast<const f32x4 *>(&t[r * TP + c]);
+        if (m < a.M && c < cw)
+            *reinterpret_cast<f32x4 *>(&a.partial[((int64_t)split * a.M + m) * a.ntot + a.col0[si] + c0 + c]) = u;
     }
 }
 
@@ -526,21 +728,39 @@ void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A1
     if (splits > 1 && !workspace) throw std::invalid_argument("w8a16: split-K needs a workspace");
     const unsigned blocks = (unsigned)((a.units + 7) / 8 * 16); // pairs of 8-block groups
     profile_begin(KernelId::W8A16, stream);
-#define TL_W8_LAUNCH(G)                                                                             \
+    if (packed) {
+        // Several scale groups per wave (gs < 128) or more than one 512-row
+        // batch per split need the second accumulator.
+        const bool     acc = gs < 128 || a.chunks_per_split > 8;
+        const unsigned units = (unsigned)(splits * tiles * mt);
+#define TL_W8_SK_LAUNCH(G)                                                                          \
     do {                                                                                            \
-        if (packed)                                                                                 \
-            hipLaunchKernelGGL((w8a16_mfma_kernel<G, true>), dim3(blocks), dim3(kThreads), 0, stream, a);  \
+        if (acc)                                                                                    \
+            hipLaunchKernelGGL((w8a16_sk_kernel<G, true>), dim3(units), dim3(256), 0, stream, a);   \
         else                                                                                        \
-            hipLaunchKernelGGL((w8a16_mfma_kernel<G, false>), dim3(blocks), dim3(kThreads), 0, stream, a); \
+            hipLaunchKernelGGL((w8a16_sk_kernel<(G < 128 ? 128 : G), false>), dim3(units), dim3(256), 0, \
+                               stream, a);                                                          \
     } while (0)
-    switch (gs) {
-    case 32: TL_W8_LAUNCH(32); break;
-    case 64: TL_W8_LAUNCH(64); break;
-    case 128: TL_W8_LAUNCH(128); break;
-    case 256: TL_W8_LAUNCH(256); break;
-    default: TL_W8_LAUNCH(512); break;
-    }
+        switch (gs) {
+        case 32: TL_W8_SK_LAUNCH(32); break;
+        case 64: TL_W8_SK_LAUNCH(64); break;
+        case 128: TL_W8_SK_LAUNCH(128); break;
+        case 256: TL_W8_SK_LAUNCH(256); break;
+        default: TL_W8_SK_LAUNCH(512); break;
+        }
+#undef TL_W8_SK_LAUNCH
+    } else {
+#define TL_W8_LAUNCH(G) \
+    hipLaunchKernelGGL((w8a16_mfma_kernel<G>), dim3(blocks), dim3(kThreads), 0, stream, a)
+        switch (gs) {
+        case 32: TL_W8_LAUNCH(32); break;
+        case 64: TL_W8_LAUNCH(64); break;
+        case 128: TL_W8_LAUNCH(128); break;
+        case 256: TL_W8_LAUNCH(256); break;
+        default: TL_W8_LAUNCH(512); break;
+        }
 #undef TL_W8_LAUNCH
+    }
     HIP_CHECK(hipGetLastError());
     profile_end(KernelId::W8A16, stream);
     if (splits > 1) {
