@@ -72,8 +72,7 @@ struct PrefillArgs {
     const __half       *q;
     __half             *out;
     KvView              kv;
-    const PrefillEntry *entries;
-    const int32_t      *work;
+    const int32_t      *work; // kPrefillItemWords words per item, or null (uniform)
     int64_t             q_tok;
     int64_t             q_head;
     int64_t             q_entry;
@@ -159,14 +158,13 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     const int g = blockIdx.x - item * a.Hkv;
     int64_t   q_off;
     int       p0, n, row, qt;
-    if (a.entries) {
-        const int e = a.work[2 * item];
-        qt = a.work[2 * item + 1];
-        const PrefillEntry E = a.entries[e];
-        q_off = E.q_off;
-        p0 = E.p0;
-        n = E.n;
-        row = E.row;
+    if (a.work) { // one self-contained record: a single dependent load
+        const int32_t *w = a.work + (int64_t)kPrefillItemWords * item;
+        q_off = (int64_t)(((uint64_t)(uint32_t)w[1] << 32) | (uint32_t)w[0]);
+        p0 = w[2];
+        n = w[3];
+        row = w[4];
+        qt = w[5];
     } else { // uniform entries, the query tiles with the most keys first
         const int nqt = (a.uniform_n + BQ - 1) / BQ;
         const int b = item % a.uniform_b;
@@ -376,22 +374,44 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
         if (kt + 1 < ntile) tile_step(kt + 1, ks1, vt1, ks0, vt0);
     }
 
+    // Output: the wave's normalised fp16 rows go through LDS (the K/V
+    // buffers are free after the last barrier; wave w uses the w-th of the
+    // four, rows padded by 8 halves), then every lane stores 16 contiguous
+    // bytes and each group of D/8 lanes one whole row -- full cache lines
+    // instead of 8-byte pieces of 16 rows per store.
+    constexpr int OP = D + 8;        // staged row pitch (halves)
+    constexpr int R = 16 * NQG;      // rows of the wave
+    constexpr int PPR = D / 8;       // 16-byte pieces per row
+    constexpr int NCH = R * PPR / 64; // pieces per lane
+    static_assert(R * OP <= kKeyTile * ROWH, "staging fits one K/V buffer");
+    uint16_t *stg = wave == 0 ? ks0 : (wave == 1 ? ks1 : (wave == 2 ? vt0 : vt1));
 #pragma unroll
     for (int j = 0; j < NQG; ++j) {
         float l = l_run[j] + __shfl_xor(l_run[j], 16);
         l += __shfl_xor(l, 32);
         const float inv = 1.0f / (l + 1e-6f);
-        if (valid[j]) {
-            __half *op = a.out + qrow[j] + 4 * qg;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const __half2 lo = __floats2half2_rn(acc[j][dt][0] * inv, acc[j][dt][1] * inv);
-                const __half2 hi = __floats2half2_rn(acc[j][dt][2] * inv, acc[j][dt][3] * inv);
-                uint2         w;
-                w.x = __builtin_bit_cast(uint32_t, lo);
-                w.y = __builtin_bit_cast(uint32_t, hi);
-                *reinterpret_cast<uint2 *>(op + 16 * dt) = w;
-            }
+        for (int dt = 0; dt < DT; ++dt) {
+            const __half2 lo = __floats2half2_rn(acc[j][dt][0] * inv, acc[j][dt][1] * inv);
+            const __half2 hi = __floats2half2_rn(acc[j][dt][2] * inv, acc[j][dt][3] * inv);
+            uint2         w;
+            w.x = __builtin_bit_cast(uint32_t, lo);
+            w.y = __builtin_bit_cast(uint32_t, hi);
+            *reinterpret_cast<uint2 *>(&stg[(j * 16 + c) * OP + 16 * dt + 4 * qg]) = w;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int u = 0; u < NCH; ++u) {
+        const int k = u * 64 + lane;
+        const int rr = k / PPR, pc = k - rr * PPR;
+        const int r = wave * R + rr; // workgroup row: token r / G, head r % G of kv group g
+        const int qi = qt * BQ + r / G;
+        if (qi < n) {
+            const int64_t o = q_off + (int64_t)qi * a.q_tok + (int64_t)(g * G + r % G) * a.q_head + 8 * pc;
+            *reinterpret_cast<uint4 *>(a.out + o) = *reinterpret_cast<const uint4 *>(&stg[rr * OP + 8 * pc]);
         }
     }
 }
@@ -479,10 +499,16 @@ void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<
             items.push_back({(int64_t)entries[e].p0 + std::min(entries[e].n, (qt + 1) * BQ), e, qt});
     }
     std::stable_sort(items.begin(), items.end(), [](const It &x, const It &y) { return x.keys > y.keys; });
-    work.resize(2 * items.size());
+    work.assign(kPrefillItemWords * items.size(), 0);
     for (size_t i = 0; i < items.size(); ++i) {
-        work[2 * i] = items[i].e;
-        work[2 * i + 1] = items[i].qt;
+        const PrefillEntry &E = entries[items[i].e];
+        int32_t            *w = &work[kPrefillItemWords * i];
+        w[0] = (int32_t)(uint32_t)((uint64_t)E.q_off & 0xffffffffu);
+        w[1] = (int32_t)(uint32_t)((uint64_t)E.q_off >> 32);
+        w[2] = E.p0;
+        w[3] = E.n;
+        w[4] = E.row;
+        w[5] = items[i].qt;
     }
 }
 
@@ -490,7 +516,7 @@ void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int H
                          float scale, hipStream_t stream) {
     const int G = Hq / Hkv;
     int       items;
-    if (p.entries) {
+    if (p.work) {
         items = p.n_items;
     } else {
         const int BQ = prefill_block_tokens(D, G);
@@ -501,7 +527,6 @@ void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int H
     a.q = p.q;
     a.out = p.out;
     a.kv = kv;
-    a.entries = p.entries;
     a.work = p.work;
     a.q_tok = p.q_tok_stride;
     a.q_head = p.q_head_stride;

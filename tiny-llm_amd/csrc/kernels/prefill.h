@@ -34,7 +34,10 @@ static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
 inline int prefill_block_tokens(int D, int G) { return (D <= 128 ? 128 : 64) / G; }
 
 // Work items (entry, query tile), most keys first (LPT order for the
-// hardware dispatcher): work[2i], work[2i+1].
+// hardware dispatcher), each a self-contained record of kPrefillItemWords
+// 32-bit words: {q_off low, q_off high, p0, n, row, query tile, 0, 0}, so a
+// workgroup needs one dependent load before its Q and K/V loads.
+constexpr int kPrefillItemWords = 8;
 void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<int32_t> &work);
 
 struct PrefillLaunch {
@@ -42,11 +45,11 @@ struct PrefillLaunch {
     __half             *out = nullptr;
     int64_t             q_tok_stride = 0;
     int64_t             q_head_stride = 0;
-    // Either a device entry table and work list (n_items items) ...
-    const PrefillEntry *entries = nullptr;
+    // Either a device work list of n_items records (plan_prefill; 32-byte
+    // aligned) ...
     const int32_t      *work = nullptr;
     int                 n_items = 0;
-    // ... or, with entries == NULL, `uniform_b` entries b with p0 = 0,
+    // ... or, with work == NULL, `uniform_b` entries b with p0 = 0,
     // n = uniform_n, row = b and q_off = b * q_entry_stride.
     int                 uniform_b = 0;
     int                 uniform_n = 0;

@@ -792,25 +792,24 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
     }
     std::vector<int32_t> work;
     detail::plan_prefill(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads, work);
-    // Device copy: [entries (6 words each) | token rows T | token positions T | work].
+    // Device copy: [work items (8 words each, first: 32-byte aligned) |
+    // token rows T | token positions T].
     const size_t T = static_cast<size_t>(total);
-    const size_t words = 6 * static_cast<size_t>(n) + 2 * T + work.size();
+    const size_t words = work.size() + 2 * T;
     int32_t     *h = static_cast<int32_t *>(meta_->begin(words * 4));
-    std::memcpy(h, entries.data(), static_cast<size_t>(n) * sizeof(detail::PrefillEntry));
-    int32_t *rows = h + 6 * static_cast<size_t>(n), *pos = rows + T;
+    if (!work.empty()) std::memcpy(h, work.data(), work.size() * 4);
+    int32_t *rows = h + work.size(), *pos = rows + T;
     size_t   k = 0;
     for (int i = 0; i < n; ++i)
         for (int j = 0; j < num_tokens[i]; ++j, ++k) {
             rows[k] = slots[static_cast<size_t>(i)];
             pos[k] = entries[static_cast<size_t>(i)].p0 + j;
         }
-    if (!work.empty()) std::memcpy(pos + T, work.data(), work.size() * 4);
     const int32_t *d = static_cast<const int32_t *>(meta_->commit(stream));
-    d_entries_ = reinterpret_cast<const detail::PrefillEntry *>(d);
-    d_tok_row_ = d + 6 * static_cast<size_t>(n);
+    d_work_ = d;
+    d_tok_row_ = d + work.size();
     d_tok_pos_ = d_tok_row_ + T;
-    d_work_ = d_tok_pos_ + T;
-    n_items_ = static_cast<int>(work.size() / 2);
+    n_items_ = static_cast<int>(work.size() / detail::kPrefillItemWords);
     ids_.assign(seq_ids, seq_ids + n);
     counts_.assign(num_tokens, num_tokens + n);
     n_ = n;
@@ -854,7 +853,6 @@ Result<void> PrefillBatch::attention(int layer_idx, const half *q, half *out, fl
     p.out = out;
     p.q_tok_stride = static_cast<int64_t>(num_q_heads_) * cfg.head_dim;
     p.q_head_stride = cfg.head_dim;
-    p.entries = d_entries_;
     p.work = d_work_;
     p.n_items = n_items_;
     p.max_keys = max_keys_;

@@ -259,7 +259,6 @@ class PrefillBatch {
     std::vector<int32_t> ids_, counts_;
     std::unique_ptr<detail::MetaRing> meta_;
     const int32_t       *d_tok_row_ = nullptr, *d_tok_pos_ = nullptr, *d_work_ = nullptr;
-    const detail::PrefillEntry *d_entries_ = nullptr;
 };
 
 } // namespace tiny_llm
