@@ -14,7 +14,9 @@
 // Workgroup: 4 waves, one kv head g, 128 query rows = 128/G tokens x G heads
 // (64 rows for head_dim 256); each wave owns two (one) 16-row query column
 // groups.  Keys stream in tiles of 64 tokens through double-buffered LDS,
-// K and V both row-major (16-byte stores).  Per wave, group and tile:
+// K and V both row-major, written by the LDS DMA load (global_load_lds,
+// 16 bytes per lane) with XOR-swizzled 16-byte slots.  Per wave, group and
+// tile:
 //   S^T = K Q^T        v_mfma_f32_16x16x32_f16: A = K rows (token l%16,
 //                      dims 8(l/16)..+7), B = Q (query l%16, same dims),
 //                      D = S^T (tokens 4(l/16)+i, query l%16)
@@ -30,10 +32,10 @@
 //                      V tile with ds_read_b64_tr_b16 (gfx950's transposing
 //                      LDS read); D = O^T (dims 4(l/16)+i, query l%16), so
 //                      the rescale by the running max is lane-local.
-// The next tile's K/V rows are loaded into registers while the current one
-// is computed.  Grid: work items x Hkv, kv head fastest, so with 8 kv heads
-// every workgroup of head g runs on XCD g and the tiles it re-reads stay in
-// that XCD's L2.
+// The next tile's DMA runs while the current one is computed; the output
+// rows go through LDS so that every store is a whole row.  Grid: work items
+// x Hkv, kv head fastest, so with 8 kv heads every workgroup of head g runs
+// on XCD g and the tiles it re-reads stay in that XCD's L2.
 #include "prefill.h"
 
 #include "tiny_llm/hip_utils.h"
