@@ -409,8 +409,10 @@ def prefill_bench(args, tl, torch, np):
     """Prefill into the cache at Llama-3-8B attention shapes (32 q / 8 kv
     heads, head_dim 128): --prefill-seqs prompts of --prefill-tokens new tokens
     on top of --prefill-prefix cached ones, one layer.  A step is
-    PrefillBatch.prepare + run (append of the new K/V rows, then causal GQA
-    attention of every new token over its sequence's cache).  The cache is
+    PrefillBatch.prepare + run: one launch that attends every new token
+    causally over its sequence's cache (keys at or past the write position
+    read from the new K/V rows) and writes the new rows into the cache (the
+    append).  The cache is
     rewound after each step (lengths are not committed), so every step
     repeats the same work."""
     Hq, Hkv, D = 32, 8, 128

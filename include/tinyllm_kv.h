@@ -259,7 +259,8 @@ void tl_get_attention_weights(const void *q, const void *k, void *weights, float
  *   append:  new_k/new_v [T][num_heads*head_dim], sequences back to back,
  *            T = sum of num_tokens (bytes identical to appendKV per sequence);
  *   attention: q/out [T][num_q_heads][head_dim];
- *   run:     append + attention;
+ *   run:     append + attention in one launch (same bytes and outputs; q,
+ *            out, new_k and new_v 16-byte aligned);
  *   commit:  advanceSeqLen(seq_ids[i], num_tokens[i]).
  * num_q_heads / num_heads in {1,2,4,8}; head_dim in {32,64,128,256}. */
 typedef struct tl_kv_prefill tl_kv_prefill;

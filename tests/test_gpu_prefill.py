@@ -159,6 +159,57 @@ def test_chunked_prefill_equals_one_shot(tl, D, G):
     assert np.array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("kind", ["slots", "blocks"])
+@pytest.mark.parametrize("D,G", [(128, 4), (64, 8), (32, 1), (256, 2)])
+def test_fused_prefill_equals_append_then_attention(tl, kind, D, G):
+    """PrefillBatch.run (one launch: keys at or past the write position read
+    from new_k/new_v, the rows written into the cache by the attention
+    kernel) == append() followed by attention(): identical cache bytes and
+    identical outputs, for prompts that start empty or continue a cached
+    prefix."""
+    rng = np.random.default_rng(D + 3 * G + len(kind))
+    L, H, M, B = 2, 2, 512, 4
+    Hq = H * G
+    prefix, new = [0, 70, 0, 200], [33, 64, 150, 1]
+    outs, pools = [], []
+    q = f16bits(rng, (sum(new), Hq, D))
+    nk, nv = f16bits(rng, (sum(new), H * D)), f16bits(rng, (sum(new), H * D))
+    pre = [(f16bits(rng, p0 * H * D), f16bits(rng, p0 * H * D)) for p0 in prefix]
+    keep = []
+    for fused in (False, True):
+        g = make_pool(tl, kind, L, H, D, M, B, np.random.default_rng(7))
+        ids = []
+        for p0, (k, v) in zip(prefix, pre):
+            sid, _ = g.allocateSequence(M)
+            ids.append(sid)
+            if p0:
+                dk, dv = to_dev(k), to_dev(v)
+                keep += [dk, dv]
+                assert g.appendKV(sid, 1, dk.data_ptr(), dv.data_ptr(), p0, stream()) is None
+                g.advanceSeqLen(sid, p0)
+        pb = tl.PrefillBatch(g, B, Hq)
+        pb.prepare(ids, new, stream())
+        dq, dk, dv = to_dev(q), to_dev(nk), to_dev(nv)
+        out = empty_dev((sum(new), Hq, D))
+        keep += [dq, dk, dv]
+        if fused:
+            pb.run(1, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), D ** -0.5, stream())
+        else:
+            pb.append(1, dk.data_ptr(), dv.data_ptr(), stream())
+            pb.attention(1, dq.data_ptr(), out.data_ptr(), D ** -0.5, stream())
+        outs.append(to_host(out))
+        lens = [p + n for p, n in zip(prefix, new)]
+        db = tl.DecodeBatch(g, B, Hq)
+        db.prepare_lengths(ids, lens, stream())
+        smax = max(lens)
+        gk, gv = empty_dev((B, H, smax, D)), empty_dev((B, H, smax, D))
+        db.gather(1, gk.data_ptr(), gv.data_ptr(), smax, stream())
+        pools.append((to_host(gk), to_host(gv)))
+        keep.append(g)
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(pools[0][0], pools[1][0]) and np.array_equal(pools[0][1], pools[1][1])
+
+
 def test_prefill_batch_errors(tl):
     g = tl.KVCacheManager(1, 2, 64, 64, 3)
     a, _ = g.allocateSequence(64)

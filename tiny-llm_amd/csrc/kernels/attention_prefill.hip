@@ -80,6 +80,8 @@ struct PrefillArgs {
     int64_t             q_entry;
     int                 uniform_b;
     int                 uniform_n;
+    const __half       *new_k; // fused append source or null
+    const __half       *new_v;
     int                 Hkv;
     float               scale_log2;
 };
@@ -134,7 +136,7 @@ __device__ __forceinline__ float materialize(float x) {
 }
 
 template <int D, int G, bool PAGED>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(PrefillArgs a) {
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
     constexpr int NQG = kQueryGroups<D>;    // 16-query column groups per wave
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     const int item = blockIdx.x / a.Hkv;
     const int g = blockIdx.x - item * a.Hkv;
     int64_t   q_off;
-    int       p0, n, row, qt;
+    int       p0, n, row, qt, tok0 = 0;
     if (a.work) { // one self-contained record: a single dependent load
         const int32_t *w = a.work + (int64_t)kPrefillItemWords * item;
         q_off = (int64_t)(((uint64_t)(uint32_t)w[1] << 32) | (uint32_t)w[0]);
@@ -167,6 +169,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
         n = w[3];
         row = w[4];
         qt = w[5];
+        tok0 = w[6];
     } else { // uniform entries, the query tiles with the most keys first
         const int nqt = (a.uniform_n + BQ - 1) / BQ;
         const int b = item % a.uniform_b;
@@ -225,14 +228,22 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
         for (int u = 0; u < NKI; ++u) {
             const int sl = u * kPThreads + tid;
             const int r = sl / KP, x = (sl % KP) ^ (r & (KP - 1));
-            const int64_t off = roff(min(t0 + r, kend - 1), x);
+            const int t = min(t0 + r, kend - 1);
+            const char *ks, *vs;
+            if (a.new_k && t >= p0) { // a new token: its row in the fused append's input
+                const int64_t o = ((int64_t)(tok0 + t - p0) * a.Hkv + g) * (2 * D) + 16 * x;
+                ks = reinterpret_cast<const char *>(a.new_k) + o;
+                vs = reinterpret_cast<const char *>(a.new_v) + o;
+            } else {
+                const int64_t off = roff(t, x);
+                ks = kr.kbase + off;
+                vs = kr.vbase + off;
+            }
             const int lbase = (u * kPThreads + wave * 64) * 8; // halves, wave-uniform
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(kr.kbase + off),
-                (__attribute__((address_space(3))) void *)(&kdst[lbase]), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(kr.vbase + off),
-                (__attribute__((address_space(3))) void *)(&vdst[lbase]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)ks,
+                                             (__attribute__((address_space(3))) void *)(&kdst[lbase]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)vs,
+                                             (__attribute__((address_space(3))) void *)(&vdst[lbase]), 16, 0, 0);
         }
     };
 
@@ -252,6 +263,21 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2))) 
     // kd/vd, wait for the DMA, barrier.
     auto tile_step = [&](int kt, const uint16_t *kd, const uint16_t *vd, uint16_t *kn, uint16_t *vn)
                          __attribute__((always_inline)) {
+        if (a.new_k) {
+            // Fused appendKV: the rows of this query tile's own tokens (kv
+            // head g) that lie in tile kt go from LDS into the cache --
+            // nothing in this launch reads them from there.
+            const int lo = max(kt * kKeyTile, p0 + qt * BQ);
+            const int hi = min(kt * kKeyTile + kKeyTile, p0 + min(n, qt * BQ + BQ));
+            for (int e = tid; e < (hi - lo) * KP; e += kPThreads) {
+                const int     t = lo + e / KP, x = e % KP, sl = slot(t - kt * kKeyTile, x);
+                const uint4   kk = *reinterpret_cast<const uint4 *>(&kd[sl * 8]);
+                const uint4   vv = *reinterpret_cast<const uint4 *>(&vd[sl * 8]);
+                const int64_t d = kr.off(t) + 16 * x;
+                *reinterpret_cast<uint4 *>(const_cast<char *>(kr.kbase) + d) = kk;
+                *reinterpret_cast<uint4 *>(const_cast<char *>(kr.vbase) + d) = vv;
+            }
+        }
         // the next tile lands in the other buffer during this tile's math
         if (kt + 1 < ntile) issue_tile(kt + 1, kn, vn);
 
@@ -511,6 +537,7 @@ void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<
         w[3] = E.n;
         w[4] = E.row;
         w[5] = items[i].qt;
+        w[6] = E.tok0;
     }
 }
 
@@ -535,6 +562,10 @@ void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int H
     a.q_entry = p.q_entry_stride;
     a.uniform_b = p.uniform_b;
     a.uniform_n = p.uniform_n;
+    if ((p.new_k != nullptr) != (p.new_v != nullptr) || (p.new_k && !p.work))
+        throw std::invalid_argument("attention_prefill: the fused append needs new_k, new_v and a work list");
+    a.new_k = p.new_k;
+    a.new_v = p.new_v;
     a.Hkv = Hkv;
     a.scale_log2 = scale * 1.4426950408889634f;
     const int64_t grid = (int64_t)items * Hkv;

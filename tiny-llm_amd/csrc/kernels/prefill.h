@@ -18,13 +18,15 @@ namespace detail {
 // One sequence of a prefill call: its n new query tokens sit at positions
 // p0 .. p0+n-1 of cache row `row`; query token i, head h is at
 // q + q_off + i * q_tok_stride + h * q_head_stride (out likewise), and it
-// attends to the keys at positions 0 .. p0+i of that row.
+// attends to the keys at positions 0 .. p0+i of that row.  tok0: index of
+// its first token in the call's token batch (the row of new_k / new_v when
+// the append is fused).
 struct PrefillEntry {
     int64_t q_off;
     int32_t p0;
     int32_t n;
     int32_t row;
-    int32_t pad;
+    int32_t tok0;
 };
 
 static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
@@ -35,8 +37,8 @@ inline int prefill_block_tokens(int D, int G) { return (D <= 128 ? 128 : 64) / G
 
 // Work items (entry, query tile), most keys first (LPT order for the
 // hardware dispatcher), each a self-contained record of kPrefillItemWords
-// 32-bit words: {q_off low, q_off high, p0, n, row, query tile, 0, 0}, so a
-// workgroup needs one dependent load before its Q and K/V loads.
+// 32-bit words: {q_off low, q_off high, p0, n, row, query tile, tok0, 0}, so
+// a workgroup needs one dependent load before its Q and K/V loads.
 constexpr int kPrefillItemWords = 8;
 void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<int32_t> &work);
 
@@ -57,6 +59,13 @@ struct PrefillLaunch {
     // Largest p0 + n over the entries (the offset-width check of
     // contiguous rows).
     int                 max_keys = 0;
+    // Fused append (work-list launches only): the new tokens' K/V rows,
+    // [tokens][Hkv * D].  Keys at positions >= p0 are then read from here,
+    // and the workgroup of each query tile writes its own tokens' rows of
+    // its kv head into the cache -- the bytes of appendKV -- so the cache
+    // holds them when the kernel ends.  Null: every key from the cache.
+    const __half       *new_k = nullptr;
+    const __half       *new_v = nullptr;
 };
 
 // True when (D, G) has a prefill kernel (D in {32,64,128,256}, G in {1,2,4,8}).

@@ -780,7 +780,7 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
         ends[static_cast<size_t>(i)] = sc->current_len + nt;
         max_keys = std::max(max_keys, sc->current_len + nt);
         entries[static_cast<size_t>(i)] = {total * num_q_heads_ * cfg.head_dim, sc->current_len, nt,
-                                           slot, 0};
+                                           slot, static_cast<int32_t>(total)};
         total += nt;
     }
     if (total > INT32_MAX / 2)
@@ -841,12 +841,25 @@ Result<void> PrefillBatch::append(int layer_idx, const half *new_k, const half *
 
 Result<void> PrefillBatch::attention(int layer_idx, const half *q, half *out, float scale,
                                      hipStream_t stream) {
+    return launch(layer_idx, q, nullptr, nullptr, out, scale, stream);
+}
+
+Result<void> PrefillBatch::prefill(int layer_idx, const half *q, const half *new_k,
+                                   const half *new_v, half *out, float scale, hipStream_t stream) {
+    if (new_k == nullptr) return Result<void>::err("new_k is null");
+    if (new_v == nullptr) return Result<void>::err("new_v is null");
+    return launch(layer_idx, q, new_k, new_v, out, scale, stream);
+}
+
+Result<void> PrefillBatch::launch(int layer_idx, const half *q, const half *new_k, const half *new_v,
+                                  half *out, float scale, hipStream_t stream) {
     const KVCacheConfig &cfg = mgr_.getConfig();
-    if (q == nullptr || out == nullptr) return Result<void>::err("PrefillBatch: q/out is null");
     if (layer_idx < 0 || layer_idx >= cfg.num_layers)
         return Result<void>::err("PrefillBatch: Invalid layer_idx: " + std::to_string(layer_idx));
-    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) & 15u)
-        return Result<void>::err("PrefillBatch: q and out must be 16-byte aligned");
+    if (q == nullptr || out == nullptr) return Result<void>::err("PrefillBatch: q/out is null");
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+         reinterpret_cast<uintptr_t>(new_k) | reinterpret_cast<uintptr_t>(new_v)) & 15u)
+        return Result<void>::err("PrefillBatch: q, out, new_k and new_v must be 16-byte aligned");
     if (n_items_ == 0) return Result<void>::ok();
     detail::PrefillLaunch p;
     p.q = q;
@@ -856,16 +869,11 @@ Result<void> PrefillBatch::attention(int layer_idx, const half *q, half *out, fl
     p.work = d_work_;
     p.n_items = n_items_;
     p.max_keys = max_keys_;
+    p.new_k = new_k;
+    p.new_v = new_v;
     detail::launch_attn_prefill(p, mgr_.layerView(layer_idx, nullptr), num_q_heads_, cfg.num_heads,
                                 cfg.head_dim, scale, stream);
     return Result<void>::ok();
-}
-
-Result<void> PrefillBatch::prefill(int layer_idx, const half *q, const half *new_k,
-                                   const half *new_v, half *out, float scale, hipStream_t stream) {
-    auto r = append(layer_idx, new_k, new_v, stream);
-    if (r.isErr()) return r;
-    return attention(layer_idx, q, out, scale, stream);
 }
 
 // InferenceEngine::prefill's commit (inference_engine.cpp:272):

@@ -237,7 +237,9 @@ class PrefillBatch {
     Result<void> append(int layer_idx, const half *new_k, const half *new_v, hipStream_t stream);
     // Causal attention of the new tokens over the cache (after append).
     Result<void> attention(int layer_idx, const half *q, half *out, float scale, hipStream_t stream);
-    // append + attention.
+    // append + attention in one launch: keys at or past a sequence's write
+    // position are read from new_k/new_v, and the attention kernel writes
+    // those rows into the cache (the bytes of append()).
     Result<void> prefill(int layer_idx, const half *q, const half *new_k, const half *new_v,
                          half *out, float scale, hipStream_t stream);
     // advanceSeqLen(seq, num_tokens[i]) for every sequence of the last prepare.
@@ -248,6 +250,8 @@ class PrefillBatch {
 
   private:
     PrefillBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads);
+    Result<void> launch(int layer_idx, const half *q, const half *new_k, const half *new_v, half *out,
+                        float scale, hipStream_t stream);
 
     KVCacheManager      &mgr_;
     int                  max_seqs_;
