@@ -11,9 +11,9 @@
 // from the cache instead of the current token batch, and equal to decode
 // attention over the first p0+i+1 keys.
 //
-// Workgroup: 4 waves, one kv head g, 128 query rows = 128/G tokens x G heads
-// (64 rows for head_dim 256); each wave owns two (one) 16-row query column
-// groups.  Keys stream in tiles of 64 tokens through double-buffered LDS,
+// Workgroup: 8 waves (one workgroup per CU), one kv head g, 256 query rows =
+// 256/G tokens x G heads (head_dim 256: 4 waves, 64 rows); each wave owns two
+// (one) 16-row query column groups.  Keys stream in tiles of 64 tokens through double-buffered LDS,
 // K and V both row-major, written by the LDS DMA load (global_load_lds,
 // 16 bytes per lane) with XOR-swizzled 16-byte slots.  Per wave, group and
 // tile:
@@ -63,7 +63,11 @@ __device__ __forceinline__ __attribute__((address_space(3))) s16x4 *lds_ptr(cons
     return (__attribute__((address_space(3))) s16x4 *)(p);
 }
 
-constexpr int kPThreads = 256;
+// Threads per workgroup: 8 waves (two per SIMD, one workgroup per CU) up to
+// head_dim 128, so each K/V tile in LDS serves 256 query rows; 4 waves for
+// head_dim 256, whose register file allows one wave per SIMD.
+template <int D>
+constexpr int kPThreads = D <= 128 ? 512 : 256;
 // Lazy rescaling threshold of the online softmax, in log2 units.
 constexpr float kLazyMax = 8.0f;
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt == 0 only.
@@ -136,17 +140,20 @@ __device__ __forceinline__ float materialize(float x) {
 }
 
 template <int D, int G, bool PAGED>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(PrefillArgs a) {
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
     constexpr int NQG = kQueryGroups<D>;    // 16-query column groups per wave
-    constexpr int ROWS = 4 * 16 * NQG;      // query rows per workgroup
+    constexpr int NT = kPThreads<D>;        // threads
+    constexpr int NW = NT / 64;             // waves
+    constexpr int ROWS = NW * 16 * NQG;     // query rows per workgroup
     constexpr int BQ = ROWS / G;            // query tokens per workgroup
     constexpr int KS = D / 32;              // k steps of S^T
     constexpr int DT = D / 16;              // dim tiles of O^T
     constexpr int KP = D / 8;               // 16-byte pieces per row
     constexpr int ROWH = D;                 // halves per LDS row (unpadded, swizzled)
-    constexpr int NKI = kKeyTile * KP / kPThreads;            // K pieces per thread
+    constexpr int PIECES = kKeyTile * KP;   // 16-byte pieces of a K (or V) tile
+    constexpr int NKI = (PIECES + NT - 1) / NT; // K pieces per thread
     // Two buffers per operand as distinct arrays, so the compiler can tell
     // that the DMA into one does not alias the reads of the other and does
     // not wait for it before computing.
@@ -226,7 +233,8 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 
         const int t0 = kt * kKeyTile;
 #pragma unroll
         for (int u = 0; u < NKI; ++u) {
-            const int sl = u * kPThreads + tid;
+            const int sl = u * NT + tid;
+            if (NKI * NT > PIECES && sl >= PIECES) break; // whole waves (PIECES % 64 == 0)
             const int r = sl / KP, x = (sl % KP) ^ (r & (KP - 1));
             const int t = min(t0 + r, kend - 1);
             const char *ks, *vs;
@@ -239,7 +247,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 
                 ks = kr.kbase + off;
                 vs = kr.vbase + off;
             }
-            const int lbase = (u * kPThreads + wave * 64) * 8; // halves, wave-uniform
+            const int lbase = (u * NT + wave * 64) * 8; // halves, wave-uniform
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)ks,
                                              (__attribute__((address_space(3))) void *)(&kdst[lbase]), 16, 0, 0);
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)vs,
@@ -269,7 +277,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 
             // nothing in this launch reads them from there.
             const int lo = max(kt * kKeyTile, p0 + qt * BQ);
             const int hi = min(kt * kKeyTile + kKeyTile, p0 + min(n, qt * BQ + BQ));
-            for (int e = tid; e < (hi - lo) * KP; e += kPThreads) {
+            for (int e = tid; e < (hi - lo) * KP; e += NT) {
                 const int     t = lo + e / KP, x = e % KP, sl = slot(t - kt * kKeyTile, x);
                 const uint4   kk = *reinterpret_cast<const uint4 *>(&kd[sl * 8]);
                 const uint4   vv = *reinterpret_cast<const uint4 *>(&vd[sl * 8]);
@@ -411,8 +419,19 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D <= 
     constexpr int R = 16 * NQG;      // rows of the wave
     constexpr int PPR = D / 8;       // 16-byte pieces per row
     constexpr int NCH = R * PPR / 64; // pieces per lane
-    static_assert(R * OP <= kKeyTile * ROWH, "staging fits one K/V buffer");
-    uint16_t *stg = wave == 0 ? ks0 : (wave == 1 ? ks1 : (wave == 2 ? vt0 : vt1));
+    // Staging: up to head_dim 128 a region of its own (the workgroup has the
+    // CU's LDS to itself); head_dim 256 reuses the K/V buffers, two waves per
+    // buffer.
+    constexpr bool OWN = D <= 128;
+    __shared__ __align__(16) uint16_t own_stg[OWN ? NW * R * OP : 8];
+    static_assert(OWN || ((NW + 3) / 4) * R * OP <= kKeyTile * ROWH, "staging fits the K/V buffers");
+    uint16_t *stg;
+    if constexpr (OWN) {
+        stg = own_stg + wave * R * OP;
+    } else {
+        const int w4 = wave & 3;
+        stg = (w4 == 0 ? ks0 : (w4 == 1 ? ks1 : (w4 == 2 ? vt0 : vt1))) + (wave >> 2) * R * OP;
+    }
 #pragma unroll
     for (int j = 0; j < NQG; ++j) {
         float l = l_run[j] + __shfl_xor(l_run[j], 16);
@@ -492,9 +511,9 @@ __global__ __launch_bounds__(256) void attention_weights_kernel(const __half *q,
 template <int D, int G>
 void launch_dg(const PrefillArgs &a, int grid, bool paged, hipStream_t stream) {
     if (paged)
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true>), dim3(grid), dim3(kPThreads), 0, stream, a);
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true>), dim3(grid), dim3(kPThreads<D>), 0, stream, a);
     else
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false>), dim3(grid), dim3(kPThreads), 0, stream, a);
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false>), dim3(grid), dim3(kPThreads<D>), 0, stream, a);
 }
 
 template <int D>

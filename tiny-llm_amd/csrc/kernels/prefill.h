@@ -31,9 +31,9 @@ struct PrefillEntry {
 
 static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
 
-// Query tokens per workgroup: 128 query rows (64 for head_dim 256) of
-// (token, head) pairs, G heads of one kv group per token.
-inline int prefill_block_tokens(int D, int G) { return (D <= 128 ? 128 : 64) / G; }
+// Query tokens per workgroup: 256 query rows (8 waves; 64 rows, 4 waves, for
+// head_dim 256) of (token, head) pairs, G heads of one kv group per token.
+inline int prefill_block_tokens(int D, int G) { return (D <= 128 ? 256 : 64) / G; }
 
 // Work items (entry, query tile), most keys first (LPT order for the
 // hardware dispatcher), each a self-contained record of kPrefillItemWords
