@@ -310,7 +310,9 @@ int tl_w8a16_set_path(int path);
  * 0 = VALU v_dot2 over the loaded K rows, 1 = MFMA v_mfma_f32_16x16x32_f16
  * over an LDS-transposed K tile (head_dim <= 128; VALU above), 2 = auto,
  * which resolves to VALU for every supported group (<= 8): both paths are
- * HBM-bound and MFMA was never faster on the measured decode workloads.
+ * HBM-bound and MFMA was never faster on the measured decode workloads;
+ * 3 = both contractions on MFMA (S^T = K Q^T and O^T = V^T P^T, K/V quarters
+ * streamed into LDS by DMA; head_dim 64 and 128, other head_dims take 2).
  * Both give results within the 1e-3 gate of the same oracle.  Initial value
  * from the environment variable TL_ATTN_QK ("valu" / "mfma" / "auto"), else
  * 2.  No reference counterpart (tuning knob). */

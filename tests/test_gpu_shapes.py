@@ -36,7 +36,7 @@ def f16bits(rng, shape):
 @pytest.mark.parametrize("paged", [False, True])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 @pytest.mark.parametrize("D", [32, 64, 128, 256])
-@pytest.mark.parametrize("path", [0, 1])
+@pytest.mark.parametrize("path", [0, 1, 3])
 def test_decode_step_all_shapes(tl, orc, score_path, waves, monkeypatch, path, D, G, paged, chunk,
                                 nw):
     """chunk=256 forces the smallest work items (one 64-token tile per wave,

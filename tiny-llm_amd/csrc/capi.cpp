@@ -460,8 +460,9 @@ void tl_get_attention_weights(const void *q, const void *k, void *weights, float
 }
 
 int tl_attn_set_score_path(int path) {
-    if (path < 0 || path > 2)
-        return fail(TL_ERR_INVALID, "tl_attn_set_score_path: path must be 0 (valu), 1 (mfma) or 2 (auto)");
+    if (path < 0 || path > 3)
+        return fail(TL_ERR_INVALID,
+                    "tl_attn_set_score_path: path must be 0 (valu), 1 (mfma), 2 (auto) or 3 (mma)");
     tiny_llm::detail::set_score_path(path);
     return TL_OK;
 }

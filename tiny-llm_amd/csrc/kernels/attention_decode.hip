@@ -700,6 +700,256 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     }
 }
 
+// ----------------------------------------------------------------- MMA path
+// Decode attention with both contractions on MFMA (head_dim 64 and 128).
+// Each wave streams 16-token quarters of its tiles (wave w: tiles w, w+NW,
+// ...) straight from HBM into its own LDS with the LDS DMA load
+// (global_load_lds, 16 bytes per lane, whole rows per instruction), the next
+// quarter in flight in the other buffer while the current one is computed;
+// no workgroup barrier until the final combine.  Per quarter:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = K rows (token l%16, dims
+//                 8(l/16) + 32ks), B = q (head l%16, same dims; zero for heads
+//                 >= G) -> lane: tokens 4(l/16)+i of head l%16
+//   softmax       per head column in the log2 domain, lazy rescale (the
+//                 reference point moves only on jumps above 2^8)
+//   O^T += V^T P^T  v_mfma_f32_16x16x16_f16, A = V^T (dim l%16, tokens
+//                 4(l/16)..+3) by ds_read_b64_tr_b16 from the row-major V
+//                 rows, B = P^T exactly as the S^T fragment holds it.
+// The combine across waves, the partials and the fused append are those of
+// attn_decode_kernel.
+constexpr float kMmaLazy = 8.0f;
+constexpr int   kVmcntAll = 0x0F70; // s_waitcnt vmcnt(0)
+
+typedef _Float16 f16x4m __attribute__((ext_vector_type(4)));
+typedef short    s16x4m __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __attribute__((address_space(3))) s16x4m *mma_lds(const uint16_t *p) {
+    return (__attribute__((address_space(3))) s16x4m *)(p);
+}
+
+template <int D, int G, bool PAGED, int kNW>
+__global__ __launch_bounds__(kNW * 64) void attn_decode_mma_kernel(AttnArgs a) {
+    static_assert(D == 64 || D == 128, "head_dim");
+    static_assert(G >= 1 && G <= 8, "group size");
+    constexpr int kThreads = kNW * 64;
+    constexpr int KP = D / 8;          // 16-byte pieces per row
+    constexpr int QH = 16 * D;         // halves of one 16-row quarter (K or V)
+    constexpr int NQI = 16 * KP / 64;  // DMA pieces per lane per quarter and operand
+    constexpr int KS = D / 32;         // k steps of S^T
+    constexpr int DT = D / 16;         // dim tiles of O^T
+    // Two buffers as distinct arrays (quarter k uses buffer k & 1), so the
+    // compiler sees that the DMA into one does not alias reads of the other.
+    __shared__ __align__(16) uint16_t qk0[kNW * QH], qv0[kNW * QH], qk1[kNW * QH], qv1[kNW * QH];
+    __shared__ float sm_m[kNW * G], sm_l[kNW * G];
+    // piece x of quarter row r at slot r * KP + (x ^ (r % KP))
+    auto slot = [](int r, int x) { return r * KP + (x ^ (r & (KP - 1))); };
+
+    const int       lane = threadIdx.x & 63;
+    // wave-uniform in a scalar register: the quarter loop's branches then
+    // stay scalar, and the compiler's vmcnt bookkeeping survives them
+    const int       wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const AttnPlan &pl = a.plan;
+    const int       item = blockIdx.x / a.Hkv;
+    const int       g = blockIdx.x - item * a.Hkv;
+    int             b, c, S, nch, widx, row;
+    if (a.meta.n) {
+        const int32_t *w = a.meta.w;
+        b = w[a.meta.off_work + 2 * item];
+        c = w[a.meta.off_work + 2 * item + 1];
+        S = w[b];
+        const int pb = w[a.meta.off_part + b];
+        nch = w[a.meta.off_part + b + 1] - pb;
+        widx = pb + c;
+        row = a.meta.has_rows ? w[a.meta.off_rows + b] : b;
+    } else {
+        if (pl.work) {
+            b = pl.work[2 * item];
+            c = pl.work[2 * item + 1];
+        } else {
+            b = item / pl.nchunk;
+            c = item - b * pl.nchunk;
+        }
+        S = pl.seq_lens ? pl.seq_lens[b] : pl.uniform_len;
+        nch = pl.part_base ? pl.part_base[b + 1] - pl.part_base[b] : pl.nchunk;
+        widx = pl.part_base ? pl.part_base[b] + c : item;
+        row = a.kv.seq_row ? a.kv.seq_row[b] : b;
+    }
+    const int t0 = c * pl.chunk;
+    const int n = __builtin_amdgcn_readfirstlane(min(pl.chunk, S - t0));
+    const RowAddr<PAGED> ra(a.kv, row, g);
+
+    if (a.new_k && c == nch - 1) {
+        // Fused appendKV(n=1) of head g at position S-1 (kv_cache.cpp:230-233).
+        const int tid = threadIdx.x;
+        if (tid < 2 * KP) {
+            const int     which = tid / KP, e = tid - which * KP;
+            const __half *src = (which ? a.new_v : a.new_k) + ((int64_t)b * a.Hkv + g) * D + e * 8;
+            const char   *base = which ? ra.vbase : ra.kbase;
+            char         *dst = const_cast<char *>(base) + ra.lane_off(S - 1) + 16 * e;
+            *reinterpret_cast<uint4 *>(dst) = *reinterpret_cast<const uint4 *>(src);
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
+
+    // q as the B operand of S^T: head l%16 (< G), dims 8(l/16) + 32ks
+    const int hc = lane & 15, kq = lane >> 4;
+    f16x8     qb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (hc < G)
+            v = *reinterpret_cast<const uint4 *>(a.q + ((int64_t)b * a.Hq + (int64_t)g * G + hc) * D +
+                                                 8 * kq + 32 * ks);
+        qb[ks] = __builtin_bit_cast(f16x8, v);
+    }
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // The wave's quarters: k -> tile wave + kNW * (k / 4), quarter k % 4.
+    auto qstart = [&](int k) { return (wave + kNW * (k >> 2)) * kTile + 16 * (k & 3); };
+    uint16_t *k0 = qk0 + wave * QH, *v0 = qv0 + wave * QH, *k1 = qk1 + wave * QH, *v1 = qv1 + wave * QH;
+    // DMA of quarter k: K rows into kbuf, V rows into vbuf.
+    auto issue = [&](int k, uint16_t *kbuf, uint16_t *vbuf) {
+        const int qs = min(qstart(k), n - 1); // past the end: the last row again (a harmless re-read)
+        int64_t   blk = 0;
+        if constexpr (PAGED) blk = (int64_t)ra.bt_row[(t0 + qs) >> ra.log2_blk] * ra.blk_bytes; // uniform
+#pragma unroll
+        for (int u = 0; u < NQI; ++u) {
+            const int    sl = u * 64 + lane;
+            const int    r = sl / KP, x = (sl % KP) ^ (r & (KP - 1));
+            const int    t = t0 + min(qs + r, n - 1);
+            const int64_t off = blk + (int64_t)ra.in_block(t) + 16 * x;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(ra.kbase + off),
+                                             (__attribute__((address_space(3))) void *)(kbuf + u * 512), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(ra.vbase + off),
+                                             (__attribute__((address_space(3))) void *)(vbuf + u * 512), 16, 0, 0);
+        }
+    };
+    // The fragments of one quarter from LDS: K rows as the A operand of S^T
+    // (token hc, pieces kq + 4ks) and V^T by the transposing read (lane i of
+    // each 16-lane group names 4 dims of one V row; afterwards lane i holds
+    // dim 16dt + i of rows 4kq .. 4kq+3).
+    struct Frags {
+        f16x8  kf[KS];
+        s16x4m vf[DT];
+    };
+    auto read_frags = [&](const uint16_t *kb, const uint16_t *vb, Frags &f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) f.kf[ks] = *reinterpret_cast<const f16x8 *>(&kb[slot(hc, kq + 4 * ks) * 8]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int vr = 4 * kq + (hc >> 2), vx = 2 * dt + ((hc & 3) >> 1), vh = 4 * (hc & 1);
+            f.vf[dt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(mma_lds(&vb[slot(vr, vx) * 8 + vh]));
+        }
+    };
+    // One quarter from its fragments.
+    auto quarter = [&](int k, const Frags &f) __attribute__((always_inline)) {
+        const int qs = qstart(k);
+        f32x4     st = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.kf[ks], qb[ks], st, 0, 0, 0);
+        float sv[4];
+        float mq = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = qs + 4 * kq + i < n ? st[i] * a.scale_log2 : -INFINITY;
+            mq = fmaxf(mq, sv[i]);
+        }
+        mq = fmaxf(mq, __shfl_xor(mq, 16));
+        mq = fmaxf(mq, __shfl_xor(mq, 32));
+        if (__any(mq > m_run + kMmaLazy)) {
+            const float m_new = fmaxf(m_run, mq);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new); // 0 on the first quarter
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+            l_run *= alpha;
+            m_run = m_new;
+        }
+        f16x4m pb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float    pv = sv[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[i] - m_run);
+            const _Float16 ph = (_Float16)pv;
+            l_run += (float)ph; // the normaliser sums the weights the MFMA uses
+            pb[i] = ph;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4m, f.vf[dt]), pb, acc[dt], 0, 0,
+                                                            0);
+    };
+
+    // Quarter k: wait for its DMA (the only one in flight), read its
+    // fragments, issue quarter k+1's DMA into the other buffers, compute.
+    // The reads precede the next DMA, so nothing in flight can alias them.
+    if (qstart(0) < n) {
+        issue(0, k0, v0);
+        Frags f;
+        for (int k = 0;; k += 2) {
+            __builtin_amdgcn_s_waitcnt(kVmcntAll);
+            read_frags(k0, v0, f);
+            const bool more1 = qstart(k + 1) < n;
+            if (more1) issue(k + 1, k1, v1);
+            quarter(k, f);
+            if (!more1) break;
+            __builtin_amdgcn_s_waitcnt(kVmcntAll);
+            read_frags(k1, v1, f);
+            const bool more2 = qstart(k + 2) < n;
+            if (more2) issue(k + 2, k0, v0);
+            quarter(k + 1, f);
+            if (!more2) break;
+        }
+    }
+
+    // ---- per-wave (m, l, o) -> LDS, combine the waves, emit
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    __syncthreads(); // every wave is done with the quarter buffers
+    float *so = reinterpret_cast<float *>(qk0) + wave * G * D;
+    static_assert(G * D * 4 <= QH * 2, "a wave's o fits its quarter of qk0");
+    if (hc < G) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+            *reinterpret_cast<float4 *>(so + hc * D + 16 * dt + 4 * kq) =
+                make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+        if (kq == 0) {
+            const bool any = qstart(0) < n;
+            sm_m[wave * G + hc] = any ? m_run : -INFINITY;
+            sm_l[wave * G + hc] = any ? l_run : 0.0f;
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+        const int h = idx / D;
+        const int d = idx - h * D;
+        float     mh = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kNW; ++w) mh = fmaxf(mh, sm_m[w * G + h]);
+        float o = 0.0f, lh = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kNW; ++w) {
+            const float mw = sm_m[w * G + h];
+            const float wgt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mh);
+            o = fmaf(wgt, reinterpret_cast<const float *>(qk0)[w * G * D + idx], o);
+            lh = fmaf(wgt, sm_l[w * G + h], lh);
+        }
+        const int64_t orow = (int64_t)b * a.Hq + (int64_t)g * G + h;
+        if (nch == 1) {
+            a.out[orow * D + d] = __float2half(o * (1.0f / (lh + 1e-6f)));
+        } else {
+            const int64_t prow = (int64_t)widx * a.Hq + (int64_t)g * G + h;
+            a.part_o[prow * D + d] = o;
+            if (d == 0) {
+                a.part_ml[prow * 2] = mh;
+                a.part_ml[prow * 2 + 1] = lh;
+            }
+        }
+    }
+}
+
 struct MergeArgs {
     const float   *part_o;  // [n_work][Hq][D]
     const float   *part_ml; // [n_work][Hq][2]
@@ -802,6 +1052,29 @@ void launch_merge_g(const MergeArgs &m, int B, int Hkv, int G, hipStream_t strea
     }
 }
 
+template <int D, int G>
+void launch_mma_dg(const AttnArgs &args, int n_work, int Hkv, bool paged, int nw, hipStream_t stream) {
+    const dim3 grid((unsigned)n_work * (unsigned)Hkv);
+    if (nw == 8) {
+        if (paged) hipLaunchKernelGGL((attn_decode_mma_kernel<D, G, true, 8>), grid, dim3(512), 0, stream, args);
+        else hipLaunchKernelGGL((attn_decode_mma_kernel<D, G, false, 8>), grid, dim3(512), 0, stream, args);
+    } else {
+        if (paged) hipLaunchKernelGGL((attn_decode_mma_kernel<D, G, true, 4>), grid, dim3(256), 0, stream, args);
+        else hipLaunchKernelGGL((attn_decode_mma_kernel<D, G, false, 4>), grid, dim3(256), 0, stream, args);
+    }
+}
+
+template <int D>
+void launch_mma_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, int nw, hipStream_t stream) {
+    switch (G) {
+    case 1: launch_mma_dg<D, 1>(args, n_work, Hkv, paged, nw, stream); break;
+    case 2: launch_mma_dg<D, 2>(args, n_work, Hkv, paged, nw, stream); break;
+    case 4: launch_mma_dg<D, 4>(args, n_work, Hkv, paged, nw, stream); break;
+    case 8: launch_mma_dg<D, 8>(args, n_work, Hkv, paged, nw, stream); break;
+    default: break;
+    }
+}
+
 template <int D, int G, bool PAGED, bool MFMA, int NW>
 void launch_one(const AttnArgs &args, int n_work, int Hkv, hipStream_t stream) {
     using SM = Smem<D, G, MFMA, NW>;
@@ -850,12 +1123,13 @@ void launch_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool
     }
 }
 
-// Score path: TL_ATTN_QK ("valu" / "mfma" / "auto") at first use, else
-// auto; tl_attn_set_score_path overrides it.  Auto resolves to VALU for every
-// supported group: measured on the decode workloads (group 4 and 8, uniform
-// and ragged contexts) the MFMA path is never faster -- both are HBM-bound,
-// and at group 8 the MFMA path's LDS staging and K double buffer spill a few
-// more registers than the VALU path.
+// Score path: TL_ATTN_QK ("valu" / "mfma" / "auto" / "mma") at first use,
+// else auto; tl_attn_set_score_path overrides it.  Within attn_decode_kernel
+// auto resolves to VALU for every supported group: measured on the decode
+// workloads (group 4 and 8, uniform and ragged contexts) its MFMA score path
+// is never faster -- both are HBM-bound, and at group 8 the MFMA path's LDS
+// staging and K double buffer spill a few more registers than the VALU path.
+// Path 3 runs attn_decode_mma_kernel instead (use_mma_path).
 std::atomic<int> g_score_path{-1};
 
 int score_path_setting() {
@@ -865,9 +1139,21 @@ int score_path_setting() {
         v = 2;
         if (e && std::strcmp(e, "mfma") == 0) v = 1;
         if (e && std::strcmp(e, "valu") == 0) v = 0;
+        if (e && std::strcmp(e, "mma") == 0) v = 3;
         g_score_path.store(v);
     }
     return v;
+}
+
+// Both contractions on MFMA (attn_decode_mma_kernel), path 3 only.  Measured
+// against attn_decode_kernel (VALU scores): group 8 on the Llama-3-8B decode
+// shape with 64 q heads 377 vs 397 us per step, but group 4 375 vs 334 and
+// the ragged group-8 churn workload 1100 vs about 1060: each wave keeps one
+// 16-token quarter in flight, which caps its stream, so auto stays on the
+// VALU kernel.
+bool use_mma_path(int D, int G) {
+    (void)G;
+    return (D == 64 || D == 128) && score_path_setting() == 3;
 }
 
 bool use_mfma_scores(int D, int G) {
@@ -1037,7 +1323,14 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     if (inl) std::memcpy(&args.meta, inl, sizeof(InlineMeta));
     else args.meta.n = 0;
 
-    if (plan.n_work > 0) {
+    if (plan.n_work > 0 && use_mma_path(D, G)) {
+        const int nw = waves_for((int64_t)plan.n_work * Hkv);
+        profile_begin(KernelId::AttnChunk, stream);
+        if (D == 64) launch_mma_d<64>(args, plan.n_work, Hkv, G, paged, nw, stream);
+        else launch_mma_d<128>(args, plan.n_work, Hkv, G, paged, nw, stream);
+        HIP_CHECK(hipGetLastError());
+        profile_end(KernelId::AttnChunk, stream);
+    } else if (plan.n_work > 0) {
         const int nw = waves_for((int64_t)plan.n_work * Hkv);
         profile_begin(KernelId::AttnChunk, stream);
         switch (D) {

@@ -406,11 +406,13 @@ def attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, s
 SCORE_VALU = 0
 SCORE_MFMA = 1
 SCORE_AUTO = 2
+SCORE_MMA = 3
 
 
 def set_score_path(path: int):
     """0 = VALU dot products, 1 = MFMA over an LDS-transposed K tile,
-    2 = auto (VALU for every supported group)."""
+    2 = auto (VALU for every supported group), 3 = both contractions on MFMA
+    (head_dim 64 and 128; other head_dims take the auto kernel)."""
     _check(load().tl_attn_set_score_path(path))
 
 
