@@ -172,6 +172,28 @@ def test_w8a16_packed_matches_oracle(tl, orc, M, N, K, gs):
     assert np.array_equal(to_host(dh3), got_p)
 
 
+def test_w8a16_packed_interleaved_shapes_repeat_bits(tl, orc):
+    """Interleaved packed calls of shapes with different row-tile, column-tile
+    and split counts (sharing the library's split-K workspace) each give their
+    first call's bits again."""
+    rng = np.random.default_rng(77)
+    runs = []
+    for M, N, K, gs in [(64, 512, 4096, 128), (130, 96, 1056, 64), (200, 320, 2048, 32)]:
+        x, w, s = operands(orc, rng, M, N, K, gs)
+        dx, dp, ds = to_dev(x), packed_dev(tl, w), to_dev(s)
+        runs.append((M, N, K, gs, dx, dp, ds))
+
+    def call(M, N, K, gs, dx, dp, ds):
+        dh = to_dev(np.zeros((M, N), np.uint16))
+        tl.w8a16_matmul_residual(dx.data_ptr(), dp.data_ptr(), ds.data_ptr(), dh.data_ptr(), M, N, K,
+                                 gs, stream(), packed=True)
+        return to_host(dh)
+    first = [call(*r) for r in runs]
+    for _ in range(2):
+        for r, f in zip(reversed(runs), reversed(first)):
+            assert np.array_equal(call(*r), f)
+
+
 def test_w8a16_nonpositive_dims_noop(tl):
     out = to_dev(np.full((2, 16), 0x3C00, np.uint16))
     tl.w8a16_matmul(0, 0, 0, out.data_ptr(), 0, 16, 32, 32, stream())  # M = 0
