@@ -13,9 +13,10 @@
 // Packed weights (w8a16_sk_kernel, the fast path; layout of
 // launch_w8a16_pack): one workgroup = 4 waves = a 64x64 output tile over one
 // split; wave w takes every fourth group of 4 k steps for the whole tile,
-// with W fragments (8 bytes per lane) and x fragments (16 bytes per lane)
-// loaded straight into MFMA operands -- no staging, no barrier until the
-// waves' tiles are summed through LDS.
+// with W fragments (8 bytes per lane) loaded straight into MFMA operands and
+// x staged two k steps at a time in the wave's own LDS by the LDS DMA load
+// (coalesced rows) -- no barrier until the waves' tiles are summed through
+// LDS.
 //
 // Reference layout (w8a16_mfma_kernel):
 //   One workgroup = 4 waves = a 64-row x 64-column output tile over one split
@@ -73,6 +74,8 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kRing = 8;      // chunks whose loads are issued together
 constexpr int kXPitch = kBK + 8; // halves per staged x row (16-byte pad)
 constexpr int kWPitch = kBK + 8; // halves per staged transposed W column (16-byte rows)
+constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0)
+constexpr int kWaitLgkm0 = 0xC07F; // s_waitcnt lgkmcnt(0)
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
@@ -343,9 +346,8 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
 // Packed-weight kernel, split-K inside the workgroup: one workgroup (4 waves)
 // per unit (64-row tile, 64-column tile, K split); wave w takes k steps
 // 4w..4w+3 of every 16-step (512-row) batch of the split for the whole 64x64
-// tile, with its operands straight from global memory (W: 8 bytes per lane
-// per fragment, packed; x: 16 bytes per lane per fragment, two steps ahead),
-// 16 MFMAs per step.  Scale groups are folded in step order.  The four
+// tile, W straight from global memory (8 bytes per lane per fragment,
+// packed), x through the wave's LDS stage (below), 16 MFMAs per step.  Scale groups are folded in step order.  The four
 // waves' tiles are summed through LDS in wave order, wave w finishing row
 // block w (each wave passes on the three row blocks it does not finish: 48
 // KB of LDS, three workgroups per CU).  ACC: a second accumulator for
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
     static_assert(ACC || NS == 1, "several groups per wave need the accumulator");
     __shared__ __align__(16) float red[4 * 3 * 4 * 64 * 4]; // [src wave][rb != src][cb][lane][4]
     const int     lane = threadIdx.x & 63;
-    const int     wave = threadIdx.x >> 6;
+    const int     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int     unit = blockIdx.x;
     const int     split = unit % a.splits;
     const int     rest = unit / a.splits;
@@ -381,18 +383,43 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
     const int       ngroups = (a.K + GS - 1) / GS;
     const int       m0 = mt * kBM;
 
-    const int8_t *wp[4];
+    const int8_t *wp[4]; // uniform column-block bases; lanes add 8 * lane (+ 512 per step)
     const __half *sp[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
         const int nb = min((c0 >> 4) + cb, nblk - 1);
-        wp[cb] = sg.w + ((int64_t)nb * ksteps * 64 + lane) * 8;
-        sp[cb] = sg.s + 16 * nb + (lane & 15);
+        wp[cb] = sg.w + (int64_t)nb * ksteps * 512;
+        sp[cb] = sg.s + 16 * nb;
     }
-    const __half *xp[4];
+    // x reaches the MFMA through LDS: a wave stages two k steps of its 64 rows
+    // (128 bytes per row, 8 KB) with the LDS DMA load, whole 128-byte row
+    // pieces per 8 lanes, so that a load instruction touches 8 cache lines
+    // (the A-layout load straight from global memory touches 64: 16 rows per
+    // 16 lanes).  Row r's 16-byte chunk c sits in slot c ^ f(r) of the row,
+    // f(r) = (r & 7) ^ ((r >> 3) & 1), so that the fragment reads (16 rows,
+    // one chunk) fall on distinct banks.  The stage lives in `red`, which the
+    // waves use for the cross-wave sum only after the main loop.
+    uint16_t *const xs = reinterpret_cast<uint16_t *>(red) + wave * 4096;
+    const __half   *xt = a.x + (int64_t)m0 * a.ldx; // the row tile (32-bit offsets below)
+    auto issue_x = [&](int st0) __attribute__((always_inline)) { // steps st0, st0 + 1
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-        xp[rb] = a.x + (int64_t)min(m0 + 16 * rb + (lane & 15), a.M - 1) * a.ldx + 8 * (lane >> 4);
+        for (int u = 0; u < 8; ++u) {
+            const int      c = (lane & 7) ^ (lane >> 3) ^ (u & 1);
+            const int      st = min(st0 + (c >> 2), ksteps - 1);
+            const int      row = min(8 * u + (lane >> 3), a.M - 1 - m0);
+            const uint32_t off = (uint32_t)row * (uint32_t)a.ldx + (uint32_t)(32 * st + 8 * (c & 3));
+            const __half  *src = xt + off;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                             (__attribute__((address_space(3))) void *)(xs + u * 512), 16, 0, 0);
+        }
+    };
+    auto read_x = [&](int s, f16x8(&dst)[4]) __attribute__((always_inline)) { // step s of the stage
+        const int c = 4 * s + (lane >> 4);
+        const int p = c ^ (lane & 7) ^ ((lane >> 3) & 1);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+            dst[rb] = *reinterpret_cast<const f16x8 *>(xs + (2 * rb + ((lane & 15) >> 3)) * 512 + (lane & 7) * 64 + 8 * p);
+    };
 
     f32x4 P[4][4], acc[4][4];
 #pragma unroll
@@ -408,21 +435,14 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
         const int first = sb + 4 * wave; // this wave's 4 steps
         const int nsteps = max(0, min(4, s_end - first));
         if (nsteps == 0) continue;
+        issue_x(first); // x first (L2 hits), then W (HBM)
         uint2 wv[4][4];
-        f16x8 xv[2][4];
-        auto  load_x = [&](int j, f16x8(&dst)[4]) __attribute__((always_inline)) {
-            const int st = min(first + j, ksteps - 1);
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) dst[rb] = *reinterpret_cast<const f16x8 *>(xp[rb] + 32 * st);
-        };
-        load_x(0, xv[0]); // x first (L2 hits), then W (HBM)
-        load_x(1, xv[1]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int st = min(first + j, ksteps - 1);
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
-                wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + (int64_t)st * 512);
+                wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + (uint32_t)(st * 512 + 8 * lane));
         }
         uint16_t sraw[NS][4];
 #pragma unroll
@@ -430,21 +450,30 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
                 sraw[g][cb] = *reinterpret_cast<const uint16_t *>(
-                    sp[cb] + (int64_t)min((first + g * SPG) * 32 / GS, ngroups - 1) * sg.n);
+                    sp[cb] + (uint32_t)(min((first + g * SPG) * 32 / GS, ngroups - 1) * sg.n + (lane & 15)));
+        f16x8 xv[2][4];
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        read_x(0, xv[0]);
+        read_x(1, xv[1]);
+        if (nsteps > 2) { // the stage's reads complete before the DMA refills it
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            issue_x(first + 2);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if (j >= nsteps) continue; // uniform
-            f16x8 xa[4];
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) xa[rb] = xv[j & 1][rb];
-            if (j + 2 < 4) load_x(j + 2, xv[j & 1]);
+            if (j == 2) {
+                __builtin_amdgcn_s_waitcnt(kWaitVm0);
+                read_x(0, xv[0]);
+                read_x(1, xv[1]);
+            }
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) {
                 const uint2 lo = i8x4_to_f16x4(wv[j][cb].x), hi = i8x4_to_f16x4(wv[j][cb].y);
                 const f16x8 bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb)
-                    P[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rb], bop, P[rb][cb], 0, 0, 0);
+                    P[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv[j & 1][rb], bop, P[rb][cb], 0, 0, 0);
             }
             if constexpr (ACC) {
                 if ((j + 1) % SPG == 0 || j + 1 == nsteps) { // end of a group or of the wave's steps
@@ -465,6 +494,8 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) s_last[cb] = h2f(__builtin_bit_cast(__half, sraw[0][cb]));
         }
+        // the next batch's DMA refills the stage: its reads are complete
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     }
     // The wave's result r = acc, or P * s.
     if constexpr (!ACC) {
@@ -476,6 +507,8 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
                 for (int i = 0; i < 4; ++i) acc[rb][cb][i] = P[rb][cb][i] * s_last[cb];
     }
 
+    __builtin_amdgcn_s_waitcnt(kWaitVm0); // no DMA into the stage is still in flight
+    __syncthreads();                      // every wave is done with its x stage in `red`
     // Pass on the three row blocks this wave does not finish.
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
