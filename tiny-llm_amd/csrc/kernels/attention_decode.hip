@@ -29,7 +29,9 @@
 //            batch (and, at phase ends, the first batch of the next phase or
 //            tile) is in flight while the current one is consumed.
 //   scores   VALU path: v_dot2_f32_f16 of the lane's 8 dims with the G heads,
-//            DPP sum over the row's LPR lanes; lane p keeps heads h%LPR == p.
+//            DPP sum over the row's LPR lanes; lane p keeps heads h%LPR == p
+//            (16 lanes per row, G >= 2: a transposing DPP reduction, lane p
+//            keeps head f(p); see ValuScorer).
 //            MFMA path: the K rows of 16 tokens go through a padded LDS tile
 //            and are read back in the B layout of v_mfma_f32_16x16x32_f16
 //            with q as the A operand (G of its 16 rows non-zero).
@@ -251,23 +253,63 @@ struct Smem {
 // lane is responsible for; it turns the K batches of a tile into fp16 p in
 // LDS and hands the per-head rescale factors to the P.V stage.
 
+// One step of the transposing row reduction: the N slots of every lane are
+// halved by adding the partner's (DPP CTRL) upper half onto the lower half;
+// with one slot left, the partner's slot is added.
+template <int CTRL, int N>
+__device__ __forceinline__ void xpose_step(float *d) {
+    if constexpr (N >= 2) {
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k) d[k] += dpp_f<CTRL>(d[k + N / 2]);
+    } else {
+        d[0] += dpp_f<CTRL>(d[0]);
+    }
+}
+
 // VALU: lane (r = lane / LPR, p = lane % LPR); owner of heads h % LPR == p.
+// With 16 lanes per row and G a power of two >= 2 (XP), the G head sums are
+// instead reduced transposingly: lane p's slot k holds head k ^ f(p), so that
+// adding the partner's upper half of the slots (partners p ^ 15, p ^ 7, p ^ 2,
+// p ^ 1: row_mirror, row_half_mirror, quad_perm) onto the lower half leaves
+// lane p with the row's full sum for head f(p) after G - 1 + (4 - log2 G)
+// DPP adds instead of 4 G.  f is linear in p's bits with f(15) = G/2,
+// f(7) = G/4, f(2) = G/8, f(1) = G/16 (integer division), which is what makes
+// the partner's slot k + N/2 hold the same head as slot k at every step; the
+// 16/G lanes of a head are the p that differ in the low log2(16/G) bits, and
+// the one with those bits zero owns it.
 template <int D, int G>
 struct ValuScorer {
     static constexpr int LPR = D / 8;
     static constexpr int TPI = 64 / LPR;
     static constexpr int NSTEP = kTile / TPI;
     static constexpr int HPL = (G + LPR - 1) / LPR;
+    static constexpr bool XP = LPR == 16 && G >= 2 && G <= 16 && (G & (G - 1)) == 0;
+    static constexpr int  F1 = G / 16, F2 = G / 8, F7 = G / 4, F15 = G / 2;
+    static __device__ __forceinline__ constexpr int fhead(int q) {
+        return ((q & 1) ? F1 : 0) ^ ((q & 2) ? F2 : 0) ^ ((q & 4) ? (F7 ^ F1 ^ F2) : 0) ^ ((q & 8) ? (F15 ^ F7) : 0);
+    }
+    static __device__ __forceinline__ constexpr int owner(int h) { // lane of head h with the low bits zero
+        int q = 0;
+        while (fhead(q) != h || (q & (16 / G - 1)) != 0) ++q;
+        return q;
+    }
     uint4 qv[G];
     float sc[HPL][NSTEP];
     float mrun[HPL], lrun[HPL], alpha[HPL];
     int   r, p;
 
+    // Head of the lane's slot hh, and whether the lane writes its results.
+    __device__ __forceinline__ int lane_head(int hh) const { return XP ? fhead(p) : hh * LPR + p; }
+    __device__ __forceinline__ bool lane_owns(int hh) const {
+        return XP ? (p & (16 / G - 1)) == 0 : hh * LPR + p < G;
+    }
+
     __device__ __forceinline__ void init(const __half *qrow, int lane) {
         r = lane / LPR;
         p = lane % LPR;
+        const int f = XP ? fhead(p) : 0;
 #pragma unroll
-        for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const uint4 *>(qrow + h * D + 8 * p);
+        for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const uint4 *>(qrow + (h ^ f) * D + 8 * p);
 #pragma unroll
         for (int hh = 0; hh < HPL; ++hh) {
             mrun[hh] = -INFINITY;
@@ -276,6 +318,22 @@ struct ValuScorer {
     }
     // Scores of load step s (tokens s*TPI + r of the tile) from the lane's row piece.
     __device__ __forceinline__ void step(int s, uint4 k, bool valid, float scale_log2) {
+        if constexpr (XP) {
+            float d[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                d[h] = fdot2(qv[h].x, k.x, 0.0f);
+                d[h] = fdot2(qv[h].y, k.y, d[h]);
+                d[h] = fdot2(qv[h].z, k.z, d[h]);
+                d[h] = fdot2(qv[h].w, k.w, d[h]);
+            }
+            xpose_step<0x140, G>(d);                       // row_mirror: p ^ 15
+            xpose_step<0x141, (G / 2 > 1 ? G / 2 : 1)>(d); // row_half_mirror: p ^ 7
+            xpose_step<0x4E, (G / 4 > 1 ? G / 4 : 1)>(d);  // quad_perm [2,3,0,1]: p ^ 2
+            xpose_step<0xB1, (G / 8 > 1 ? G / 8 : 1)>(d);  // quad_perm [1,0,3,2]: p ^ 1
+            sc[0][s] = valid ? d[0] * scale_log2 : -INFINITY;
+            return;
+        }
         float mine[HPL];
 #pragma unroll
         for (int hh = 0; hh < HPL; ++hh) mine[hh] = 0.0f;
@@ -295,7 +353,7 @@ struct ValuScorer {
     __device__ __forceinline__ void softmax(uint16_t *pp) {
 #pragma unroll
         for (int hh = 0; hh < HPL; ++hh) {
-            const int h = hh * LPR + p;
+            const int h = lane_head(hh);
             float     m = -INFINITY;
 #pragma unroll
             for (int s = 0; s < NSTEP; ++s) m = fmaxf(m, sc[hh][s]);
@@ -305,7 +363,7 @@ struct ValuScorer {
             alpha[hh] = mrun[hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun[hh] - mnew);
             mrun[hh] = mnew;
             float l = 0.0f;
-            if (h < G) {
+            if (lane_owns(hh)) {
 #pragma unroll
                 for (int s = 0; s < NSTEP; ++s) {
                     const float    pv = sc[hh][s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[hh][s] - mnew);
@@ -319,7 +377,10 @@ struct ValuScorer {
         }
     }
     // Rescale factor of head h, broadcast to every lane.
-    __device__ __forceinline__ float head_alpha(int h) const { return bcast(alpha[h / LPR], h % LPR); }
+    __device__ __forceinline__ float head_alpha(int h) const {
+        if constexpr (XP) return bcast(alpha[0], owner(h));
+        else return bcast(alpha[h / LPR], h % LPR);
+    }
     // Final (m, l) of the lane's heads into LDS.
     __device__ __forceinline__ void finish(float *sm, float *sl) {
 #pragma unroll
@@ -327,8 +388,8 @@ struct ValuScorer {
             float l = lrun[hh];
 #pragma unroll
             for (int off = LPR; off < 64; off <<= 1) l += __shfl_xor(l, off);
-            const int h = hh * LPR + p;
-            if (r == 0 && h < G) {
+            const int h = lane_head(hh);
+            if (r == 0 && lane_owns(hh)) {
                 sm[h] = mrun[hh];
                 sl[h] = l;
             }
