@@ -285,14 +285,19 @@ struct ValuScorer {
     static constexpr int HPL = (G + LPR - 1) / LPR;
     static constexpr bool XP = LPR == 16 && G >= 2 && G <= 16 && (G & (G - 1)) == 0;
     static constexpr int  F1 = G / 16, F2 = G / 8, F7 = G / 4, F15 = G / 2;
-    static __device__ __forceinline__ constexpr int fhead(int q) {
+    static __host__ __device__ constexpr int fhead(int q) {
         return ((q & 1) ? F1 : 0) ^ ((q & 2) ? F2 : 0) ^ ((q & 4) ? (F7 ^ F1 ^ F2) : 0) ^ ((q & 8) ? (F15 ^ F7) : 0);
     }
-    static __device__ __forceinline__ constexpr int owner(int h) { // lane of head h with the low bits zero
-        int q = 0;
-        while (fhead(q) != h || (q & (16 / G - 1)) != 0) ++q;
-        return q;
+    struct Owners {
+        int lane[16];
+    };
+    static constexpr Owners owners() { // lane of head h with the low bits zero
+        Owners o{};
+        for (int q = 15; q >= 0; --q)
+            if ((q & (16 / G - 1)) == 0) o.lane[fhead(q)] = q;
+        return o;
     }
+    static constexpr Owners kOwners = owners();
     uint4 qv[G];
     float sc[HPL][NSTEP];
     float mrun[HPL], lrun[HPL], alpha[HPL];
@@ -378,7 +383,7 @@ struct ValuScorer {
     }
     // Rescale factor of head h, broadcast to every lane.
     __device__ __forceinline__ float head_alpha(int h) const {
-        if constexpr (XP) return bcast(alpha[0], owner(h));
+        if constexpr (XP) return bcast(alpha[0], kOwners.lane[h]);
         else return bcast(alpha[h / LPR], h % LPR);
     }
     // Final (m, l) of the lane's heads into LDS.
