@@ -186,11 +186,10 @@ int tl_kv_batch_gather(tl_kv_batch *batch, int layer, void *k_out, void *v_out, 
  * [ceil(hidden/group_size)][num_heads*head_dim] fp16.  Optionally (wq, sq,
  * q_out all non-NULL) q_out[n][num_q_heads*head_dim] = x @ dequant(wq, sq) in
  * the same launch.  packed != 0: all weights are in the layout of
- * tl_w8a16_pack (the fast path; hidden % 32 == 0 and group_size in
- * {32, 64, 128, 256, 512}); its sums run in another order than the
- * reference-layout kernel's, so the bytes are those of
- * tl_w8a16_matmul_residual(packed) onto zeros, within rounding of
- * tl_w8a16_matmul's.  Does not advance lengths (commit does). */
+ * tl_w8a16_pack (hidden % 32 == 0 and group_size in {32, 64, 128, 256,
+ * 512}); the MFMA kernel reads both layouts into the same fragments and
+ * sums in the same order, so the bytes equal the reference layout's.  Does
+ * not advance lengths (commit does). */
 int tl_kv_batch_project(tl_kv_batch *batch, int layer, const void *x, int hidden, int group_size,
                         const int8_t *wk, const void *sk, const int8_t *wv, const void *sv,
                         const int8_t *wq, const void *sq, void *q_out, int packed, void *stream);

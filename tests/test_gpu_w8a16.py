@@ -148,10 +148,10 @@ PACKED_SHAPES = [sh[:4] for sh in SHAPES if sh[4]] + [
 
 @pytest.mark.parametrize("M,N,K,gs", PACKED_SHAPES)
 def test_w8a16_packed_matches_oracle(tl, orc, M, N, K, gs):
-    """The packed-weight kernel (o_proj + residual onto a zero residual, i.e.
-    fp16(acc)) and the reference-layout MFMA kernel both stay within 1e-3 of
-    the oracle; the packed kernel gives the same bits on a second call
-    (fixed summation order)."""
+    """The MFMA kernel on the reference layout (o_proj + residual onto a zero
+    residual, i.e. fp16(acc)) stays within 1e-3 of the oracle, and on packed
+    weights gives the same bits (same fragments, same summation order), again
+    on a second call."""
     rng = np.random.default_rng(M * 3 + N + K * 5 + gs)
     x, w, s = operands(orc, rng, M, N, K, gs)
     ref32, _ = orc.w8a16_matmul(x, w, s, M, N, K, gs)
@@ -165,7 +165,7 @@ def test_w8a16_packed_matches_oracle(tl, orc, M, N, K, gs):
                              stream(), packed=True)
     got, got_p = to_host(dh), to_host(dh2)
     assert rows_close(got, ref32) <= TOL
-    assert rows_close(got_p, ref32) <= TOL
+    assert np.array_equal(got, got_p)
     dh3 = to_dev(zero)
     tl.w8a16_matmul_residual(dx.data_ptr(), dp.data_ptr(), ds.data_ptr(), dh3.data_ptr(), M, N, K, gs,
                              stream(), packed=True)

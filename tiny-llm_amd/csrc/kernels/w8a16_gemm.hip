@@ -4,41 +4,31 @@
 // with an fp32 accumulator, W [K][N] int8 row-major, scales
 // [ceil(K/gs)][N] fp16.
 //
-// MFMA paths (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
-// N % 16 == 0).  Both split K across workgroups for decode-sized M (the split
+// MFMA path (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
+// N % 16 == 0).  It splits K across workgroups for decode-sized M (the split
 // count depends on (M, K) only, so an output element's value does not depend
-// on which other weight matrices share the launch) and sum the splits in a
+// on which other weight matrices share the launch) and sums the splits in a
 // fixed order, so results are deterministic.
 //
-// Packed weights (w8a16_sk_kernel, the fast path; layout of
-// launch_w8a16_pack): one workgroup = 4 waves = a 64x64 output tile over one
-// split; wave w takes every fourth group of 4 k steps for the whole tile,
-// with W fragments (8 bytes per lane) loaded straight into MFMA operands and
-// x staged two k steps at a time in the wave's own LDS by the LDS DMA load
-// (coalesced rows) -- no barrier until the waves' tiles are summed through
-// LDS.
+// One kernel, w8a16_sk_kernel, for both weight layouts: one workgroup = 4
+// waves = a 64x64 output tile over one split; wave w takes every fourth group
+// of 4 k steps for the whole tile (16 MFMAs per step: 4 row blocks x 4
+// column blocks of v_mfma_f32_16x16x32_f16 on the integer weights, converted
+// to fp16 exactly; each scale group's product folded into the fp32
+// accumulator with its scale).  x is staged two k steps at a time in the
+// wave's own LDS by the LDS DMA load (coalesced rows).  W:
+//   packed (layout of launch_w8a16_pack): B fragments, 8 bytes per lane,
+//     loaded straight into registers;
+//   reference ([K][N] row-major): two k steps of the tile's 64 columns staged
+//     in LDS by the DMA load and read as B fragments by the transposing
+//     ds_read_b64_tr_b8.
+// Both layouts give the same fragments and the same summation order, hence
+// the same bits.  No barrier until the waves' tiles are summed through LDS.
 //
-// Reference layout (w8a16_mfma_kernel):
-//   One workgroup = 4 waves = a 64-row x 64-column output tile over one split
-//   of K (split-K across workgroups when the tiles alone would leave CUs
-//   idle).  Per 64-row K chunk:
-//     - the x chunk [64 rows][64 k] fp16 is loaded cooperatively and staged in
-//       LDS (row-major, padded), read back in the A layout of
-//       v_mfma_f32_16x16x32_f16 (lane l: row l%16, k 8*(l/16)..+7);
-//     - the W chunk [64 k][64 columns] int8 is loaded cooperatively as
-//       dwords (4 rows x 4 columns per thread), transposed in registers,
-//       converted to fp16 (exact) and stored [column][k] in LDS, read back in
-//       the B layout (lane l: column l%16, k 8*(l/16)..+7); wave w owns
-//       columns 16w..16w+15;
-//     - two 32-deep k steps of MFMA on the integer weights; at the end of each
-//       scale group the group's partial product is folded into the fp32
-//       accumulator with its scale: acc += P_g * s[g][n] (a k step never
-//       straddles groups, and the fold points are compile-time constants).
-//   The loads of up to 8 chunks are issued before the first is consumed.
 // With one split the GEMM kernel applies the epilogue directly; otherwise it
 // writes fp32 partials and w8a16_reduce_kernel sums the splits in split order
-// and applies the epilogue.  The two MFMA kernels sum in different orders, so
-// their results agree to within rounding, not bit for bit.
+// and applies the epilogue.
+//
 // Generic path (any shape): one thread per output, the reference formula
 // sum = fma(x, w * s, sum) over k in order.
 //
@@ -67,18 +57,15 @@ namespace detail {
 namespace {
 
 constexpr int kBM = 64;       // rows per workgroup
-constexpr int kBN = 64;       // columns per workgroup (16 per wave)
-constexpr int kBK = 64;       // k rows per chunk
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kRing = 8;      // chunks whose loads are issued together
-constexpr int kXPitch = kBK + 8; // halves per staged x row (16-byte pad)
-constexpr int kWPitch = kBK + 8; // halves per staged transposed W column (16-byte rows)
+constexpr int kBN = 64;       // columns per workgroup
+constexpr int kBK = 64;       // k rows per chunk (split sizes count chunks)
+constexpr int kRing = 8;      // chunks per 512-row batch
 constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0)
 constexpr int kWaitLgkm0 = 0xC07F; // s_waitcnt lgkmcnt(0)
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef int      v2i32 __attribute__((ext_vector_type(2)));
 
 struct GemmArgs {
     const __half *x; // [M][K]
@@ -89,7 +76,6 @@ struct GemmArgs {
     int           chunks_per_split; // 64-row chunks of K per split
     int           tiles;            // column tiles over all segments
     int           mtiles;           // row tiles
-    int           units;            // column-tile pairs x splits x row tiles
     float        *partial;          // [splits][M][ntot] when splits > 1
     int           ntot;
     W8A16Seg      seg[kMaxSegs];
@@ -123,22 +109,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, int si, int m, int n
     }
 }
 
-// Byte transpose of a 4x4 block: d[r] holds columns 0..3 of row r; returns
-// c[j] = (row 0..3 of column j).
-__device__ __forceinline__ void transpose4x4(const uint32_t (&d)[4], uint32_t (&c)[4]) {
-    const uint32_t lo01 = __builtin_amdgcn_perm(d[1], d[0], 0x05010400u); // r0c0 r1c0 r0c1 r1c1
-    const uint32_t hi01 = __builtin_amdgcn_perm(d[1], d[0], 0x07030602u); // r0c2 r1c2 r0c3 r1c3
-    const uint32_t lo23 = __builtin_amdgcn_perm(d[3], d[2], 0x05010400u);
-    const uint32_t hi23 = __builtin_amdgcn_perm(d[3], d[2], 0x07030602u);
-    c[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-    c[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-    c[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-    c[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-}
-
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// Four signed bytes -> four fp16 (exact), packed for one 8-byte LDS store.
+// Four signed bytes -> four fp16 (exact), as two dwords of an MFMA operand.
 // u = b + 128 (b ^ 0x80) placed in the mantissa of 0x6400 (1024.0) is the
 // fp16 value 1024 + u; subtracting 1152 leaves b exactly.
 __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t v) {
@@ -150,210 +123,18 @@ __device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t v) {
                       __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) + bias));
 }
 
-// Workgroup (4 waves, 256 threads) -> (64-row tile, 64-column tile, K split).
-// Grid layout: the two column tiles of a pair (which share the 128-byte
-// lines of every weight row) get block indices 8 apart, i.e. the same XCD
-// under the round-robin dispatch of workgroups to XCDs, so each line is read
-// from HBM into one L2 once.  K is processed in batches of kRing 64-row
-// chunks; a batch starts on a multiple of 512 rows, so with GS | 512 its scale
-// groups are fixed at compile time: the batch's scales (one per lane and
-// group), W (four dwords per thread per chunk: rows 4*(t/16)..+3, columns
-// 4*(t%16)..+3) and x (two 16-byte pieces per thread per chunk) are all
-// issued before the first chunk is consumed, and the partial product of each
-// group is folded into the accumulator at a static point.  Per chunk: W is
-// transposed in registers (v_perm), converted to fp16 and stored [column][k]
-// with 8-byte LDS writes, x is staged with 16-byte writes, then two 32-deep
-// MFMA k-steps per 16-row block.
-template <int GS>
-__global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(GemmArgs a) {
-    static_assert(GS % 32 == 0 && (kRing * kBK) % GS == 0, "group size");
-    constexpr int SPG = GS / 32;                 // k steps per scale group
-    constexpr int NG = kRing * kBK / GS;         // scale groups per batch
-    // Double-buffered staging: chunk j uses buffer j & 1, so one barrier per
-    // chunk suffices (a buffer is rewritten two chunks later, after every
-    // wave has passed the intervening barrier, i.e. finished reading it).
-    __shared__ __align__(16) _Float16 xs[2][kBM * kXPitch];
-    __shared__ __align__(16) _Float16 wt[2][kBN * kWPitch];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int t = threadIdx.x;
-    // block -> (unit, half); unit -> (pair, split, m tile)
-    const int b = blockIdx.x;
-    const int unit = (b >> 4) * 8 + (b & 7);
-    const int half = (b >> 3) & 1;
-    if (unit >= a.units) return;
-    const int mt = unit % a.mtiles;
-    const int rest = unit / a.mtiles;
-    const int split = rest % a.splits;
-    const int pair = rest / a.splits;
-    int       tile = 2 * pair + half;
-    if (tile >= a.tiles) return;
-    int si = 0;
-    while (si + 1 < a.nseg && tile >= (a.seg[si].n + kBN - 1) / kBN) {
-        tile -= (a.seg[si].n + kBN - 1) / kBN;
-        ++si;
-    }
-    const W8A16Seg &sg = a.seg[si];
-    const int       c0 = tile * kBN;     // first column of the workgroup in the segment
-    const int       n0 = c0 + 16 * wave; // this wave's first column
-    const bool      wave_live = n0 < sg.n;
-    const int       m0 = mt * kBM;
-    const int       kchunks = (a.K + kBK - 1) / kBK;
-    const int       c_begin = split * a.chunks_per_split; // a multiple of kRing
-    const int       c_end = min(kchunks, c_begin + a.chunks_per_split);
-    const int       ngroups = (a.K + GS - 1) / GS;
-
-    // Loads are never masked: every address is clamped into the operand, and
-    // what a clamped element feeds is either discarded (output columns >= n,
-    // rows >= M) or skipped (k steps >= K, a uniform branch), so no load
-    // ends up in a divergent branch with a wait right behind it.
-    const int     wq = 4 * (t & 15); // W column quad (within the tile)
-    const int     wr = 4 * (t >> 4); // W row quad (within the chunk)
-    const int     wcol = min(c0 + wq, sg.n - 4);
-    const int8_t *wbase = sg.w + (int64_t)wr * sg.n + wcol;
-    const int64_t wchunk = (int64_t)kBK * sg.n;
-    const int     ksteps = a.K >> 5;
-    const __half *xrow[2];
-    int           xk[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int q = t + kThreads * u;
-        const int r = q >> 3, kp = q & 7;
-        xrow[u] = a.x + (int64_t)min(m0 + r, a.M - 1) * a.ldx;
-        xk[u] = 8 * kp;
-    }
-    const int     ncol = n0 + (lane & 15); // this lane's output column (D layout)
-    const __half *sbase = sg.s + min(ncol, sg.n - 1);
-
-    f32x4 acc[4], P[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        acc[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-
-    for (int cb = c_begin; cb < c_end; cb += kRing) {
-        // Every load below is unconditional, from an address that is valid
-        // whether or not the element is (masked elements read element 0 and
-        // are zeroed afterwards), so no load sits in a divergent branch and
-        // the waits are deferred to the first use.
-        const int g0 = cb * kBK / GS; // first scale group of the batch
-        uint16_t  sraw[NG];
-#pragma unroll
-        for (int i = 0; i < NG; ++i)
-            sraw[i] = *reinterpret_cast<const uint16_t *>(sbase + (int64_t)min(g0 + i, ngroups - 1) * sg.n);
-        // W of all kRing chunks in flight at once (HBM); x (L2-resident) one
-        // chunk ahead.
-        uint32_t wbuf[kRing][4]; // reference layout: rows wr..wr+3 x columns wq..wq+3
-        uint4    xbuf[2][2];
-        auto     load_x = [&](int j, uint4(&xv)[2]) __attribute__((always_inline)) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-                xv[u] = *reinterpret_cast<const uint4 *>(xrow[u] + min((cb + j) * kBK + xk[u], a.K - 8));
-        };
-#pragma unroll
-        for (int j = 0; j < kRing; ++j) {
-            const int c = min(cb + j, kchunks - 1);
-            const int8_t *wp = wbase + (int64_t)c * wchunk;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                wbuf[j][i] = *reinterpret_cast<const uint32_t *>(
-                    wp + (int64_t)min(i, a.K - 1 - c * kBK - wr) * sg.n); // row <= K - 1
-        }
-        load_x(0, xbuf[0]);
-#pragma unroll
-        for (int j = 0; j < kRing; ++j) {
-            const int c = cb + j;
-            if (c >= c_end) break; // uniform; zero steps add nothing, groups folded below
-            if (j + 1 < kRing) load_x(j + 1, xbuf[(j + 1) & 1]);
-            _Float16 *xsb = xs[j & 1];
-            _Float16 *wtb = wt[j & 1];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int q = t + kThreads * u;
-                const int r = q >> 3, kp = q & 7;
-                *reinterpret_cast<uint4 *>(&xsb[r * kXPitch + 8 * kp]) = xbuf[j & 1][u];
-            }
-            {
-                uint32_t col[4];
-                transpose4x4(wbuf[j], col);
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-                    *reinterpret_cast<uint2 *>(&wtb[(wq + jj) * kWPitch + wr]) = i8x4_to_f16x4(col[jj]);
-            }
-            __syncthreads();
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                if (32 * (2 * c + ks) >= a.K) break; // uniform: the half chunk beyond K (K % 64 == 32)
-                const f16x8 bop = *reinterpret_cast<const f16x8 *>(
-                    &wtb[(16 * wave + (lane & 15)) * kWPitch + 32 * ks + 8 * (lane >> 4)]);
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    const f16x8 aop = *reinterpret_cast<const f16x8 *>(
-                        &xsb[(16 * rb + (lane & 15)) * kXPitch + 32 * ks + 8 * (lane >> 4)]);
-                    P[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, P[rb], 0, 0, 0);
-                }
-                const int step = 2 * j + ks; // static
-                if ((step + 1) % SPG == 0) { // end of scale group step / SPG
-                    const float s_ = h2f(__builtin_bit_cast(__half, sraw[step / SPG])) *
-                                     (g0 + step / SPG < ngroups ? 1.0f : 0.0f);
-#pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(P[rb][i], s_, acc[rb][i]);
-                        P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
-                }
-            }
-        }
-        __syncthreads(); // the next batch restages both buffers
-        // A batch cut short inside a group (K % GS != 0): fold the rest with
-        // that group's scale.  Steps executed: those of the batch's chunks
-        // that lie below K.
-        const int done_steps = min(2 * min(kRing, c_end - cb), ksteps - 2 * cb);
-        if (done_steps % SPG) {
-            float s_ = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NG; ++i)
-                s_ = (i == done_steps / SPG && g0 + i < ngroups) ? h2f(__builtin_bit_cast(__half, sraw[i])) : s_;
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[rb][i] = fmaf(P[rb][i], s_, acc[rb][i]);
-                P[rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-        }
-    }
-    if (!wave_live) return;
-
-    // D layout: lane holds rows 16*rb + 4*(lane/16) + i, column lane%16.
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + 16 * rb + 4 * (lane >> 4) + i;
-            if (m >= a.M) continue;
-            if (a.splits > 1) {
-                a.partial[((int64_t)split * a.M + m) * a.ntot + a.col0[si] + ncol] = acc[rb][i];
-            } else {
-                epilogue(a, si, m, ncol, acc[rb][i]);
-            }
-        }
-    }
-}
-
-// Packed-weight kernel, split-K inside the workgroup: one workgroup (4 waves)
-// per unit (64-row tile, 64-column tile, K split); wave w takes k steps
-// 4w..4w+3 of every 16-step (512-row) batch of the split for the whole 64x64
-// tile, W straight from global memory (8 bytes per lane per fragment,
-// packed), x through the wave's LDS stage (below), 16 MFMAs per step.  Scale groups are folded in step order.  The four
+// Split-K inside the workgroup: one workgroup (4 waves) per unit (64-row
+// tile, 64-column tile, K split); wave w takes k steps 4w..4w+3 of every
+// 16-step (512-row) batch of the split for the whole 64x64 tile, x through
+// the wave's LDS stage, W straight from global memory (PACKED: 8 bytes per
+// lane per fragment) or through a second LDS stage (reference layout), 16
+// MFMAs per step.  Scale groups are folded in step order.  The four
 // waves' tiles are summed through LDS in wave order, wave w finishing row
 // block w (each wave passes on the three row blocks it does not finish: 48
 // KB of LDS, three workgroups per CU).  ACC: a second accumulator for
 // several scale groups per wave (group size < 128, or more than one batch);
 // without it the wave's result is P * s.
-template <int GS, bool ACC>
+template <int GS, bool ACC, bool PACKED>
 __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) {
     static_assert(GS % 32 == 0 && 512 % GS == 0, "group size");
     constexpr int SPG = GS / 32;
@@ -383,7 +164,7 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
     const int       ngroups = (a.K + GS - 1) / GS;
     const int       m0 = mt * kBM;
 
-    const int8_t *wp[4]; // uniform column-block bases; lanes add 8 * lane (+ 512 per step)
+    const int8_t *wp[4]; // packed: uniform column-block bases; lanes add 8 * lane (+ 512 per step)
     const __half *sp[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
@@ -391,6 +172,37 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
         wp[cb] = sg.w + (int64_t)nb * ksteps * 512;
         sp[cb] = sg.s + 16 * nb;
     }
+    // Reference layout (W [K][N] row-major): the wave stages the 64 rows x
+    // 64 columns of two k steps (4 KB, rows of 64 bytes) with the LDS DMA
+    // load, 16-byte piece p of row r in slot p ^ ((r >> 1) & 3), and reads each
+    // B fragment with ds_read_b64_tr_b8: lane c of a 16-lane group names 8
+    // bytes of row 8q + c/2 (q the group), columns 16cb + 8(c % 2); lane i then
+    // holds column 16cb + i of rows 8q .. 8q+7 -- the packed fragment's bytes.
+    uint8_t *const ws = reinterpret_cast<uint8_t *>(red) + 32768 + wave * 4096;
+    auto issue_w = [&](int st0) __attribute__((always_inline)) { // steps st0, st0 + 1
+        if constexpr (!PACKED) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int      r = 16 * u + (lane >> 2);                 // row of the stage
+                const int      pc = (lane & 3) ^ ((r >> 1) & 3);         // piece the slot holds
+                const int      k = min(32 * st0 + r, a.K - 1);
+                const int      col = min(c0 + 16 * pc, sg.n - 16);
+                const int8_t  *src = sg.w + (int64_t)k * sg.n + col;
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                                 (__attribute__((address_space(3))) void *)(ws + u * 1024), 16, 0,
+                                                 0);
+            }
+        }
+    };
+    auto read_w = [&](int s, uint2(&dst)[4]) __attribute__((always_inline)) { // step s of the stage
+        const int i = lane & 15, r = 32 * s + 8 * (lane >> 4) + (i >> 1);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const v2i32 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (__attribute__((address_space(3))) v2i32 *)(ws + r * 64 + 16 * (cb ^ ((r >> 1) & 3)) + 8 * (i & 1)));
+            dst[cb] = make_uint2((uint32_t)t[0], (uint32_t)t[1]);
+        }
+    };
     // x reaches the MFMA through LDS: a wave stages two k steps of its 64 rows
     // (128 bytes per row, 8 KB) with the LDS DMA load, whole 128-byte row
     // pieces per 8 lanes, so that a load instruction touches 8 cache lines
@@ -437,12 +249,16 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
         if (nsteps == 0) continue;
         issue_x(first); // x first (L2 hits), then W (HBM)
         uint2 wv[4][4];
+        if constexpr (PACKED) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int st = min(first + j, ksteps - 1);
+            for (int j = 0; j < 4; ++j) {
+                const int st = min(first + j, ksteps - 1);
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-                wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + (uint32_t)(st * 512 + 8 * lane));
+                for (int cb = 0; cb < 4; ++cb)
+                    wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + (uint32_t)(st * 512 + 8 * lane));
+            }
+        } else {
+            issue_w(first);
         }
         uint16_t sraw[NS][4];
 #pragma unroll
@@ -455,9 +271,14 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         read_x(0, xv[0]);
         read_x(1, xv[1]);
-        if (nsteps > 2) { // the stage's reads complete before the DMA refills it
+        if constexpr (!PACKED) {
+            read_w(0, wv[0]);
+            read_w(1, wv[1]);
+        }
+        if (nsteps > 2) { // the stages' reads complete before the DMA refills them
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
             issue_x(first + 2);
+            issue_w(first + 2);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -466,6 +287,10 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
                 __builtin_amdgcn_s_waitcnt(kWaitVm0);
                 read_x(0, xv[0]);
                 read_x(1, xv[1]);
+                if constexpr (!PACKED) {
+                    read_w(0, wv[2]);
+                    read_w(1, wv[3]);
+                }
             }
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) {
@@ -756,43 +581,37 @@ void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A1
     a.splits = splits;
     a.tiles = tiles;
     a.mtiles = mt;
-    a.units = (tiles + 1) / 2 * splits * mt;
     a.partial = splits > 1 ? workspace : nullptr;
     if (splits > 1 && !workspace) throw std::invalid_argument("w8a16: split-K needs a workspace");
-    const unsigned blocks = (unsigned)((a.units + 7) / 8 * 16); // pairs of 8-block groups
     profile_begin(KernelId::W8A16, stream);
-    if (packed) {
+    {
         // Several scale groups per wave (gs < 128) or more than one 512-row
         // batch per split need the second accumulator.
         const bool     acc = gs < 128 || a.chunks_per_split > 8;
         const unsigned units = (unsigned)(splits * tiles * mt);
-#define TL_W8_SK_LAUNCH(G)                                                                          \
-    do {                                                                                            \
-        if (acc)                                                                                    \
-            hipLaunchKernelGGL((w8a16_sk_kernel<G, true>), dim3(units), dim3(256), 0, stream, a);   \
-        else                                                                                        \
-            hipLaunchKernelGGL((w8a16_sk_kernel<(G < 128 ? 128 : G), false>), dim3(units), dim3(256), 0, \
-                               stream, a);                                                          \
+#define TL_W8_SK_LAUNCH(G, P)                                                                          \
+    do {                                                                                               \
+        if (acc)                                                                                       \
+            hipLaunchKernelGGL((w8a16_sk_kernel<G, true, P>), dim3(units), dim3(256), 0, stream, a);   \
+        else                                                                                           \
+            hipLaunchKernelGGL((w8a16_sk_kernel<(G < 128 ? 128 : G), false, P>), dim3(units), dim3(256), 0, \
+                               stream, a);                                                             \
     } while (0)
-        switch (gs) {
-        case 32: TL_W8_SK_LAUNCH(32); break;
-        case 64: TL_W8_SK_LAUNCH(64); break;
-        case 128: TL_W8_SK_LAUNCH(128); break;
-        case 256: TL_W8_SK_LAUNCH(256); break;
-        default: TL_W8_SK_LAUNCH(512); break;
+#define TL_W8_SK_GS(P)                          \
+    switch (gs) {                               \
+    case 32: TL_W8_SK_LAUNCH(32, P); break;     \
+    case 64: TL_W8_SK_LAUNCH(64, P); break;     \
+    case 128: TL_W8_SK_LAUNCH(128, P); break;   \
+    case 256: TL_W8_SK_LAUNCH(256, P); break;   \
+    default: TL_W8_SK_LAUNCH(512, P); break;    \
+    }
+        if (packed) {
+            TL_W8_SK_GS(true)
+        } else {
+            TL_W8_SK_GS(false)
         }
+#undef TL_W8_SK_GS
 #undef TL_W8_SK_LAUNCH
-    } else {
-#define TL_W8_LAUNCH(G) \
-    hipLaunchKernelGGL((w8a16_mfma_kernel<G>), dim3(blocks), dim3(kThreads), 0, stream, a)
-        switch (gs) {
-        case 32: TL_W8_LAUNCH(32); break;
-        case 64: TL_W8_LAUNCH(64); break;
-        case 128: TL_W8_LAUNCH(128); break;
-        case 256: TL_W8_LAUNCH(256); break;
-        default: TL_W8_LAUNCH(512); break;
-        }
-#undef TL_W8_LAUNCH
     }
     HIP_CHECK(hipGetLastError());
     profile_end(KernelId::W8A16, stream);
