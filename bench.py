@@ -50,6 +50,9 @@ def parse():
                          "fused QKV W8A16 projection writing K/V into the cache; oproj: the W8A16 "
                          "o_proj + residual (Llama-3-8B layer shapes, batch 64); prefill: prompt "
                          "tokens appended and attended causally over the cache")
+    ap.add_argument("--weights", default="packed", choices=("packed", "reference"),
+                    help="project/oproj: int8 weights packed once at load (tl_w8a16_pack), or in the "
+                         "reference's row-major [K][N] layout as the drop-in entry points take them")
     ap.add_argument("--prefill-seqs", type=int, default=4, help="prefill: prompts per step")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="prefill: new tokens per prompt")
     ap.add_argument("--prefill-prefix", type=int, default=0,
@@ -501,12 +504,16 @@ def gemm_bench(args, tl, torch, np):
     gen = torch.Generator(device=dev)
     gen.manual_seed(20261201 + 7)
 
+    packed = args.weights == "packed"
+
     def weights(n):
         """int8 weights in the MFMA-fragment layout (packed once, as an engine
-        would at load time) and their fp16 group scales."""
+        would at load time) or in the reference's row-major layout, and their
+        fp16 group scales."""
         w = torch.randint(-128, 128, (hidden, n), generator=gen, device=dev, dtype=torch.int8)
-        wp = torch.empty_like(w)
-        tl.w8a16_pack(w.data_ptr(), hidden, n, wp.data_ptr(), stream)
+        wp = torch.empty_like(w) if packed else w
+        if packed:
+            tl.w8a16_pack(w.data_ptr(), hidden, n, wp.data_ptr(), stream)
         sc = (torch.rand(((hidden + gs - 1) // gs, n), generator=gen, device=dev) * 0.02 + 1e-3).half()
         return wp, sc
     x = torch.randn((B, hidden), generator=gen, device=dev, dtype=torch.float16)
@@ -524,7 +531,7 @@ def gemm_bench(args, tl, torch, np):
             batch.prepare(ids, stream)
             batch.project(0, x.data_ptr(), hidden, gs, wk.data_ptr(), sk.data_ptr(), wv.data_ptr(),
                           sv.data_ptr(), wq.data_ptr(), sq.data_ptr(), q_out.data_ptr(), stream,
-                          packed=True)
+                          packed=packed)
             batch.commit(1)
         n_out = nq + 2 * nkv
         nbytes = hidden * n_out + ((hidden + gs - 1) // gs) * n_out * 2 + B * hidden * 2 + B * n_out * 2
@@ -537,7 +544,7 @@ def gemm_bench(args, tl, torch, np):
         def call(i):
             w, sc = W[i % sets]
             tl.w8a16_matmul_residual(x.data_ptr(), w.data_ptr(), sc.data_ptr(), h.data_ptr(), B,
-                                     hidden, hidden, gs, stream, packed=True)
+                                     hidden, hidden, gs, stream, packed=packed)
         nbytes = hidden * hidden + ((hidden + gs - 1) // gs) * hidden * 2 + B * hidden * 2 + 2 * B * hidden * 2
         desc = "o_proj + residual: hidden += fp16(attn_out @ W_o)"
     for i in range(args.warmup):
@@ -571,10 +578,11 @@ def gemm_bench(args, tl, torch, np):
         "value": round(nbytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16 x int8",
-        "data": "synthetic: x ~ N(0,1), int8 weights uniform (packed layout), scales U(0.001, "
-                "0.021) (torch, seeded)",
+        "data": f"synthetic: x ~ N(0,1), int8 weights uniform ({args.weights} layout), scales "
+                "U(0.001, 0.021) (torch, seeded)",
         "config": {"workload": f"llama3_8b_{args.path}_b64", "batch": B, "hidden": hidden,
-                   "out_columns": n_out, "group_size": gs, "weight_sets": sets, "what": desc},
+                   "out_columns": n_out, "group_size": gs, "weight_sets": sets,
+                   "weights": args.weights, "what": desc},
         "kernels_us": {"w8a16": round(g_avg * 1e3, 2), "w8a16_reduce": round(r_avg * 1e3, 2)},
         "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
         "roofline": {"kernel": "w8a16_sk_kernel + w8a16_reduce_kernel", "bound": "hbm",
