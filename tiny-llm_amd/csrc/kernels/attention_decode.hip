@@ -267,34 +267,41 @@ __device__ __forceinline__ void xpose_step(float *d) {
 }
 
 // VALU: lane (r = lane / LPR, p = lane % LPR); owner of heads h % LPR == p.
-// With 16 lanes per row and G a power of two >= 2 (XP), the G head sums are
-// instead reduced transposingly: lane p's slot k holds head k ^ f(p), so that
-// adding the partner's upper half of the slots (partners p ^ 15, p ^ 7, p ^ 2,
-// p ^ 1: row_mirror, row_half_mirror, quad_perm) onto the lower half leaves
-// lane p with the row's full sum for head f(p) after G - 1 + (4 - log2 G)
-// DPP adds instead of 4 G.  f is linear in p's bits with f(15) = G/2,
-// f(7) = G/4, f(2) = G/8, f(1) = G/16 (integer division), which is what makes
-// the partner's slot k + N/2 hold the same head as slot k at every step; the
-// 16/G lanes of a head are the p that differ in the low log2(16/G) bits, and
-// the one with those bits zero owns it.
+// With 16 (or 8) lanes per row and G a power of two in [2, LPR] (XP), the G
+// head sums are instead reduced transposingly: lane p's slot k holds head
+// k ^ f(p), so that adding the partner's upper half of the slots (partners
+// p ^ 15, p ^ 7, p ^ 2, p ^ 1 -- row_mirror, row_half_mirror, quad_perm; the
+// first only with 16 lanes) onto the lower half leaves lane p with the row's
+// full sum for head f(p) after G - 1 + (log2 LPR - log2 G) DPP adds instead
+// of G log2 LPR.  f is linear in p's bits with f(15) = G/2, f(7) = G/4,
+// f(2) = G/8, f(1) = G/16 for 16 lanes (f(7) = G/2, f(2) = G/4, f(1) = G/8
+// for 8; integer division), which is what makes the partner's slot k + N/2
+// hold the same head as slot k at every step; the LPR/G lanes of a head are
+// the p that differ in the low log2(LPR/G) bits, and the one with those bits
+// zero owns it.
 template <int D, int G>
 struct ValuScorer {
     static constexpr int LPR = D / 8;
     static constexpr int TPI = 64 / LPR;
     static constexpr int NSTEP = kTile / TPI;
     static constexpr int HPL = (G + LPR - 1) / LPR;
-    static constexpr bool XP = LPR == 16 && G >= 2 && G <= 16 && (G & (G - 1)) == 0;
-    static constexpr int  F1 = G / 16, F2 = G / 8, F7 = G / 4, F15 = G / 2;
+    static constexpr bool XP = (LPR == 16 || LPR == 8) && G >= 2 && G <= LPR && (G & (G - 1)) == 0;
+    // f at the partner masks (16 lanes: 15, 7, 2, 1; 8 lanes: 7, 2, 1)
+    static constexpr int F15 = LPR == 16 ? G / 2 : 0;
+    static constexpr int F7 = LPR == 16 ? G / 4 : G / 2;
+    static constexpr int F2 = LPR == 16 ? G / 8 : G / 4;
+    static constexpr int F1 = LPR == 16 ? G / 16 : G / 8;
     static __host__ __device__ constexpr int fhead(int q) {
-        return ((q & 1) ? F1 : 0) ^ ((q & 2) ? F2 : 0) ^ ((q & 4) ? (F7 ^ F1 ^ F2) : 0) ^ ((q & 8) ? (F15 ^ F7) : 0);
+        return ((q & 1) ? F1 : 0) ^ ((q & 2) ? F2 : 0) ^ ((q & 4) ? (F7 ^ F1 ^ F2) : 0) ^
+               ((q & 8) ? (F15 ^ F7) : 0); // bit 3 only with 16 lanes
     }
     struct Owners {
         int lane[16];
     };
     static constexpr Owners owners() { // lane of head h with the low bits zero
         Owners o{};
-        for (int q = 15; q >= 0; --q)
-            if ((q & (16 / G - 1)) == 0) o.lane[fhead(q)] = q;
+        for (int q = LPR - 1; q >= 0; --q)
+            if ((q & (LPR / G - 1)) == 0) o.lane[fhead(q)] = q;
         return o;
     }
     static constexpr Owners kOwners = owners();
@@ -306,7 +313,7 @@ struct ValuScorer {
     // Head of the lane's slot hh, and whether the lane writes its results.
     __device__ __forceinline__ int lane_head(int hh) const { return XP ? fhead(p) : hh * LPR + p; }
     __device__ __forceinline__ bool lane_owns(int hh) const {
-        return XP ? (p & (16 / G - 1)) == 0 : hh * LPR + p < G;
+        return XP ? (p & (LPR / G - 1)) == 0 : hh * LPR + p < G;
     }
 
     __device__ __forceinline__ void init(const __half *qrow, int lane) {
@@ -332,10 +339,11 @@ struct ValuScorer {
                 d[h] = fdot2(qv[h].z, k.z, d[h]);
                 d[h] = fdot2(qv[h].w, k.w, d[h]);
             }
-            xpose_step<0x140, G>(d);                       // row_mirror: p ^ 15
-            xpose_step<0x141, (G / 2 > 1 ? G / 2 : 1)>(d); // row_half_mirror: p ^ 7
-            xpose_step<0x4E, (G / 4 > 1 ? G / 4 : 1)>(d);  // quad_perm [2,3,0,1]: p ^ 2
-            xpose_step<0xB1, (G / 8 > 1 ? G / 8 : 1)>(d);  // quad_perm [1,0,3,2]: p ^ 1
+            constexpr int N0 = LPR == 16 ? G : 2 * G; // slots before the p ^ 7 step
+            if constexpr (LPR == 16) xpose_step<0x140, G>(d); // row_mirror: p ^ 15
+            xpose_step<0x141, (N0 / 2 > 1 ? N0 / 2 : 1)>(d);     // row_half_mirror: p ^ 7
+            xpose_step<0x4E, (N0 / 4 > 1 ? N0 / 4 : 1)>(d);      // quad_perm [2,3,0,1]: p ^ 2
+            xpose_step<0xB1, (N0 / 8 > 1 ? N0 / 8 : 1)>(d);      // quad_perm [1,0,3,2]: p ^ 1
             sc[0][s] = valid ? d[0] * scale_log2 : -INFINITY;
             return;
         }
