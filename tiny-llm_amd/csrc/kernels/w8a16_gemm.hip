@@ -60,6 +60,7 @@ constexpr int kBM = 64;       // rows per workgroup
 constexpr int kBN = 64;       // columns per workgroup
 constexpr int kBK = 64;       // k rows per chunk (split sizes count chunks)
 constexpr int kRing = 8;      // chunks per 512-row batch
+constexpr int kMaxSplits = 8; // K splits of the split-K plan, at most
 constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0)
 constexpr int kWaitLgkm0 = 0xC07F; // s_waitcnt lgkmcnt(0)
 
@@ -469,13 +470,20 @@ __global__ __launch_bounds__(256) void w8a16_reduce_kernel(GemmArgs a) {
     const int c = 4 * (int)(idx - (int64_t)m * q);
     int       si = 0;
     while (si + 1 < a.nseg && c >= a.col0[si + 1]) ++si;
+    // Every split's load in flight at once (at most kMaxSplits; an index past
+    // the last split re-reads it), then the sum in split order.
+    float4 p[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s)
+        p[s] = *reinterpret_cast<const float4 *>(a.partial + ((int64_t)min(s, a.splits - 1) * a.M + m) * a.ntot + c);
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s = 0; s < a.splits; ++s) {
-        const float4 p = *reinterpret_cast<const float4 *>(a.partial + ((int64_t)s * a.M + m) * a.ntot + c);
-        v.x += p.x;
-        v.y += p.y;
-        v.z += p.z;
-        v.w += p.w;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) { // a select, not a branch: the loads stay up front
+        const bool live = s < a.splits;
+        v.x = live ? v.x + p[s].x : v.x;
+        v.y = live ? v.y + p[s].y : v.y;
+        v.z = live ? v.z + p[s].z : v.z;
+        v.w = live ? v.w + p[s].w : v.w;
     }
     epilogue4(a, si, m, c - a.col0[si], v);
 }
@@ -520,7 +528,7 @@ namespace {
 // tiles.  Sets the 64-row chunks per split.
 int split_plan(int M, int K, int *chunks_per_split) {
     const int kchunks = (K + kBK - 1) / kBK;
-    int       splits = M <= 256 ? std::min(8, std::max(1, K / 512)) : 1;
+    int       splits = M <= 256 ? std::min(kMaxSplits, std::max(1, K / 512)) : 1;
     // chunks per split: a multiple of kRing, so that every batch starts on a
     // 512-row (scale-group) boundary
     const int cps = ((kchunks + splits - 1) / splits + kRing - 1) / kRing * kRing;
