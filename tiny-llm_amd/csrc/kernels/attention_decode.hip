@@ -1045,6 +1045,7 @@ constexpr int kMergeMaxChunks = 64;
 template <int D, int G>
 __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     __shared__ float s_w[kMergeMaxChunks][G];
+    __shared__ float s_lc[kMergeMaxChunks][G]; // the chunks' l, loaded with their m
     __shared__ float s_m[G], s_l[G];
     const int        b = blockIdx.x / a.Hkv;
     const int        g = blockIdx.x - b * a.Hkv;
@@ -1069,8 +1070,11 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     for (int c0 = 0; c0 < nch; c0 += kMergeMaxChunks) {
         const int cn = min(kMergeMaxChunks, nch - c0);
         for (int i = threadIdx.x; i < cn * G; i += 256) {
-            const int c = i / G, h = i - c * G;
-            s_w[c][h] = a.part_ml[((int64_t)(w0 + c0 + c) * a.Hq + (int64_t)g * G + h) * 2];
+            const int    c = i / G, h = i - c * G;
+            const float2 ml = *reinterpret_cast<const float2 *>(
+                &a.part_ml[((int64_t)(w0 + c0 + c) * a.Hq + (int64_t)g * G + h) * 2]);
+            s_w[c][h] = ml.x;
+            s_lc[c][h] = ml.y;
         }
         __syncthreads();
         if (threadIdx.x < G) { // running max and sum of head threadIdx.x
@@ -1080,7 +1084,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
             float l = c0 ? s_l[h] * __builtin_amdgcn_exp2f(mx - mnew) : 0.0f;
             for (int c = 0; c < cn; ++c) {
                 const float wgt = __builtin_amdgcn_exp2f(s_w[c][h] - mnew);
-                l = fmaf(wgt, a.part_ml[((int64_t)(w0 + c0 + c) * a.Hq + (int64_t)g * G + h) * 2 + 1], l);
+                l = fmaf(wgt, s_lc[c][h], l);
                 s_w[c][h] = wgt;
             }
             s_l[h] = l;
@@ -1093,8 +1097,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
                 const float  *po = a.part_o + ((int64_t)w0 * a.Hq + (int64_t)g * G) * D + idx;
                 const int64_t rs = (int64_t)a.Hq * D;
                 float         o = 0.0f;
+                if (cn <= 8) { // every chunk's load in flight at once; a select keeps them up front
+                    float pv[8];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) pv[c] = po[min(c, cn - 1) * rs];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) o = c < cn ? fmaf(s_w[c][h], pv[c], o) : o;
+                } else {
 #pragma unroll 16
-                for (int c = 0; c < cn; ++c) o = fmaf(s_w[c][h], po[c * rs], o);
+                    for (int c = 0; c < cn; ++c) o = fmaf(s_w[c][h], po[c * rs], o);
+                }
                 dst[idx] = __float2half(o * (1.0f / (s_l[h] + 1e-6f)));
             }
             return;
