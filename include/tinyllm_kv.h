@@ -327,6 +327,30 @@ int tl_attn_get_score_path(void);
 int tl_attn_set_waves(int waves);
 int tl_attn_get_waves(void);
 
+/* The launch plan the decode attention entry points (tl_kv_batch_attention,
+ * tl_kv_batch_decode, tl_attn_decode_gqa) make for attended lengths
+ * seq_lens[0..n) on a device of num_cus compute units -- host only, no GPU
+ * needed.  forced_chunk: 0, or a multiple of 256 tokens as TL_ATTN_CHUNK
+ * would force; waves_setting: 0 (auto), 4 or 8 as tl_attn_set_waves.
+ * with_rows != 0 counts the slot row per entry that DecodeBatch passes.
+ * Optional outputs: part_base[n + 1] (first partial row of each entry) and
+ * work[2 * work_items] ((entry, chunk) pairs in launch order, longest
+ * first).  No reference counterpart (planner introspection for tests and
+ * tuning; the reference launches one workgroup per (sequence, head),
+ * kernels/attention.cu:121-125). */
+typedef struct tl_attn_plan_info {
+    int chunk_tokens;  /* tokens per work item, a multiple of 256 */
+    int work_items;    /* workgroups of the attention launch / Hkv */
+    int waves;         /* waves per workgroup (4 or 8; 0 when no work) */
+    int any_multi;     /* some sequence spans several chunks: merge launch */
+    int any_empty;     /* some sequence attends to zero tokens */
+    int max_len;       /* longest attended length */
+    int inline_words;  /* metadata words in the kernel arguments, -1: device copy */
+} tl_attn_plan_info;
+int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
+                 int waves_setting, int with_rows, tl_attn_plan_info *info, int32_t *part_base,
+                 int32_t *work);
+
 /* ------------------------------------------------------------------------
  * Kernel timing (the reference has only an unused CudaEvent wrapper,
  * include/tiny_llm/cuda_streams.h:67-99).  When enabled, every launch of the

@@ -263,3 +263,32 @@ def test_softmax_matches_oracle(tl, orc, rows, S):
     assert np.all(np.abs(got - ref32) <= np.abs(ref32) * 2.0 ** -10 + 2.0 ** -24)
     sums = got.sum(axis=1)
     assert np.all((sums > 0.98) & (sums < 1.02)) and np.all(got >= 0)
+
+
+def test_failed_prepare_leaves_an_empty_batch(tl):
+    """A prepare that fails (here: cache overflow) must not leave the
+    previous step's plan armed: prefill/attention/append after it are
+    no-ops, and the pool keeps the committed bytes."""
+    from devutil import read_dev
+    rng = np.random.default_rng(4242)
+    H, D, M, Hq = 2, 64, 128, 4
+    g = tl.KVCacheManager(1, H, D, M, 2)
+    sid, _ = g.allocateSequence(M)
+    k, v = f16bits(rng, (100, H * D)), f16bits(rng, (100, H * D))
+    dk, dv = to_dev(k), to_dev(v)
+    pb = tl.PrefillBatch(g, 2, Hq)
+    pb.prepare([sid], [100], stream())
+    q = to_dev(f16bits(rng, (100, Hq, D)))
+    out = empty_dev((100, Hq, D))
+    pb.run(0, q.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), D ** -0.5, stream())
+    pb.commit()
+    before = read_dev(g.pool(), g.slot_bytes() // 2)
+    with pytest.raises(tl.TinyLLMError, match="cache overflow"):
+        pb.prepare([sid], [100], stream())          # 100 + 100 > 128
+    assert pb.info() == {"n": 0, "tokens": 0}
+    other = to_dev(f16bits(rng, (100, H * D)))
+    pb.run(0, q.data_ptr(), other.data_ptr(), other.data_ptr(), out.data_ptr(), D ** -0.5, stream())
+    pb.append(0, other.data_ptr(), other.data_ptr(), stream())
+    pb.commit()
+    assert np.array_equal(read_dev(g.pool(), g.slot_bytes() // 2), before)
+    assert g.getSeqLen(sid) == 100

@@ -1,0 +1,118 @@
+// Host-side planner of the split-K decode attention launch (see attn_plan.h).
+#include "attn_plan.h"
+
+#include <algorithm>
+#include <climits>
+#include <cstdlib>
+#include <cstring>
+
+namespace tiny_llm {
+namespace detail {
+
+// With W = sum(lens) * Hkv token-heads of work, C CUs and P = C *
+// kPlanSlotsPerCU resident workgroup slots:
+//  - uniform lengths: chunks of W / P (rounded up), so the items fill the
+//    slots in whole rounds -- usually the whole sequence, hence no partials;
+//  - ragged lengths no longer than the per-CU share W / C: no split (the
+//    workgroups sharing a CU share its bandwidth, and longest-first ordering
+//    balances the CUs without partials or a merge launch);
+//  - longer ragged lengths: chunks of W / (2P), so that longest-first list
+//    scheduling ends within about one small item of the ideal.
+int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int cus,
+               int forced_chunk) {
+    int64_t total = 0;
+    int     mx = 0, mn = INT_MAX;
+    for (int i = 0; i < (lens ? n : 0); ++i) {
+        total += lens[i];
+        mx = std::max(mx, (int)lens[i]);
+        mn = std::min(mn, (int)lens[i]);
+    }
+    if (!lens) {
+        total = (int64_t)n * uniform_len;
+        mx = mn = uniform_len;
+    }
+    const int cap = std::max(kPlanQuantum, (mx + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum);
+    if (forced_chunk >= kPlanQuantum && forced_chunk % kPlanQuantum == 0)
+        return std::min(forced_chunk, cap);
+    const int64_t c = std::max(1, cus);
+    const int64_t slots = c * kPlanSlotsPerCU;
+    const int64_t work = total * num_kv_heads;
+    const bool    uniform = mn >= mx - mx / 10;
+    int64_t       per;
+    if (uniform) per = (work + slots - 1) / slots;
+    else if (mx <= (work + c - 1) / c) per = mx;
+    else per = (work + slots - 1) / slots / 2;
+    const int64_t chunk = (per + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum;
+    return (int)std::min<int64_t>(std::max<int64_t>(chunk, kPlanQuantum), cap);
+}
+
+void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
+                    WorkList &out) {
+    out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
+    out.part_base.assign((size_t)std::max(n, 0) + 1, 0);
+    out.any_multi = false;
+    out.any_empty = false;
+    out.max_len = 0;
+    for (int i = 0; i < n; ++i) {
+        const int c = (lens[i] + out.chunk - 1) / out.chunk;
+        out.any_multi |= c > 1;
+        out.any_empty |= c == 0;
+        out.max_len = std::max(out.max_len, (int)lens[i]);
+        out.part_base[(size_t)i + 1] = out.part_base[(size_t)i] + c;
+    }
+    out.n_work = out.part_base[(size_t)std::max(n, 0)];
+    // (length, entry, chunk) sorted by length descending, then entry, chunk.
+    std::vector<int64_t> key((size_t)out.n_work);
+    size_t               k = 0;
+    for (int i = 0; i < n; ++i)
+        for (int c = 0; c < out.part_base[(size_t)i + 1] - out.part_base[(size_t)i]; ++c) {
+            const int len = std::min(out.chunk, lens[i] - c * out.chunk);
+            // larger length first; ties keep (entry, chunk) order
+            key[k++] = ((int64_t)(INT32_MAX - len) << 32) | (int64_t)(out.part_base[(size_t)i] + c);
+        }
+    std::sort(key.begin(), key.end());
+    out.work.resize(2 * (size_t)out.n_work);
+    // part_base is non-decreasing: entry of partial row r = last i with part_base[i] <= r
+    for (size_t w = 0; w < key.size(); ++w) {
+        const int32_t row = (int32_t)(key[w] & 0xffffffff);
+        const int     i = (int)(std::upper_bound(out.part_base.begin(), out.part_base.end(), row) -
+                            out.part_base.begin()) - 1;
+        out.work[2 * w] = i;
+        out.work[2 * w + 1] = row - out.part_base[(size_t)i];
+    }
+}
+
+int plan_waves(int64_t workgroups, int cus, int setting) {
+    if (setting == 4 || setting == 8) return setting;
+    return workgroups <= 2 * (int64_t)std::max(1, cus) ? 8 : 4;
+}
+
+int chunk_override_from_env() {
+    const char *env = std::getenv("TL_ATTN_CHUNK");
+    if (!env) return 0;
+    const int c = std::atoi(env);
+    return c >= kPlanQuantum && c % kPlanQuantum == 0 ? c : 0;
+}
+
+int inline_words(const WorkList &plan, int n, bool with_rows) {
+    return n + (n + 1) + 2 * plan.n_work + (with_rows ? n : 0);
+}
+
+bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
+                 InlineMeta &out) {
+    const int words = inline_words(plan, n, rows != nullptr);
+    if (n <= 0 || words > kInlineWords) return false;
+    out.n = n;
+    out.has_rows = rows ? 1 : 0;
+    out.off_part = n;
+    out.off_work = 2 * n + 1;
+    out.off_rows = out.off_work + 2 * plan.n_work;
+    std::memcpy(out.w, lens, (size_t)n * 4);
+    std::memcpy(out.w + out.off_part, plan.part_base.data(), (size_t)(n + 1) * 4);
+    if (plan.n_work) std::memcpy(out.w + out.off_work, plan.work.data(), (size_t)plan.n_work * 8);
+    if (rows) std::memcpy(out.w + out.off_rows, rows, (size_t)n * 4);
+    return true;
+}
+
+} // namespace detail
+} // namespace tiny_llm

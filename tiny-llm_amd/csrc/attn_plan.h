@@ -1,0 +1,73 @@
+// Host-side planner of the split-K decode attention launch: chunk length,
+// work list, waves per workgroup and the kernel-argument packing of the
+// per-step metadata.  Plain C++ (no HIP types), so the same code is built
+// into the library and, under the address and undefined-behaviour
+// sanitizers, into a host test.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+namespace tiny_llm {
+namespace detail {
+
+constexpr int kPlanTile = 64;                  // tokens per wave tile
+constexpr int kPlanQuantum = 4 * kPlanTile;    // chunk lengths are multiples of this
+constexpr int kPlanSlotsPerCU = 2;             // resident 4-wave workgroups per CU
+
+// Host side of a ragged plan: chunk length, per-entry partial-row bases and
+// the (entry, chunk) work list in longest-first order, so the hardware
+// dispatcher, which hands workgroups to CUs as they free up, schedules the
+// longest items first (LPT list scheduling).
+struct WorkList {
+    int                  chunk = 256;
+    int                  n_work = 0;
+    int                  max_len = 0;
+    bool                 any_multi = false;
+    bool                 any_empty = false;
+    std::vector<int32_t> part_base; // n + 1
+    std::vector<int32_t> work;      // 2 * n_work
+};
+
+// Chunk length (tokens per work item, a multiple of kPlanQuantum) for the
+// attended lengths lens[0..n) (or n entries of uniform_len when lens is
+// NULL) on a device of `cus` compute units.  forced_chunk > 0 (a multiple
+// of kPlanQuantum) overrides the choice, capped at the longest length
+// rounded up to the quantum.
+int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int cus,
+               int forced_chunk);
+
+// The whole ragged plan (chunk, part_base, work list) for lens[0..n).
+void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
+                    WorkList &out);
+
+// Waves per workgroup for a launch of `workgroups` workgroups: setting 4 or 8
+// forces it; 0 (auto) gives 8 when every CU gets at most two workgroups in
+// turn, else 4 (two 4-wave workgroups per CU).
+int plan_waves(int64_t workgroups, int cus, int setting);
+
+// TL_ATTN_CHUNK from the environment when it is a positive multiple of
+// kPlanQuantum, else 0.
+int chunk_override_from_env();
+
+// Plan metadata small enough to travel in the kernel arguments, so that a
+// launch needs no separate host-to-device copy.  Words:
+//   [lens n | part_base n+1 | work 2*n_work | rows n (if has_rows)]
+// rows[b] is the cache row (slot) of entry b, replacing KvView::seq_row.
+constexpr int kInlineWords = 896;
+struct InlineMeta {
+    int32_t n = 0; // entries; 0 = metadata comes through the AttnPlan pointers
+    int32_t has_rows = 0;
+    int32_t off_part = 0;
+    int32_t off_work = 0;
+    int32_t off_rows = 0;
+    int32_t w[kInlineWords];
+};
+// Words the inline metadata of this plan needs.
+int inline_words(const WorkList &plan, int n, bool with_rows);
+// Packs lens / plan / rows (rows may be NULL) into out; false if they do not fit.
+bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
+                 InlineMeta &out);
+
+} // namespace detail
+} // namespace tiny_llm

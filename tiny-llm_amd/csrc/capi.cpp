@@ -478,6 +478,38 @@ int tl_attn_set_waves(int waves) {
 
 int tl_attn_get_waves(void) { return tiny_llm::detail::waves(); }
 
+int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
+                 int waves_setting, int with_rows, tl_attn_plan_info *info, int32_t *part_base,
+                 int32_t *work) {
+    if (!info) return fail(TL_ERR_INVALID, "tl_attn_plan: info is null");
+    if (n < 0 || (n > 0 && !seq_lens)) return fail(TL_ERR_INVALID, "tl_attn_plan: invalid lengths");
+    if (num_kv_heads <= 0 || num_cus <= 0)
+        return fail(TL_ERR_INVALID, "tl_attn_plan: num_kv_heads and num_cus must be positive");
+    if (waves_setting != 0 && waves_setting != 4 && waves_setting != 8)
+        return fail(TL_ERR_INVALID, "tl_attn_plan: waves_setting must be 0 (auto), 4 or 8");
+    for (int i = 0; i < n; ++i)
+        if (seq_lens[i] < 0) return fail(TL_ERR_INVALID, "tl_attn_plan: negative sequence length");
+    return guarded([&] {
+        namespace d = tiny_llm::detail;
+        d::WorkList wl;
+        d::plan_work_list(seq_lens, n, num_kv_heads, num_cus, forced_chunk, wl);
+        info->chunk_tokens = wl.chunk;
+        info->work_items = wl.n_work;
+        info->waves = wl.n_work ? d::plan_waves((int64_t)wl.n_work * num_kv_heads, num_cus,
+                                                waves_setting)
+                                : 0;
+        info->any_multi = wl.any_multi ? 1 : 0;
+        info->any_empty = wl.any_empty ? 1 : 0;
+        info->max_len = wl.max_len;
+        const int words = d::inline_words(wl, n, with_rows != 0);
+        info->inline_words = (n > 0 && words <= d::kInlineWords) ? words : -1;
+        if (part_base) std::memcpy(part_base, wl.part_base.data(), wl.part_base.size() * 4);
+        if (work && wl.n_work) std::memcpy(work, wl.work.data(), wl.work.size() * 4);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
 void tl_profile_enable(int on) { tiny_llm::detail::profile_set(on != 0); }
 void tl_profile_reset(void) { tiny_llm::detail::profile_reset(); }
 

@@ -81,8 +81,8 @@ namespace {
 // expressed in 4-wave workgroups.
 constexpr int kWavesPerEU = 2;
 constexpr int kTile = 64;             // tokens per wave tile
-constexpr int kQuantum = 4 * kTile;   // chunk lengths are multiples of this
-constexpr int kSlotsPerCU = kWavesPerEU;
+constexpr int kQuantum = kPlanQuantum; // chunk lengths are multiples of this
+static_assert(kTile == kPlanTile && kPlanSlotsPerCU == kWavesPerEU, "planner geometry");
 
 // Tuning (compile-time): K load steps per batch, V pair blocks per batch.
 #ifndef TL_ATTN_KB
@@ -1267,11 +1267,7 @@ int waves_setting() {
     return v;
 }
 
-int waves_for(int64_t workgroups) {
-    const int v = waves_setting();
-    if (v) return v;
-    return workgroups <= 2 * (int64_t)device_cus() ? 8 : 4;
-}
+int waves_for(int64_t workgroups) { return plan_waves(workgroups, device_cus(), waves_setting()); }
 
 } // namespace
 
@@ -1288,96 +1284,14 @@ size_t attn_workspace_floats(int n_work, int Hq, int D) {
     return (size_t)n_work * (size_t)Hq * (size_t)(D + 2);
 }
 
-// Chunk length (tokens per work item), a multiple of kQuantum.  With
-// W = sum(lens) * Hkv token-heads of work, C CUs and P = C * kSlotsPerCU
-// resident workgroup slots:
-//  - uniform lengths: chunks of W / P (rounded up), so the items fill the
-//    slots in whole rounds -- usually the whole sequence, hence no partials;
-//  - ragged lengths no longer than the per-CU share W / C: no split (the
-//    workgroups sharing a CU share its bandwidth, and longest-first ordering
-//    balances the CUs without partials or a merge launch);
-//  - longer ragged lengths: chunks of W / (2P), so that longest-first list
-//    scheduling ends within about one small item of the ideal.
-// TL_ATTN_CHUNK (a multiple of kQuantum) overrides.
 int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim) {
     (void)head_dim;
-    int64_t total = 0;
-    int     mx = 0, mn = INT_MAX;
-    for (int i = 0; i < (lens ? n : 0); ++i) {
-        total += lens[i];
-        mx = std::max(mx, (int)lens[i]);
-        mn = std::min(mn, (int)lens[i]);
-    }
-    if (!lens) {
-        total = (int64_t)n * uniform_len;
-        mx = mn = uniform_len;
-    }
-    const int cap = std::max(kQuantum, (mx + kQuantum - 1) / kQuantum * kQuantum);
-    if (const char *env = std::getenv("TL_ATTN_CHUNK")) {
-        const int c = std::atoi(env);
-        if (c >= kQuantum && c % kQuantum == 0) return std::min(c, cap);
-    }
-    const int64_t cus = device_cus();
-    const int64_t slots = cus * kSlotsPerCU;
-    const int64_t work = total * num_kv_heads;
-    const bool    uniform = mn >= mx - mx / 10;
-    int64_t       per;
-    if (uniform) per = (work + slots - 1) / slots;
-    else if (mx <= (work + cus - 1) / cus) per = mx;
-    else per = (work + slots - 1) / slots / 2;
-    const int64_t chunk = (per + kQuantum - 1) / kQuantum * kQuantum;
-    return (int)std::min<int64_t>(std::max<int64_t>(chunk, kQuantum), cap);
+    return plan_chunk(lens, n, num_kv_heads, uniform_len, device_cus(), chunk_override_from_env());
 }
 
 void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out) {
-    out.chunk = choose_chunk(lens, n, num_kv_heads, 0, head_dim);
-    out.part_base.assign((size_t)n + 1, 0);
-    out.any_multi = false;
-    out.any_empty = false;
-    out.max_len = 0;
-    for (int i = 0; i < n; ++i) {
-        const int c = (lens[i] + out.chunk - 1) / out.chunk;
-        out.any_multi |= c > 1;
-        out.any_empty |= c == 0;
-        out.max_len = std::max(out.max_len, (int)lens[i]);
-        out.part_base[(size_t)i + 1] = out.part_base[(size_t)i] + c;
-    }
-    out.n_work = out.part_base[(size_t)n];
-    // (length, entry, chunk) sorted by length descending, then entry, chunk.
-    std::vector<int64_t> key((size_t)out.n_work);
-    size_t               k = 0;
-    for (int i = 0; i < n; ++i)
-        for (int c = 0; c < out.part_base[(size_t)i + 1] - out.part_base[(size_t)i]; ++c) {
-            const int len = std::min(out.chunk, lens[i] - c * out.chunk);
-            // larger length first; ties keep (entry, chunk) order
-            key[k++] = ((int64_t)(INT32_MAX - len) << 32) | (int64_t)(out.part_base[(size_t)i] + c);
-        }
-    std::sort(key.begin(), key.end());
-    out.work.resize(2 * (size_t)out.n_work);
-    // part_base is non-decreasing: entry of partial row r = last i with part_base[i] <= r
-    for (size_t w = 0; w < key.size(); ++w) {
-        const int32_t row = (int32_t)(key[w] & 0xffffffff);
-        const int     i = (int)(std::upper_bound(out.part_base.begin(), out.part_base.end(), row) -
-                            out.part_base.begin()) - 1;
-        out.work[2 * w] = i;
-        out.work[2 * w + 1] = row - out.part_base[(size_t)i];
-    }
-}
-
-bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
-                 InlineMeta &out) {
-    const int words = n + (n + 1) + 2 * plan.n_work + (rows ? n : 0);
-    if (n <= 0 || words > kInlineWords) return false;
-    out.n = n;
-    out.has_rows = rows ? 1 : 0;
-    out.off_part = n;
-    out.off_work = 2 * n + 1;
-    out.off_rows = out.off_work + 2 * plan.n_work;
-    std::memcpy(out.w, lens, (size_t)n * 4);
-    std::memcpy(out.w + out.off_part, plan.part_base.data(), (size_t)(n + 1) * 4);
-    if (plan.n_work) std::memcpy(out.w + out.off_work, plan.work.data(), (size_t)plan.n_work * 8);
-    if (rows) std::memcpy(out.w + out.off_rows, rows, (size_t)n * 4);
-    return true;
+    (void)head_dim;
+    plan_work_list(lens, n, num_kv_heads, device_cus(), chunk_override_from_env(), out);
 }
 
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
@@ -1390,8 +1304,15 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     if (plan.chunk % kQuantum != 0 || plan.chunk <= 0)
         throw std::invalid_argument("attention: chunk length must be a positive multiple of " +
                                     std::to_string(kQuantum));
-    if (!paged && (int64_t)plan.max_len * kv.tok_stride * 2 > (int64_t)UINT32_MAX)
-        throw std::invalid_argument("attention: token offsets exceed 32 bits (max_len * row bytes)");
+    // Token offsets inside a slot (contiguous) or a block (paged) are 32-bit
+    // byte offsets (RowAddr::in_block).
+    const int64_t span_tokens =
+        paged ? std::min<int64_t>((int64_t)1 << std::min(kv.log2_blk, 62), plan.max_len) : plan.max_len;
+    if (kv.log2_blk < 0 || kv.log2_blk > 30)
+        throw std::invalid_argument("attention: log2_blk must be in [0, 30]");
+    if (span_tokens * kv.tok_stride * 2 > (int64_t)UINT32_MAX)
+        throw std::invalid_argument("attention: token offsets exceed 32 bits (tokens per " +
+                                    std::string(paged ? "block" : "slot") + " * row bytes)");
     if (plan.any_multi && !part)
         throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
     AttnArgs args;

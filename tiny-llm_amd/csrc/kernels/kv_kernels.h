@@ -5,6 +5,8 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime_api.h>
 
+#include "attn_plan.h"
+
 #include <cstdint>
 #include <utility>
 #include <vector>
@@ -51,42 +53,12 @@ struct AttnPlan {
     int            max_len = 0;        // longest attended length (offset-width check)
 };
 
-// Work-list chunk length (tokens per work item, a multiple of the kernel's
-// quantum of waves-per-workgroup x 64 tokens) for a set
-// of attended lengths (lens, or n entries of uniform_len when lens is NULL).
+// Chunk length for the current device (TL_ATTN_CHUNK overrides), see
+// plan_chunk.
 int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int head_dim);
-
-// Host side of a ragged plan: chunk length, per-entry partial-row bases and
-// the (entry, chunk) work list in longest-first order, so the hardware
-// dispatcher, which hands workgroups to CUs as they free up, schedules the
-// longest items first (LPT list scheduling).
-struct WorkList {
-    int                  chunk = 256;
-    int                  n_work = 0;
-    int                  max_len = 0;
-    bool                 any_multi = false;
-    bool                 any_empty = false;
-    std::vector<int32_t> part_base; // n + 1
-    std::vector<int32_t> work;      // 2 * n_work
-};
+// The ragged plan for the current device (TL_ATTN_CHUNK overrides), see
+// plan_work_list.
 void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out);
-
-// Plan metadata small enough to travel in the kernel arguments, so that a
-// launch needs no separate host-to-device copy.  Words:
-//   [lens n | part_base n+1 | work 2*n_work | rows n (if has_rows)]
-// rows[b] is the cache row (slot) of entry b, replacing KvView::seq_row.
-constexpr int kInlineWords = 896;
-struct InlineMeta {
-    int32_t n = 0; // entries; 0 = metadata comes through the AttnPlan pointers
-    int32_t has_rows = 0;
-    int32_t off_part = 0;
-    int32_t off_work = 0;
-    int32_t off_rows = 0;
-    int32_t w[kInlineWords];
-};
-// Packs lens / plan / rows (rows may be NULL) into out; false if they do not fit.
-bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
-                 InlineMeta &out);
 
 // Partials workspace (floats) needed by launch_attn_decode for n_work items.
 size_t attn_workspace_floats(int n_work, int Hq, int D);

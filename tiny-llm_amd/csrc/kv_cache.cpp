@@ -43,6 +43,12 @@ Result<std::unique_ptr<KVCacheManager>> KVCacheManager::createPaged(const KVCach
     if (num_blocks <= 0 || num_blocks == INT32_MAX)
         return R::err("KVCacheManager: num_blocks must be in [1, 2^31 - 2] (got " +
                       std::to_string(num_blocks) + ")");
+    // The kernels address a token inside its block with a 32-bit byte offset.
+    if (config.num_heads > 0 && config.head_dim > 0 &&
+        static_cast<int64_t>(block_tokens) * config.num_heads * config.head_dim * 2 >
+            static_cast<int64_t>(UINT32_MAX))
+        return R::err("KVCacheManager: a block of " + std::to_string(block_tokens) +
+                      " tokens exceeds 4 GiB per layer and K/V region");
     return build(config, block_tokens, num_blocks);
 }
 
@@ -746,8 +752,15 @@ Result<std::unique_ptr<PrefillBatch>> PrefillBatch::create(KVCacheManager &mgr, 
 
 Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, int n,
                                    hipStream_t stream) {
+    // A failing prepare leaves an empty batch: append/attention/prefill and
+    // commit are then no-ops, never a replay of the previous step's plan.
     n_ = 0;
     tokens_ = 0;
+    n_items_ = 0;
+    max_keys_ = 0;
+    d_work_ = nullptr;
+    d_tok_row_ = nullptr;
+    d_tok_pos_ = nullptr;
     ids_.clear();
     counts_.clear();
     if (n < 0 || n > max_seqs_)

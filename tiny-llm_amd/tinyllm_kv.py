@@ -18,9 +18,9 @@ import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _REPO = os.path.dirname(_HERE)
-# TINYLLM_KV_LIB points at an alternative build of the same library (tuning
-# experiments); by default the in-tree build is loaded.
-LIB_PATH = os.environ.get("TINYLLM_KV_LIB") or os.path.join(_HERE, "_build", "libtinyllm_kv.so")
+# Always the in-tree build: no environment override, so a test, the smoke
+# check or the bench can never pick up some other copy of the library.
+LIB_PATH = os.path.join(_HERE, "_build", "libtinyllm_kv.so")
 HEADER_PATH = os.path.join(_REPO, "include", "tinyllm_kv.h")
 
 TL_OK = 0
@@ -47,12 +47,31 @@ def build(jobs: int = 8) -> str:
 def load() -> C.CDLL:
     global _lib
     if _lib is None:
+        if os.environ.get("TINYLLM_KV_LIB"):
+            raise RuntimeError("TINYLLM_KV_LIB is set; this binding loads only the in-tree "
+                               f"library {LIB_PATH}")
         if not os.path.exists(LIB_PATH):
             raise FileNotFoundError(
                 f"{LIB_PATH} is not built; run __graft_entry__.build() (or make -C tiny-llm_amd)")
         _lib = C.CDLL(LIB_PATH)
         _declare(_lib)
+        mapped = loaded_path()
+        if mapped is None or os.path.realpath(mapped) != os.path.realpath(LIB_PATH):
+            raise RuntimeError(f"libtinyllm_kv.so mapped from {mapped}, expected {LIB_PATH}")
     return _lib
+
+
+def loaded_path() -> str | None:
+    """Path of the libtinyllm_kv.so this process has mapped (from
+    /proc/self/maps), or None when none is mapped."""
+    try:
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if line.rstrip().endswith("libtinyllm_kv.so"):
+                    return line.split(None, 5)[5].strip()
+    except OSError:
+        pass
+    return None
 
 
 class KVConfig(C.Structure):
@@ -64,6 +83,11 @@ class KVView(C.Structure):
     _fields_ = [("k_base", C.c_void_p), ("v_base", C.c_void_p), ("block_table", C.c_void_p),
                 ("bt_stride", C.c_int), ("log2_blk", C.c_int), ("blk_stride", C.c_int64),
                 ("tok_stride", C.c_int64), ("head_stride", C.c_int64)]
+
+
+class AttnPlanInfo(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("chunk_tokens", "work_items", "waves", "any_multi",
+                                       "any_empty", "max_len", "inline_words")]
 
 
 def _declare(L: C.CDLL) -> None:
@@ -127,6 +151,7 @@ def _declare(L: C.CDLL) -> None:
         "tl_attn_get_score_path": (i, []),
         "tl_attn_set_waves": (i, [i]),
         "tl_attn_get_waves": (i, []),
+        "tl_attn_plan": (i, [vp, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
         "tl_profile_enable": (None, [i]),
         "tl_profile_reset": (None, []),
         "tl_profile_query": (i, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
@@ -427,6 +452,27 @@ def set_waves(waves: int):
 
 def get_waves() -> int:
     return load().tl_attn_get_waves()
+
+
+def attn_plan(seq_lens, num_kv_heads, num_cus=256, forced_chunk=0, waves=0, with_rows=True):
+    """The decode attention launch plan for these attended lengths (host
+    only): a dict of tl_attn_plan_info plus part_base and the work list as
+    (entry, chunk) pairs in launch order."""
+    import numpy as np
+    lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    n = lens.size
+    info = AttnPlanInfo()
+    _check(load().tl_attn_plan(lens.ctypes.data if n else None, n, num_kv_heads, num_cus,
+                               forced_chunk, waves, int(with_rows), C.byref(info), None, None))
+    part = np.zeros(n + 1, dtype=np.int32)
+    work = np.zeros(max(1, 2 * info.work_items), dtype=np.int32)
+    _check(load().tl_attn_plan(lens.ctypes.data if n else None, n, num_kv_heads, num_cus,
+                               forced_chunk, waves, int(with_rows), C.byref(info),
+                               part.ctypes.data, work.ctypes.data))
+    out = {name: getattr(info, name) for name, _ in AttnPlanInfo._fields_}
+    out["part_base"] = part
+    out["work"] = work[:2 * info.work_items].reshape(-1, 2)
+    return out
 
 
 def profile_enable(on: bool = True):
