@@ -110,7 +110,7 @@ def test_cfg3_full_size(tl, orc):
     scale = cfg.scale
     slot_elems = g.slot_bytes() // 2
     for step in range(2):
-        S = ctx + step + 1
+        S = ctx + 1  # attended: the context plus the token this step appends
         batch.prepare(ids, stream())
         info = batch.info()
         assert info["chunk_tokens"] == 8448 and info["work_items"] == 64
