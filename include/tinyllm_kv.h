@@ -224,6 +224,23 @@ typedef struct tl_kv_view {
 int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_lens_host, int B,
                        int Hq, int Hkv, int D, float scale, void *out, void *stream);
 
+/* tl_attn_decode_gqa without any allocation: no hipMalloc, hipFree, pinned
+ * host memory or host-to-device copy, so it can run under HIP graph capture
+ * or where the caller forbids allocation.  No counterpart in the reference:
+ * it exists for callers that cannot allocate.  Same arguments, launches and
+ * results (bit for bit) as tl_attn_decode_gqa; the split-K partials and, for
+ * plans too large for the kernel arguments, the plan metadata go to a static
+ * device array of tl_attn_noalloc_scratch_bytes() bytes (16 MiB) that each GPU
+ * holds until the process ends.  A call that would need more is rejected
+ * with TL_ERR_INVALID: per split item Hq*(D+2)*4 bytes of partials, plus
+ * 4*(2B+1+2*items) bytes of metadata when that exceeds 896 words.  All calls
+ * on one GPU share its array (the last call's contents stay): calls that
+ * overlap on one GPU race. */
+int tl_attn_decode_gqa_noalloc(const void *q, const tl_kv_view *kv, const int32_t *seq_lens_host,
+                               int B, int Hq, int Hkv, int D, float scale, void *out, void *stream);
+/* Size in bytes of the static scratch array of tl_attn_decode_gqa_noalloc. */
+size_t tl_attn_noalloc_scratch_bytes(void);
+
 /* attention_decode (kernels/attention.cuh:15-18, attention.cu:114-128):
  * q [B][H][D], k/v [B][H][S][D], out [B][H][D] fp16 device pointers.
  * Silently returns on non-positive dimensions, like the reference. */

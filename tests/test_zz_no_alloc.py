@@ -1,0 +1,95 @@
+"""GPU: tl_attn_decode_gqa_noalloc, the decode attention entry point that
+allocates nothing (split-K partials and spilled plan metadata in the
+library's static device scratch), against tl_attn_decode_gqa on the same
+inputs: bit-identical outputs on two calls in a row, the second smaller than
+the first, and the oracle's 1e-3 gate.  A call that needs more scratch than
+the array holds is rejected before any launch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from devutil import rel_err, stream, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def paged_cache(tl, rng, lens, Hkv, D, blk=16):
+    """K/V in 16-token blocks at seeded random physical positions; returns
+    (keep-alive tensors, tl view, host pool bits, oracle block table)."""
+    nblk = [max(1, -(-int(s) // blk)) for s in lens]
+    total = sum(nblk)
+    phys = rng.permutation(total).astype(np.int32)
+    width = max(nblk)
+    bt = np.zeros((len(lens), width), dtype=np.int32)
+    o = 0
+    for b, n in enumerate(nblk):
+        bt[b, :n] = phys[o:o + n]
+        o += n
+    row = Hkv * D
+    pool = (rng.standard_normal(2 * total * blk * row) * 1.0).astype(np.float16).view(np.uint16)
+    dpool = torch.from_numpy(pool.view(np.int16).copy()).cuda()
+    dbt = torch.from_numpy(bt.copy()).cuda()
+    base = dpool.data_ptr()
+    view = tl.KVView(base, base + 2 * total * blk * row, dbt.data_ptr(), width, 4, blk * row, row, D)
+    return (dpool, dbt), view, pool, bt, total * blk * row
+
+
+def run_pair(tl, orc, rng, lens, Hq, Hkv, D):
+    keep, view, pool, bt, v_off = paged_cache(tl, rng, lens, Hkv, D)
+    B = len(lens)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16).view(np.uint16)
+    dq = torch.from_numpy(q.view(np.int16).copy()).cuda()
+    ref_out = torch.empty((B, Hq, D), dtype=torch.float16, device="cuda")
+    got_out = torch.full((B, Hq, D), float("nan"), dtype=torch.float16, device="cuda")
+    scale = 1.0 / np.sqrt(D)
+    tl.attn_decode_gqa(dq.data_ptr(), view, lens, Hq, Hkv, D, scale, ref_out.data_ptr(), stream())
+    tl.attn_decode_gqa_noalloc(dq.data_ptr(), view, lens, Hq, Hkv, D, scale, got_out.data_ptr(),
+                               stream())
+    got, ref = to_host(got_out), to_host(ref_out)
+    assert np.array_equal(got, ref), "noalloc output differs from tl_attn_decode_gqa"
+    oview = orc.View(pool, 0, v_off, bt, 4, 16 * Hkv * D, Hkv * D, D)
+    ref32, _ = orc.attn_decode_gqa(q, oview, np.asarray(lens), Hq, Hkv, D, scale, nthreads=8)
+    g32 = got.view(np.float16).astype(np.float32)
+    errs = [rel_err(g32[b], ref32[b]) for b in range(B)]
+    assert max(errs) <= 1e-3, max(errs)
+    return keep
+
+
+def test_noalloc_matches_decode_gqa_twice_then_smaller(tl, orc):
+    rng = np.random.default_rng(20261202)
+    Hq, Hkv, D = 16, 2, 128
+    # call 1: 300 sequences, one of 30000 tokens split into many chunks
+    # (partials in the scratch), metadata beyond the kernel arguments (filled
+    # into the scratch by the metadata kernel), empty sequences included
+    lens1 = np.concatenate([[30000, 0], rng.integers(1, 1000, 298)]).astype(np.int32)
+    p1 = tl.attn_plan(lens1, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
+                      with_rows=False)
+    assert p1["any_multi"] == 1 and p1["inline_words"] == -1
+    run_pair(tl, orc, rng, lens1, Hq, Hkv, D)
+    # call 2: five sequences, metadata in the kernel arguments, partials in
+    # the scratch the first call left behind
+    lens2 = np.array([5000, 100, 0, 3000, 1], dtype=np.int32)
+    p2 = tl.attn_plan(lens2, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
+                      with_rows=False)
+    assert p2["any_multi"] == 1 and p2["inline_words"] > 0
+    run_pair(tl, orc, rng, lens2, Hq, Hkv, D)
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch(tl, monkeypatch):
+    """400 split items of 64 heads x (256 + 2) fp32 need 26 MB of partials,
+    more than the 16 MiB array: rejected with a clear error, nothing runs."""
+    assert tl.attn_noalloc_scratch_bytes() == 16 << 20
+    monkeypatch.setenv("TL_ATTN_CHUNK", "256")
+    B, Hq, Hkv, D = 100, 64, 8, 256
+    buf = torch.zeros(1 << 16, dtype=torch.float16, device="cuda")
+    bt = torch.zeros((B, 64), dtype=torch.int32, device="cuda")
+    out = torch.zeros((B, Hq, D), dtype=torch.float16, device="cuda")
+    view = tl.KVView(buf.data_ptr(), buf.data_ptr(), bt.data_ptr(), 64, 4, 16 * Hkv * D, Hkv * D, D)
+    lens = np.full(B, 1000, dtype=np.int32)
+    with pytest.raises(tl.TinyLLMError, match="bytes of scratch"):
+        tl.attn_decode_gqa_noalloc(buf.data_ptr(), view, lens, Hq, Hkv, D, 0.0625, out.data_ptr(),
+                                   stream())
+    torch.cuda.synchronize()
+    assert not out.any().item()

@@ -24,24 +24,32 @@ namespace {
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 } // namespace
 
+std::string check_decode_view_args(const char *who, const __half *q, const KvView &kv,
+                                   const int32_t *seq_lens_host, int B, int Hq, int Hkv, int D,
+                                   const __half *out) {
+    const std::string w(who);
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0) return w + ": invalid dimensions";
+    if (B == 0) return "";
+    if (Hq % Hkv != 0) return w + ": Hq must be a multiple of Hkv";
+    if (!attn_shape_supported(D, Hq / Hkv))
+        return w + ": unsupported head_dim/group (head_dim in {32,64,128,256}, Hq/Hkv in {1,2,4,8})";
+    if (!q || !out || !kv.k_base || !kv.v_base || !seq_lens_host) return w + ": null pointer argument";
+    if (!aligned16(q) || !aligned16(kv.k_base) || !aligned16(kv.v_base))
+        return w + ": q, k_base and v_base must be 16-byte aligned";
+    if (kv.tok_stride % 8 != 0 || kv.head_stride % 8 != 0 || kv.blk_stride % 8 != 0)
+        return w + ": strides must be multiples of 8 elements";
+    if (kv.log2_blk < 4 || kv.log2_blk > 30) return w + ": log2_blk must be in [4, 30]";
+    for (int b = 0; b < B; ++b)
+        if (seq_lens_host[b] < 0) return w + ": negative sequence length";
+    return "";
+}
+
 // Returns "" on success, else the reason the call was rejected.
 std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *seq_lens_host, int B,
                              int Hq, int Hkv, int D, float scale, __half *out, hipStream_t stream) {
-    if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0) return "tl_attn_decode_gqa: invalid dimensions";
-    if (B == 0) return "";
-    if (Hq % Hkv != 0) return "tl_attn_decode_gqa: Hq must be a multiple of Hkv";
-    if (!attn_shape_supported(D, Hq / Hkv))
-        return "tl_attn_decode_gqa: unsupported head_dim/group (head_dim in {32,64,128,256}, "
-               "Hq/Hkv in {1,2,4,8})";
-    if (!q || !out || !kv.k_base || !kv.v_base || !seq_lens_host)
-        return "tl_attn_decode_gqa: null pointer argument";
-    if (!aligned16(q) || !aligned16(kv.k_base) || !aligned16(kv.v_base))
-        return "tl_attn_decode_gqa: q, k_base and v_base must be 16-byte aligned";
-    if (kv.tok_stride % 8 != 0 || kv.head_stride % 8 != 0 || kv.blk_stride % 8 != 0)
-        return "tl_attn_decode_gqa: strides must be multiples of 8 elements";
-    if (kv.log2_blk < 4 || kv.log2_blk > 30) return "tl_attn_decode_gqa: log2_blk must be in [4, 30]";
-    for (int b = 0; b < B; ++b)
-        if (seq_lens_host[b] < 0) return "tl_attn_decode_gqa: negative sequence length";
+    const std::string bad =
+        check_decode_view_args("tl_attn_decode_gqa", q, kv, seq_lens_host, B, Hq, Hkv, D, out);
+    if (!bad.empty() || B == 0) return bad;
 
     WorkList wl;
     plan_work(seq_lens_host, B, Hkv, D, wl);

@@ -316,6 +316,31 @@ int tl_attn_decode_gqa(const void *q, const tl_kv_view *kv, const int32_t *seq_l
     });
 }
 
+int tl_attn_decode_gqa_noalloc(const void *q, const tl_kv_view *kv, const int32_t *seq_lens_host,
+                               int B, int Hq, int Hkv, int D, float scale, void *out,
+                               void *stream) {
+    if (!kv) return fail(TL_ERR_INVALID, "tl_attn_decode_gqa_noalloc: kv is null");
+    return guarded([&] {
+        tiny_llm::detail::KvView v;
+        v.k_base = as_half(kv->k_base);
+        v.v_base = as_half(kv->v_base);
+        v.block_table = kv->block_table;
+        v.seq_row = nullptr;
+        v.bt_stride = kv->bt_stride;
+        v.log2_blk = kv->log2_blk;
+        v.blk_stride = kv->blk_stride;
+        v.tok_stride = kv->tok_stride;
+        v.head_stride = kv->head_stride;
+        const std::string err = tiny_llm::detail::attn_decode_view_noalloc(
+            as_half(q), v, seq_lens_host, B, Hq, Hkv, D, scale, as_half(out), as_stream(stream));
+        if (!err.empty()) return fail(TL_ERR_INVALID, err);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+size_t tl_attn_noalloc_scratch_bytes(void) { return tiny_llm::detail::attn_noalloc_scratch_bytes(); }
+
 int tl_w8a16_matmul(const void *input, const int8_t *weight, const void *scales, void *output, int M,
                     int N, int K, int group_size, void *stream) {
     return guarded([&] {

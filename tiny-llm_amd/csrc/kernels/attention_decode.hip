@@ -1296,7 +1296,8 @@ void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkL
 
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
                         int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
-                        const __half *new_v, hipStream_t stream, const InlineMeta *inl) {
+                        const __half *new_v, hipStream_t stream, const InlineMeta *inl,
+                        bool hooks) {
     const int G = Hq / Hkv;
     if (plan.n_work <= 0 && !plan.any_empty) return;
     const bool paged = kv.block_table != nullptr;
@@ -1332,14 +1333,14 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
 
     if (plan.n_work > 0 && use_mma_path(D, G)) {
         const int nw = waves_for((int64_t)plan.n_work * Hkv);
-        profile_begin(KernelId::AttnChunk, stream);
+        if (hooks) profile_begin(KernelId::AttnChunk, stream);
         if (D == 64) launch_mma_d<64>(args, plan.n_work, Hkv, G, paged, nw, stream);
         else launch_mma_d<128>(args, plan.n_work, Hkv, G, paged, nw, stream);
         HIP_CHECK(hipGetLastError());
-        profile_end(KernelId::AttnChunk, stream);
+        if (hooks) profile_end(KernelId::AttnChunk, stream);
     } else if (plan.n_work > 0) {
         const int nw = waves_for((int64_t)plan.n_work * Hkv);
-        profile_begin(KernelId::AttnChunk, stream);
+        if (hooks) profile_begin(KernelId::AttnChunk, stream);
         switch (D) {
         case 32: launch_d<32>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
         case 64: launch_d<64>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
@@ -1348,7 +1349,7 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         default: break;
         }
         HIP_CHECK(hipGetLastError());
-        profile_end(KernelId::AttnChunk, stream);
+        if (hooks) profile_end(KernelId::AttnChunk, stream);
     }
 
     if (plan.any_multi || plan.any_empty) {
@@ -1362,7 +1363,7 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         m.Hkv = Hkv;
         if (inl) std::memcpy(&m.meta, inl, sizeof(InlineMeta));
         else m.meta.n = 0;
-        profile_begin(KernelId::AttnMerge, stream);
+        if (hooks) profile_begin(KernelId::AttnMerge, stream);
         switch (D) {
         case 32: launch_merge_g<32>(m, B, Hkv, G, stream); break;
         case 64: launch_merge_g<64>(m, B, Hkv, G, stream); break;
@@ -1371,7 +1372,7 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         default: break;
         }
         HIP_CHECK(hipGetLastError());
-        profile_end(KernelId::AttnMerge, stream);
+        if (hooks) profile_end(KernelId::AttnMerge, stream);
     }
 }
 

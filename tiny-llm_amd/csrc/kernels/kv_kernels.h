@@ -8,6 +8,7 @@
 #include "attn_plan.h"
 
 #include <cstdint>
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -74,9 +75,28 @@ bool attn_shape_supported(int D, int G);
 // offset of a non-paged view does not fit in 32 bits.
 // inl (optional): the plan's metadata in kernel arguments; when given, the
 // seq_lens / work / part_base pointers of plan and kv.seq_row are not read.
+// hooks = false: no tl_profile_* event hooks around the launches (the
+// no-allocation entry point).
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
                         int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
-                        const __half *new_v, hipStream_t stream, const InlineMeta *inl = nullptr);
+                        const __half *new_v, hipStream_t stream, const InlineMeta *inl = nullptr,
+                        bool hooks = true);
+
+// Argument checks shared by the view-based decode entry points: "" when the
+// call is valid, else the reason, prefixed by `who`.
+std::string check_decode_view_args(const char *who, const __half *q, const KvView &kv,
+                                   const int32_t *seq_lens_host, int B, int Hq, int Hkv, int D,
+                                   const __half *out);
+
+// tl_attn_decode_gqa_noalloc: the same launches as the view-based decode,
+// with the split-K partials and, when the plan does not fit in the kernel
+// arguments, its metadata in the library's static device scratch array
+// (no allocation).  "" on success, else the reason the call was rejected.
+std::string attn_decode_view_noalloc(const __half *q, const KvView &kv,
+                                     const int32_t *seq_lens_host, int B, int Hq, int Hkv, int D,
+                                     float scale, __half *out, hipStream_t stream);
+// Bytes of the static scratch array of attn_decode_view_noalloc.
+size_t attn_noalloc_scratch_bytes();
 
 // One token row ([Hkv][D] contiguous: tok_stride == Hkv*D, head_stride == D)
 // per (entry i, layer l) for n entries and num_layers layers.

@@ -135,6 +135,8 @@ def _declare(L: C.CDLL) -> None:
         "tl_w8a16_matmul_residual": (i, [vp, vp, vp, vp, i, i, i, i, i, vp]),
         "tl_w8a16_set_path": (i, [i]),
         "tl_attn_decode_gqa": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
+        "tl_attn_decode_gqa_noalloc": (i, [vp, C.POINTER(KVView), vp, i, i, i, i, f, vp, vp]),
+        "tl_attn_noalloc_scratch_bytes": (sz, []),
         "tl_attention_decode": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
         "tl_attention_prefill": (None, [vp, vp, vp, vp, f, i, i, i, i, vp]),
         "tl_softmax": (None, [vp, vp, i, i, vp]),
@@ -420,6 +422,19 @@ def attn_decode_gqa(q, view: KVView, seq_lens, Hq, Hkv, D, scale, out, stream=0)
     lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
     _check(load().tl_attn_decode_gqa(q, C.byref(view), lens.ctypes.data, lens.size, Hq, Hkv, D,
                                      scale, out, stream))
+
+
+def attn_decode_gqa_noalloc(q, view: KVView, seq_lens, Hq, Hkv, D, scale, out, stream=0):
+    """tl_attn_decode_gqa_noalloc: tl_attn_decode_gqa with the library's
+    static device scratch instead of any allocation."""
+    import numpy as np
+    lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    _check(load().tl_attn_decode_gqa_noalloc(q, C.byref(view), lens.ctypes.data, lens.size, Hq,
+                                             Hkv, D, scale, out, stream))
+
+
+def attn_noalloc_scratch_bytes() -> int:
+    return load().tl_attn_noalloc_scratch_bytes()
 
 
 def attention_decode(q, k, v, out, scale, batch, num_heads, seq_len, head_dim, stream=0):
