@@ -8,7 +8,7 @@
 #include "kernels/prefill.h"
 #include "runtime.h"
 #include "tiny_llm/hip_utils.h"
-#include "tiny_llm/logger.h"
+#include "tl_log.h"
 
 #include <algorithm>
 #include <cstdint>
@@ -169,7 +169,7 @@ void attention_prefill(const half *query, const half *key, const half *value, ha
     } catch (const std::exception &e) {
         err = e.what();
     }
-    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+    if (!err.empty()) TL_LOG_ERROR("%s", err.c_str());
 }
 
 void softmax(const half *input, half *output, int batch_size, int seq_len, hipStream_t stream) {
@@ -177,7 +177,7 @@ void softmax(const half *input, half *output, int batch_size, int seq_len, hipSt
     try {
         detail::launch_softmax(input, output, batch_size, seq_len, stream);
     } catch (const std::exception &e) {
-        TLLM_ERROR("softmax: %s", e.what());
+        TL_LOG_ERROR("softmax: %s", e.what());
     }
 }
 
@@ -189,7 +189,7 @@ void get_attention_weights(const half *query, const half *key, half *weights, fl
         detail::launch_attention_weights(query, key, weights, scale, batch_size, num_heads,
                                          query_len, key_len, head_dim, apply_causal_mask, stream);
     } catch (const std::exception &e) {
-        TLLM_ERROR("get_attention_weights: %s", e.what());
+        TL_LOG_ERROR("get_attention_weights: %s", e.what());
     }
 }
 
@@ -204,7 +204,7 @@ void attention_decode(const half *query, const half *k_cache, const half *v_cach
     } catch (const std::exception &e) {
         err = e.what();
     }
-    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+    if (!err.empty()) TL_LOG_ERROR("%s", err.c_str());
 }
 
 } // namespace kernels

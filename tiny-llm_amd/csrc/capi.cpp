@@ -6,7 +6,7 @@
 #include "runtime.h"
 #include "tiny_llm/kernels/attention.h"
 #include "tiny_llm/kv_cache.h"
-#include "tiny_llm/logger.h"
+#include "tl_log.h"
 
 #include <algorithm>
 #include <cstring>
@@ -391,7 +391,7 @@ void tl_attention_decode(const void *q, const void *k, const void *v, void *out,
             as_half(q), as_half(k), as_half(v), as_half(out), scale, batch, num_heads, seq_len,
             head_dim, as_stream(stream));
         if (!err.empty()) {
-            TLLM_ERROR("%s", err.c_str());
+            TL_LOG_ERROR("%s", err.c_str());
             return fail(TL_ERR_INVALID, err);
         }
         g_last_error.clear();
@@ -464,7 +464,7 @@ void tl_attention_prefill(const void *q, const void *k, const void *v, void *out
             as_half(q), as_half(k), as_half(v), as_half(out), scale, batch, num_heads, seq_len,
             head_dim, as_stream(stream));
         if (!err.empty()) {
-            TLLM_ERROR("%s", err.c_str());
+            TL_LOG_ERROR("%s", err.c_str());
             return fail(TL_ERR_INVALID, err);
         }
         g_last_error.clear();

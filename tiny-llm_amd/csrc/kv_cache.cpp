@@ -13,7 +13,7 @@
 #include "kernels/prefill.h"
 #include "kernels/w8a16.h"
 #include "runtime.h"
-#include "tiny_llm/logger.h"
+#include "tl_log.h"
 
 #include <algorithm>
 #include <climits>
@@ -173,7 +173,7 @@ Result<int> KVCacheManager::allocateSequence(int max_len) {
 Result<void> KVCacheManager::releaseSequence(int seq_id) {
     auto it = seq_to_slot_.find(seq_id);
     if (it == seq_to_slot_.end()) {
-        TLLM_WARN("releaseSequence: sequence not found: %d", seq_id);
+        TL_LOG_WARN("releaseSequence: sequence not found: %d", seq_id);
         return Result<void>::err("Sequence not found: " + std::to_string(seq_id));
     }
     auto &slot = slots_[static_cast<size_t>(it->second)];
@@ -181,7 +181,7 @@ Result<void> KVCacheManager::releaseSequence(int seq_id) {
     slot.active = false;
     slot.seq_id = -1;
     slot.current_len = 0;
-    TLLM_DEBUG("KVCache: released sequence %d (slot %d)", seq_id, it->second);
+    TL_LOG_DEBUG("KVCache: released sequence %d (slot %d)", seq_id, it->second);
     seq_to_slot_.erase(it);
     return Result<void>::ok();
 }
@@ -208,7 +208,7 @@ Result<std::pair<half *, half *>> KVCacheManager::getCacheChecked(int seq_id, in
 std::pair<half *, half *> KVCacheManager::getCache(int seq_id, int layer_idx) {
     auto result = getCacheChecked(seq_id, layer_idx);
     if (result.isErr()) {
-        TLLM_WARN("getCache: %s", result.error().c_str());
+        TL_LOG_WARN("getCache: %s", result.error().c_str());
         return {nullptr, nullptr};
     }
     return result.value();
@@ -218,27 +218,27 @@ std::pair<half *, half *> KVCacheManager::getCache(int seq_id, int layer_idx) {
 Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new_k,
                                       const half *new_v, int num_tokens, hipStream_t stream) {
     if (new_k == nullptr) {
-        TLLM_ERROR("appendKV: new_k is null");
+        TL_LOG_ERROR("appendKV: new_k is null");
         return Result<void>::err("new_k is null");
     }
     if (new_v == nullptr) {
-        TLLM_ERROR("appendKV: new_v is null");
+        TL_LOG_ERROR("appendKV: new_v is null");
         return Result<void>::err("new_v is null");
     }
     if (num_tokens <= 0) {
-        TLLM_ERROR("appendKV: invalid num_tokens: %d", num_tokens);
+        TL_LOG_ERROR("appendKV: invalid num_tokens: %d", num_tokens);
         return Result<void>::err("appendKV: num_tokens must be positive: " +
                                  std::to_string(num_tokens));
     }
     if (layer_idx < 0 || layer_idx >= config_.num_layers) {
         std::string msg = "appendKV: Invalid layer_idx: " + std::to_string(layer_idx) +
                           " (valid range: 0-" + std::to_string(config_.num_layers - 1) + ")";
-        TLLM_ERROR("%s", msg.c_str());
+        TL_LOG_ERROR("%s", msg.c_str());
         return Result<void>::err(msg);
     }
     auto it = seq_to_slot_.find(seq_id);
     if (it == seq_to_slot_.end()) {
-        TLLM_ERROR("appendKV: sequence not found: %d", seq_id);
+        TL_LOG_ERROR("appendKV: sequence not found: %d", seq_id);
         return Result<void>::err("appendKV: sequence not found: " + std::to_string(seq_id));
     }
     const int slot_idx = it->second;
@@ -247,7 +247,7 @@ Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new
     // advanced once after the last layer (kv_cache.cpp:204-208).
     const int write_pos = slot.current_len;
     if (write_pos + num_tokens > slot.max_len) {
-        TLLM_ERROR("appendKV: cache overflow. seq_id=%d, write_pos=%d, num_tokens=%d, max_len=%d",
+        TL_LOG_ERROR("appendKV: cache overflow. seq_id=%d, write_pos=%d, num_tokens=%d, max_len=%d",
                    seq_id, write_pos, num_tokens, slot.max_len);
         return Result<void>::err("appendKV: cache overflow. Current: " + std::to_string(write_pos) +
                                  ", appending: " + std::to_string(num_tokens) +
@@ -258,7 +258,7 @@ Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new
         const int need = (write_pos + num_tokens + block_tokens_ - 1) / block_tokens_;
         if (!blocks_->ensure(slot_idx, need)) {
             auto r = exhausted(need - blocks_->mapped(slot_idx));
-            TLLM_ERROR("appendKV: %s", r.error().c_str());
+            TL_LOG_ERROR("appendKV: %s", r.error().c_str());
             return r;
         }
         syncTable(stream);
@@ -278,7 +278,7 @@ Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new
         v.bt_stride = 0;
         detail::launch_kv_append(v, 0, nullptr, write_pos, num_tokens, 1, row, new_k, new_v, stream);
     }
-    TLLM_TRACE("appendKV: seq_id=%d, layer=%d, num_tokens=%d, write_pos=%d", seq_id, layer_idx,
+    TL_LOG_TRACE("appendKV: seq_id=%d, layer=%d, num_tokens=%d, write_pos=%d", seq_id, layer_idx,
                num_tokens, write_pos);
     return Result<void>::ok();
 }
@@ -286,13 +286,13 @@ Result<void> KVCacheManager::appendKV(int seq_id, int layer_idx, const half *new
 // advanceSeqLen (kv_cache.cpp:240-259).
 Result<void> KVCacheManager::advanceSeqLen(int seq_id, int num_tokens) {
     if (num_tokens <= 0) {
-        TLLM_ERROR("advanceSeqLen: invalid num_tokens: %d", num_tokens);
+        TL_LOG_ERROR("advanceSeqLen: invalid num_tokens: %d", num_tokens);
         return Result<void>::err("advanceSeqLen: num_tokens must be positive: " +
                                  std::to_string(num_tokens));
     }
     auto it = seq_to_slot_.find(seq_id);
     if (it == seq_to_slot_.end()) {
-        TLLM_ERROR("advanceSeqLen: sequence not found: %d", seq_id);
+        TL_LOG_ERROR("advanceSeqLen: sequence not found: %d", seq_id);
         return Result<void>::err("advanceSeqLen: sequence not found: " + std::to_string(seq_id));
     }
     auto     &slot = slots_[static_cast<size_t>(it->second)];
@@ -304,12 +304,12 @@ Result<void> KVCacheManager::advanceSeqLen(int seq_id, int num_tokens) {
         const int need = (new_len + block_tokens_ - 1) / block_tokens_;
         if (!blocks_->ensure(it->second, need)) {
             auto r = exhausted(need - blocks_->mapped(it->second));
-            TLLM_ERROR("advanceSeqLen: %s", r.error().c_str());
+            TL_LOG_ERROR("advanceSeqLen: %s", r.error().c_str());
             return r;
         }
     }
     slot.current_len = new_len;
-    TLLM_TRACE("advanceSeqLen: seq_id=%d, %d -> %d", seq_id, old_len, slot.current_len);
+    TL_LOG_TRACE("advanceSeqLen: seq_id=%d, %d -> %d", seq_id, old_len, slot.current_len);
     (void)old_len;
     return Result<void>::ok();
 }

@@ -2,7 +2,7 @@
 
 #include "kernels/kv_kernels.h"
 #include "tiny_llm/hip_utils.h"
-#include "tiny_llm/logger.h"
+#include "tl_log.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -18,38 +18,40 @@
 
 namespace tiny_llm {
 
-// ------------------------------------------------------------------ logger
+// ------------------------------------------------------------------ log
+namespace detail {
+namespace log {
 namespace {
-LogLevel level_from_env() {
+Level level_from_env() {
     const char *s = std::getenv("TLLM_LOG_LEVEL");
-    if (!s) return LogLevel::WARN;
-    const std::pair<const char *, LogLevel> names[] = {
-        {"trace", LogLevel::TRACE}, {"debug", LogLevel::DEBUG}, {"info", LogLevel::INFO},
-        {"warn", LogLevel::WARN},   {"error", LogLevel::ERROR}, {"critical", LogLevel::CRITICAL},
-        {"off", LogLevel::OFF}};
+    if (!s) return Level::WARN;
+    const std::pair<const char *, Level> names[] = {
+        {"trace", Level::TRACE}, {"debug", Level::DEBUG}, {"info", Level::INFO},
+        {"warn", Level::WARN},   {"error", Level::ERROR}, {"critical", Level::CRITICAL},
+        {"off", Level::OFF}};
     for (const auto &n : names)
         if (std::strcmp(s, n.first) == 0) return n.second;
-    return LogLevel::WARN;
+    return Level::WARN;
 }
 std::atomic<int> g_level{-1};
-const char      *level_name(LogLevel l) {
+const char      *level_name(Level l) {
     static const char *n[] = {"trace", "debug", "info", "warn", "error", "critical", "off"};
     return n[static_cast<int>(l)];
 }
 } // namespace
 
-void Logger::setLevel(LogLevel level) { g_level.store(static_cast<int>(level)); }
+void set_level(Level level) { g_level.store(static_cast<int>(level)); }
 
-LogLevel Logger::level() {
+Level level() {
     int l = g_level.load(std::memory_order_relaxed);
     if (l < 0) {
         l = static_cast<int>(level_from_env());
         g_level.store(l);
     }
-    return static_cast<LogLevel>(l);
+    return static_cast<Level>(l);
 }
 
-void Logger::log(LogLevel level, const char *fmt, ...) {
+void write(Level level, const char *fmt, ...) {
     char    buf[1024];
     va_list ap;
     va_start(ap, fmt);
@@ -57,6 +59,8 @@ void Logger::log(LogLevel level, const char *fmt, ...) {
     va_end(ap);
     std::fprintf(stderr, "[tiny_llm] [%s] %s\n", level_name(level), buf);
 }
+} // namespace log
+} // namespace detail
 
 namespace detail {
 

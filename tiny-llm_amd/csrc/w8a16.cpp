@@ -8,7 +8,7 @@
 #include "kernels/w8a16.h"
 #include "runtime.h"
 #include "tiny_llm/hip_utils.h"
-#include "tiny_llm/logger.h"
+#include "tl_log.h"
 
 #include <mutex>
 #include <string>
@@ -61,7 +61,7 @@ void w8a16_matmul(const half *input, const int8_t *weight, const half *scales, h
     } catch (const std::exception &e) {
         err = e.what();
     }
-    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+    if (!err.empty()) TL_LOG_ERROR("%s", err.c_str());
 }
 
 void w8a16_matmul_residual(const half *input, const int8_t *weight, const half *scales, half *hidden,
@@ -73,7 +73,7 @@ void w8a16_matmul_residual(const half *input, const int8_t *weight, const half *
     } catch (const std::exception &e) {
         err = e.what();
     }
-    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+    if (!err.empty()) TL_LOG_ERROR("%s", err.c_str());
 }
 
 void w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, hipStream_t stream) {
@@ -83,7 +83,7 @@ void w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, hipStream_t 
     } catch (const std::exception &e) {
         err = e.what();
     }
-    if (!err.empty()) TLLM_ERROR("%s", err.c_str());
+    if (!err.empty()) TL_LOG_ERROR("%s", err.c_str());
 }
 
 } // namespace kernels
