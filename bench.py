@@ -35,7 +35,6 @@ sys.path.insert(0, os.path.join(REPO, "tiny-llm_amd"))
 METRIC = ("decode attn+KV append µs/step and achieved HBM GB/s (% of peak), "
           "8B GQA b64 ctx8k")
 HBM_PEAK_GBPS = 8000.0
-PMC_SUMMARY = os.path.join(REPO, "profiles", "attn_decode_kernel_cfg3_pmc.txt")
 
 
 def parse():
@@ -44,7 +43,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=0,
                     help="timed steps (default: 100 for configs 2-4, 1000 for config 5)")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5))
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5),
+                    help="1: latency of the small MHA case; 2-4: fixed batches; 5: churn")
     ap.add_argument("--path", default="decode", choices=("decode", "project", "oproj", "prefill"),
                     help="decode: append + attention (the headline); project: the decode step's "
                          "fused QKV W8A16 projection writing K/V into the cache; oproj: the W8A16 "
@@ -60,7 +60,7 @@ def parse():
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="target CPU work of the cpu_baseline sample")
+                    help="target CPU work of the cpu_baseline sample (at least one full step)")
     ap.add_argument("--q-heads", type=int, default=0,
                     help="override the number of query heads of configs 2-4 (64 on config 3 "
                          "gives the group-8 head shape of config 5 at batch 64 / context 8192)")
@@ -70,18 +70,28 @@ def parse():
     ap.add_argument("--block-tokens", type=int, default=16, help="tokens per block of --alloc blocks")
     ap.add_argument("--kv-gib", type=float, default=0.0,
                     help="config 5: HBM budget of the KV pool in GiB (default: 1280 full slots)")
+    ap.add_argument("--max-seq-len", type=int, default=0,
+                    help="configs 1-4: max_seq_len of the pool (default: the context plus the "
+                         "appended steps, rounded up to 64 tokens)")
+    ap.add_argument("--launch-log", default="",
+                    help="append the algorithmic bytes of every decode attention launch (fused "
+                         "append included), in launch order, as JSON lines to this file "
+                         "(profiling runs: matched against rocprofv3 --pmc dispatches)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run one device-to-device copy of this many MiB (HBM counter "
                          "calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
-def cpu_threads() -> int:
+def cpu_counts():
+    """(CPUs this process may run on, OpenMP threads the CPU baseline uses).
+    A one-GPU box allots 16 host CPUs to the job, so at most 16 threads run
+    whatever the affinity mask shows."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(16, n))
+    return n, max(1, min(16, n))
 
 
 def _cpu_model() -> str:
@@ -95,66 +105,184 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(cfg, target_s: float):
-    """The oracle (C restatement of the reference path) on host cores: a
-    bounded sample of the same workload -- 8 of the 64 sequences at full
-    context, full decode steps (appendKV + attention + advance)."""
+def d2h(dst_ptr: int, src_ptr: int, nbytes: int):
+    """hipMemcpy device -> host (the caller synchronised the device)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    rc = hip.hipMemcpy(dst_ptr, src_ptr, nbytes, 2)
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy D2H failed: {rc}")
+
+
+def host_bits(t):
+    """fp16 device tensor -> numpy uint16 bit patterns."""
+    import numpy as np
+    import torch
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def cpu_baseline_fixed(st, target_s: float):
+    """The oracle (the C restatement of the reference's path) on the host
+    cores, on the inputs the GPU run ended with: the device pool is copied
+    byte for byte into the oracle's pool (same layout), then full-batch decode
+    steps run -- per layer the step's K/V row of every sequence written at its
+    tail (appendKV), attention of every sequence over its cache, then
+    advanceSeqLen -- until target_s of work (at least one step, at most what
+    the pool's max_seq_len leaves)."""
     import numpy as np
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as orc
     import workloads
 
-    nseq, ctx = 8, int(cfg.contexts[0])
-    Hkv, Hq, D = cfg.hkv, cfg.hq, cfg.head_dim
-    M = ctx + 64
-    kv = orc.KVCacheOracle(1, Hkv, D, M, nseq)
-    rng = np.random.default_rng(workloads.seed(3, 1))
-    ids = []
-    for _ in range(nseq):
-        sid, _ = kv.allocate(M)
-        k = rng.standard_normal(ctx * Hkv * D, dtype=np.float32).astype(np.float16).view(np.uint16)
-        v = rng.standard_normal(ctx * Hkv * D, dtype=np.float32).astype(np.float16).view(np.uint16)
-        kv.append(sid, 0, k, v, ctx)
-        kv.advance(sid, ctx)
-        ids.append(sid)
-    threads = cpu_threads()
-    q = rng.standard_normal((nseq, Hq, D), dtype=np.float32).astype(np.float16).view(np.uint16)
-    nk = rng.standard_normal((nseq, Hkv * D), dtype=np.float32).astype(np.float16).view(np.uint16)
+    mgr, ids, L, Hq, Hkv, D, M = st["mgr"], st["ids"], st["L"], st["Hq"], st["Hkv"], st["D"], st["M"]
+    B = len(ids)
+    o = orc.KVCacheOracle(L, Hkv, D, M, B)
+    oids = [o.allocate(M)[0] for _ in ids]
+    assert [o.slot_of(x) for x in oids] == [mgr.slot_of(x) for x in ids]
+    st["torch"].cuda.synchronize()
+    pool = o.pool()
+    d2h(pool.ctypes.data, mgr.pool(), pool.nbytes)
+    lens = np.array([mgr.getSeqLen(x) for x in ids], dtype=np.int64)
+    for x, n in zip(oids, lens):
+        assert o.advance(x, int(n)) is None
+    qh = [host_bits(st["q"][layer]) for layer in range(L)]
+    nkh = [host_bits(st["nk"][layer]) for layer in range(L)]
+    nvh = [host_bits(st["nv"][layer]) for layer in range(L)]
+    row, kvpl = Hkv * D, Hkv * M * D
+    bs = st["block_tokens"]
+    if bs:  # block map over the slot pool: the GPU's physical blocks
+        bt = np.array([mgr.blockTable(x)[0] for x in ids], dtype=np.int32)
+        lg = bs.bit_length() - 1
+        views = [orc.paged_view(pool, L, Hkv, D, M, layer, bt, lg) for layer in range(L)]
+    else:
+        slots = [o.slot_of(x) for x in oids]
+        views = [orc.cache_view(pool, L, Hkv, D, M, layer, slots) for layer in range(L)]
+    nproc, threads = cpu_counts()
+    room = int(M - lens.max())
     steps, total_bytes, t_used = 0, 0, 0.0
-    while t_used < target_s and steps < 1024:
-        lens = np.array([kv.seq_len(s) + 1 for s in ids])
+    while steps < room and (steps == 0 or t_used < target_s):
+        t0 = time.perf_counter()
+        for layer in range(L):
+            for i, x in enumerate(oids):
+                if bs:
+                    t = int(lens[i])
+                    e = layer * 2 * kvpl + int(bt[i, t >> lg]) * bs * row + (t & (bs - 1)) * row
+                    pool[e:e + row] = nkh[layer][i]
+                    pool[e + kvpl:e + kvpl + row] = nvh[layer][i]
+                else:
+                    o.append(x, layer, nkh[layer][i], nvh[layer][i], 1)
+            orc.attn_decode_gqa(qh[layer], views[layer], lens + 1, Hq, Hkv, D, st["scale"],
+                                nthreads=threads)
+        for x in oids:
+            o.advance(x, 1)
+        t_used += time.perf_counter() - t0
+        total_bytes += workloads.step_bytes(lens, Hq, Hkv, D, layers=L, paged_block=bs)
+        lens += 1
+        steps += 1
+    return {"value": round(total_bytes / t_used / 1e9, 3), "unit": "GB/s",
+            "us_per_step": round(t_used / steps * 1e6, 1), "cores": threads, "kind": "port",
+            "sample": f"oracle C restatement on the GPU run's final cache (copied byte for byte), "
+                      f"full batch of {B} sequences x {L} layer(s), {steps} decode steps "
+                      f"(append + attention + advance), {t_used:.1f} s, {threads} OpenMP threads "
+                      f"of {nproc} CPUs in the affinity mask, cpu={_cpu_model()}"}
+
+
+def cpu_baseline_churn(st, target_s: float):
+    """Configuration 5 on the host cores: the oracle replays the same
+    seeded event sequence on the reference's slot allocator -- every arrival
+    allocated and its prompt appended (the same source rows as the GPU run),
+    every finished sequence released -- and runs full decode steps
+    (append + attention over every live sequence + advance) on evenly spaced
+    steps until target_s of attention work; the other steps advance the
+    bookkeeping only.  value = bytes of the sampled decode steps / their
+    time."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as orc
+    import workloads
+
+    K, M, slots, Hq, Hkv, D = st["K"], st["M"], st["slots"], st["Hq"], st["Hkv"], st["D"]
+    o = orc.KVCacheOracle(1, Hkv, D, M, slots)
+    sim = workloads.ChurnSim(steps=K, hq=Hq, hkv=Hkv, head_dim=D, max_seq_len=M, slots=slots)
+    nproc, threads = cpu_counts()
+    every = max(1, K // 20)
+    live, length = {}, {}
+    t_book, t_dec, dec_bytes, dec_steps, live_sampled = 0.0, 0.0, 0, 0, 0
+    for ev in sim.events():
+        t0 = time.perf_counter()
+        for prompt, life in zip(ev.arrivals, ev.lifetimes):
+            sid, err = o.allocate(M)
+            if err is not None:
+                continue
+            o.append(sid, 0, st["src_k"][:prompt], st["src_v"][:prompt], prompt)
+            o.advance(sid, prompt)
+            live[sid] = max(1, life)
+            length[sid] = prompt
+        ids = list(live)
+        t_book += time.perf_counter() - t0
+        sample = ids and ev.step % every == every - 1 and (dec_steps == 0 or t_dec < target_s)
         t0 = time.perf_counter()
         for i, sid in enumerate(ids):
-            kv.append(sid, 0, nk[i], nk[i], 1)
-        view = orc.cache_view(kv.pool(), 1, Hkv, D, M, 0, [kv.slot_of(s) for s in ids])
-        orc.attn_decode_gqa(q, view, lens, Hq, Hkv, D, cfg.scale, nthreads=threads)
+            o.append(sid, 0, st["nk"][i], st["nv"][i], 1)
+        if sample:
+            lens = np.fromiter((length[x] + 1 for x in ids), dtype=np.int64, count=len(ids))
+            view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(x) for x in ids])
+            orc.attn_decode_gqa(st["q"][:len(ids)], view, lens, Hq, Hkv, D, st["scale"],
+                                nthreads=threads)
         for sid in ids:
-            kv.advance(sid, 1)
-        t_used += time.perf_counter() - t0
-        total_bytes += workloads.step_bytes(lens - 1, Hq, Hkv, D)
-        steps += 1
-    return {"value": round(total_bytes / t_used / 1e9, 3), "unit": "GB/s", "cores": threads,
+            o.advance(sid, 1)
+            live[sid] -= 1
+            length[sid] += 1
+            if live[sid] == 0 or length[sid] >= M:
+                del live[sid]
+                del length[sid]
+                o.release(sid)
+        dt = time.perf_counter() - t0
+        if sample:
+            t_dec += dt
+            dec_bytes += workloads.step_bytes(lens - 1, Hq, Hkv, D)
+            dec_steps += 1
+            live_sampled += len(ids)
+        else:
+            t_book += dt
+    return {"value": round(dec_bytes / t_dec / 1e9, 3) if t_dec else None, "unit": "GB/s",
+            "us_per_step": round(t_dec / max(1, dec_steps) * 1e6, 1), "cores": threads,
             "kind": "port",
-            "sample": f"oracle C restatement, {nseq} of {cfg.batch} sequences at context {ctx}, "
-                      f"{steps} full decode steps (append+attention), {t_used:.1f} s, "
-                      f"{threads} OpenMP threads, cpu={_cpu_model()}"}
+            "sample": f"oracle C restatement replaying the same {K}-step event sequence on the "
+                      f"reference's slot allocator: {dec_steps} full decode steps (every {every}th "
+                      f"step, {live_sampled / max(1, dec_steps):.0f} live sequences on average) "
+                      f"timed, {t_dec:.1f} s; bookkeeping, prompt and token appends of all steps "
+                      f"{t_book:.1f} s (not in value); {threads} OpenMP threads of {nproc} CPUs, "
+                      f"cpu={_cpu_model()}"}
+
+
+def log_launches(path: str, n: int, nbytes: int, seqs: int):
+    with open(path, "a") as f:
+        for _ in range(n):
+            f.write(json.dumps({"attn_bytes": int(nbytes), "seqs": int(seqs)}) + "\n")
 
 
 def read_pmc(workload: str):
-    """HBM bytes per launch of attn_decode_kernel from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated with a copy
-    kernel), or None when no summary covers this workload."""
-    try:
-        with open(PMC_SUMMARY) as f:
-            for line in f:
-                line = line.strip()
-                if line.startswith("{"):
-                    d = json.loads(line)
-                    if d.get("workload") == workload:
-                        return d.get("traffic_bytes_per_launch")
-    except (OSError, ValueError):
-        pass
-    return None
+    """HBM bytes per launch of attn_decode_kernel for this workload from a
+    committed rocprofv3 --pmc summary (profiles/attn_decode_kernel_*_pmc.txt:
+    FETCH_SIZE + WRITE_SIZE, calibrated with a copy kernel) and the file it
+    came from, or (None, None) when no summary covers the workload.  The
+    counters cannot be read from inside this process, so the figure is the
+    profile's, not this run's."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", "attn_decode_kernel_*_pmc.txt"))):
+        try:
+            with open(path) as f:
+                for line in f:
+                    line = line.strip()
+                    if line.startswith("{"):
+                        d = json.loads(line)
+                        if d.get("workload") == workload and "traffic_bytes_per_launch" in d:
+                            return d["traffic_bytes_per_launch"], os.path.relpath(path, REPO)
+        except (OSError, ValueError):
+            continue
+    return None, None
 
 
 def kernel_stats(tl):
@@ -166,7 +294,7 @@ def kernel_stats(tl):
 
 
 def fixed_batch(args, tl, torch, workloads, np):
-    """Configurations 2-4: a fixed batch prefilled through appendKV, then K
+    """Configurations 1-4: a fixed batch prefilled through appendKV, then K
     decode steps over every layer."""
     cfg = workloads.config(args.config)
     if args.q_heads:
@@ -177,6 +305,11 @@ def fixed_batch(args, tl, torch, workloads, np):
     ctx = cfg.contexts.astype(np.int64)
     bt = cfg.block_tokens
     M = int((ctx.max() + K + 1 + 63) // 64 * 64)
+    if args.max_seq_len:
+        if args.max_seq_len < ctx.max() + K + 1 or (bt and args.max_seq_len % bt):
+            raise SystemExit(f"--max-seq-len {args.max_seq_len} cannot hold the context and "
+                             f"{K} steps" + (f" in {bt}-token blocks" if bt else ""))
+        M = args.max_seq_len
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream().cuda_stream
 
@@ -210,8 +343,14 @@ def fixed_batch(args, tl, torch, workloads, np):
     batch = tl.DecodeBatch(mgr, B, Hq)
     torch.cuda.synchronize()
 
+    paged_block = bt or (args.block_tokens if blocks else 0)
+
     def step(advance):
         batch.prepare(ids, stream)
+        if args.launch_log:
+            att = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int64)
+            log_launches(args.launch_log, L, workloads.step_bytes(att, Hq, Hkv, D, 1, paged_block),
+                         B)
         for layer in range(L):
             batch.decode(layer, q[layer].data_ptr(), nk[layer].data_ptr(), nv[layer].data_ptr(),
                          out.data_ptr(), cfg.scale, stream)
@@ -237,6 +376,16 @@ def fixed_batch(args, tl, torch, workloads, np):
     elapsed_ms = ev0.elapsed_time(ev1)
     info = batch.info()
 
+    # Per-step pass: the same steps (lengths not advanced) with one event
+    # between consecutive steps, for the spread of the step time.
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    evs[0].record()
+    for i in range(K):
+        step(advance=False)
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per_step = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(K)]) * 1e3
+
     # Kernel-timing pass: the same steps (lengths not advanced) with hipEvents
     # around every launch on the launch stream.
     tl.profile_reset()
@@ -258,6 +407,7 @@ def fixed_batch(args, tl, torch, workloads, np):
         b_ = bt or args.block_tokens
         attn_bytes += 4 * B + 4 * int(((lens_k + 1 + b_ - 1) // b_).sum())
     conf = {"workload": cfg.name, "layers": L, "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+            "max_seq_len": M,
             "head_dim": D, "context_first": int(lens0.min()), "context_max_first": int(lens0.max()),
             "context_sum_first": int(lens0.sum()),
             "block_tokens": args.block_tokens if blocks else bt, "kv_std": cfg.kv_std,
@@ -266,8 +416,14 @@ def fixed_batch(args, tl, torch, workloads, np):
             "parallelism": "single GPU"}
     data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) (torch.randn, seeded), prefilled "
             f"via appendKV" + (", 16-token blocks behind a seeded random permutation" if bt else ""))
+    cpu = None
+    if args.cpu_baseline and not blocks:
+        cpu = cpu_baseline_fixed(dict(mgr=mgr, ids=ids, L=L, Hq=Hq, Hkv=Hkv, D=D, M=M, q=q, nk=nk,
+                                      nv=nv, block_tokens=bt, scale=cfg.scale, torch=torch),
+                                 args.cpu_seconds)
     return dict(cfg=cfg, K=K, elapsed_ms=elapsed_ms, t_wall=t_wall, total_bytes=total_bytes,
                 attn_bytes=attn_bytes, ks=ks, kpass=kpass, conf=conf, data=data,
+                per_step_us=per_step, cpu=cpu,
                 kpass_desc=f"separate pass of {kpass} steps (lengths not advanced)")
 
 
@@ -317,7 +473,12 @@ def churn(args, tl, torch, workloads, np):
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         ev0.record()
+        step_ev = []
         for ev in sim.events():
+            if profile:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                step_ev.append(e)
             for prompt, life in zip(ev.arrivals, ev.lifetimes):
                 sid, err = mgr.allocateSequence(M)
                 if err is None and blocks and mgr.freeBlocks() < -(-prompt // bt) + len(live):
@@ -353,6 +514,8 @@ def churn(args, tl, torch, workloads, np):
                              stream)
                 batch.commit(1)
                 sb = workloads.step_bytes(ctx, Hq, Hkv, D)
+                if args.launch_log:
+                    log_launches(args.launch_log, 1, sb, len(ids))
                 nbytes += sb
                 attn_nbytes += sb
             live_sum += len(ids)
@@ -368,6 +531,11 @@ def churn(args, tl, torch, workloads, np):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = ev0.elapsed_time(ev1)
+        per_step = None
+        if profile and step_ev:
+            step_ev.append(ev1)
+            per_step = np.array([step_ev[i].elapsed_time(step_ev[i + 1])
+                                 for i in range(len(step_ev) - 1)]) * 1e3
         for s in list(live):
             mgr.releaseSequence(s)
         ks = None
@@ -376,6 +544,7 @@ def churn(args, tl, torch, workloads, np):
             ks = kernel_stats(tl)
             tl.profile_reset()
         return dict(ms=ms, wall=wall, nbytes=nbytes, attn_nbytes=attn_nbytes, rejected=rejected,
+                    per_step=per_step,
                     preempted=preempted, used_avg=used_sum / sim.steps,
                     live_avg=live_sum / sim.steps,
                     live_peak=peak, ks=ks)
@@ -400,9 +569,15 @@ def churn(args, tl, torch, workloads, np):
             "kv_used_avg_gib": round(timed["used_avg"] / (1 << 30), 2)}
     if blocks:
         conf["preempted"] = timed["preempted"]
+    cpu = None
+    if args.cpu_baseline:
+        cpu = cpu_baseline_churn(dict(K=K, M=M, slots=slots, Hq=Hq, Hkv=Hkv, D=D, scale=scale,
+                                      src_k=host_bits(src_k), src_v=host_bits(src_v),
+                                      q=host_bits(q), nk=host_bits(nk), nv=host_bits(nv)),
+                                 args.cpu_seconds)
     return dict(cfg=None, K=K, elapsed_ms=timed["ms"], t_wall=timed["wall"],
                 total_bytes=timed["nbytes"], attn_bytes=prof["attn_nbytes"] / launches, ks=ks,
-                kpass=K, conf=conf,
+                kpass=K, conf=conf, per_step_us=prof["per_step"], cpu=cpu,
                 data="synthetic: KV/Q ~ N(0,1) (torch.randn, seeded); Poisson/uniform/geometric "
                      "events from the seeded simulator",
                 kpass_desc=f"second run of the same {K}-step event sequence")
@@ -635,19 +810,26 @@ def main():
     achieved = r["attn_bytes"] / (chunk_avg_ms * 1e-3) / 1e9 if chunk_n else 0.0
     sp = tl.get_score_path()
     score_kind = "mfma" if sp == 1 and D <= 128 else "valu"
-    metric = METRIC if args.config == 3 and not args.q_heads else \
-        f"decode attn+KV append µs/step and achieved HBM GB/s (% of peak), {conf['workload']}"
+    traffic, traffic_src = read_pmc(conf["workload"])
+    latency = args.config == 1
+    if args.config == 3 and not args.q_heads:
+        metric = METRIC
+    elif latency:
+        metric = f"decode attn+KV append latency µs/step, {conf['workload']}"
+    else:
+        metric = f"decode attn+KV append µs/step and achieved HBM GB/s (% of peak), {conf['workload']}"
     line = {
         "metric": metric,
-        "value": round(value, 2),
-        "unit": "GB/s",
+        "value": round(ms_per_step * 1e3, 2) if latency else round(value, 2),
+        "unit": "us" if latency else "GB/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "us_per_step": round(ms_per_step * 1e3, 2),
+        "achieved_gbps": round(value, 2),
         "frac_of_peak": round(value / HBM_PEAK_GBPS, 4),
-        "higher_is_better": True,
+        "higher_is_better": not latency,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
@@ -662,11 +844,25 @@ def main():
         "roofline": {"kernel": f"attn_decode_kernel<D={D},G={Hq // Hkv},{score_kind}>",
                      "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": read_pmc(conf["workload"])},
-        "cpu_baseline": None,
+                     "traffic": traffic,
+                     "traffic_source": (f"{traffic_src}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                                        "of this workload, calibrated by a 1 GiB copy; a committed "
+                                        "profile, not this run" if traffic_src else None)},
+        "cpu_baseline": r.get("cpu"),
+        "library": tl.loaded_path(),
+        "device": {"name": torch.cuda.get_device_properties(0).name,
+                   "cus": torch.cuda.get_device_properties(0).multi_processor_count,
+                   "host": os.uname().nodename},
     }
-    if args.cpu_baseline and args.config == 3 and not args.q_heads:
-        line["cpu_baseline"] = cpu_baseline(r["cfg"], args.cpu_seconds)
+    ps = r.get("per_step_us")
+    if ps is not None and len(ps):
+        line["step_us_stats"] = {"median": round(float(np.median(ps)), 2),
+                                 "min": round(float(ps.min()), 2),
+                                 "max": round(float(ps.max()), 2),
+                                 "source": ("the profiled run of the same event sequence, one "
+                                            "hipEvent per step" if args.config == 5 else
+                                            "separate pass of the same steps (lengths not "
+                                            "advanced), one hipEvent between steps")}
     print(json.dumps(line), flush=True)
 
 

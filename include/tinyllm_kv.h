@@ -121,7 +121,10 @@ int    tl_kv_free_blocks(const tl_kv_manager *mgr);
 /* Bytes of one block (all layers, K and V); 0 for other pools. */
 size_t tl_kv_block_bytes(const tl_kv_manager *mgr);
 /* Physical blocks of a sequence in token order: writes min(*n, mapped) ids
- * to out and sets *n to the number mapped. */
+ * to out and sets *n to the number mapped.  Block pools: ids of
+ * tl_kv_create_paged's layout; a block map over the slot pool
+ * (tl_kv_set_block_map): all max_seq_len/block_tokens ids of the sequence's
+ * slot, counted in blocks of block_tokens tokens from a layer's K base. */
 int tl_kv_block_table(const tl_kv_manager *mgr, int seq_id, int32_t *out, int *n);
 
 /* ------------------------------------------------------------------------

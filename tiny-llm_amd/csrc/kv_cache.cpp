@@ -356,9 +356,14 @@ size_t KVCacheManager::blockBytes() const noexcept {
 
 Result<std::vector<int32_t>> KVCacheManager::blockTable(int seq_id) const {
     using R = Result<std::vector<int32_t>>;
-    if (!blocks_) return R::err("blockTable: not a block pool");
     const int slot = slotOf(seq_id);
+    if (!blocks_ && block_map_host_.empty()) return R::err("blockTable: not a paged pool");
     if (slot < 0) return R::err("Sequence not found: " + std::to_string(seq_id));
+    if (!blocks_) { // block map over the slot pool: every block of the slot is mapped
+        const size_t per_slot = static_cast<size_t>(config_.max_seq_len / block_tokens_);
+        const auto   first = block_map_host_.begin() + static_cast<std::ptrdiff_t>(slot * per_slot);
+        return R::ok(std::vector<int32_t>(first, first + static_cast<std::ptrdiff_t>(per_slot)));
+    }
     const auto  &t = blocks_->table();
     const size_t base = static_cast<size_t>(slot) * static_cast<size_t>(blocks_->blocksPerRow());
     return R::ok(std::vector<int32_t>(t.begin() + static_cast<std::ptrdiff_t>(base),
