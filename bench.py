@@ -211,11 +211,15 @@ def cpu_baseline_churn(st, target_s: float):
     t_book, t_dec, dec_bytes, dec_steps, live_sampled = 0.0, 0.0, 0, 0, 0
     for ev in sim.events():
         t0 = time.perf_counter()
+        row = 0  # a step's arrivals take consecutive source rows, as on the GPU
         for prompt, life in zip(ev.arrivals, ev.lifetimes):
             sid, err = o.allocate(M)
             if err is not None:
                 continue
-            o.append(sid, 0, st["src_k"][:prompt], st["src_v"][:prompt], prompt)
+            if row + prompt > len(st["src_k"]):
+                row = 0
+            o.append(sid, 0, st["src_k"][row:row + prompt], st["src_v"][row:row + prompt], prompt)
+            row += prompt
             o.advance(sid, prompt)
             live[sid] = max(1, life)
             length[sid] = prompt
@@ -447,8 +451,10 @@ def churn(args, tl, torch, workloads, np):
     stream = torch.cuda.current_stream().cuda_stream
     gen = torch.Generator(device=dev)
     gen.manual_seed(workloads.seed(5, 1))
-    src_k = torch.randn((4096, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    src_v = torch.randn((4096, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    # prompt K/V: a step's arrivals take consecutive rows of these, from row 0
+    src_rows = 32768
+    src_k = torch.randn((src_rows, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    src_v = torch.randn((src_rows, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
     q = torch.randn((slots, Hq, D), generator=gen, device=dev, dtype=torch.float16)
     nk = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
     nv = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
@@ -459,13 +465,33 @@ def churn(args, tl, torch, workloads, np):
     else:
         mgr = tl.KVCacheManager(1, Hkv, D, M, slots)
     batch = tl.DecodeBatch(mgr, slots, Hq)
+    prompts_in = tl.PrefillBatch(mgr, slots, Hq)  # the batched append of a step's prompts
+
+    def append_prompts(new):
+        """The prompt K/V of a step's arrivals, (seq id, prompt) in arrival
+        order, appended with one launch per src_rows tokens: the bytes of
+        appendKV(seq, 0, rows, prompt) per arrival, then advanceSeqLen."""
+        i = 0
+        while i < len(new):
+            group, tok = [], 0
+            while i < len(new) and tok + new[i][1] <= src_rows:
+                group.append(new[i])
+                tok += new[i][1]
+                i += 1
+            prompts_in.prepare([g[0] for g in group], [g[1] for g in group], stream)
+            prompts_in.append(0, src_k.data_ptr(), src_v.data_ptr(), stream)
+            prompts_in.commit()
 
     def run(profile):
         sim = workloads.ChurnSim(hq=Hq, hkv=Hkv, head_dim=D, max_seq_len=M, slots=slots, **sim_args)
-        live = {}    # seq id -> remaining decode steps
-        length = {}  # seq id -> getSeqLen, tracked on the host side of the loop
+        events = list(sim.events())  # drawn before the clock starts
+        # live sequences in admission order: id, remaining decode steps, length
+        ids_a = np.zeros(slots, dtype=np.int32)
+        rem_a = np.zeros(slots, dtype=np.int64)
+        len_a = np.zeros(slots, dtype=np.int64)
+        n = 0
         nbytes, attn_nbytes, rejected, live_sum, peak = 0, 0, 0, 0, 0
-        preempted, used_sum, arrival = 0, 0, {}  # arrival: seq id -> admission order
+        preempted, used_sum = 0, 0
         if profile:
             tl.profile_reset()
             tl.profile_enable(True)
@@ -474,59 +500,60 @@ def churn(args, tl, torch, workloads, np):
         t0 = time.perf_counter()
         ev0.record()
         step_ev = []
-        for ev in sim.events():
+        for ev in events:
             if profile:
                 e = torch.cuda.Event(enable_timing=True)
                 e.record()
                 step_ev.append(e)
+            new, pending = [], 0  # admitted this step; blocks their prompts will map
             for prompt, life in zip(ev.arrivals, ev.lifetimes):
                 sid, err = mgr.allocateSequence(M)
-                if err is None and blocks and mgr.freeBlocks() < -(-prompt // bt) + len(live):
+                if err is None and blocks and mgr.freeBlocks() < pending + -(-prompt // bt) + n:
                     mgr.releaseSequence(sid)  # admit only with a block of headroom per live seq
                     err = "exhausted"
                 if err is not None:
                     rejected += 1
                     continue
-                assert mgr.appendKV(sid, 0, src_k.data_ptr(), src_v.data_ptr(), prompt, stream) is None
-                mgr.advanceSeqLen(sid, prompt)
-                arrival[sid] = len(arrival)
+                new.append((sid, prompt))
+                pending += -(-prompt // bt)
                 nbytes += 2 * prompt * Hkv * D * 2 * 2  # read + write of K and V
-                live[sid] = max(1, life)
-                length[sid] = prompt
+                ids_a[n], rem_a[n], len_a[n] = sid, max(1, life), prompt
+                n += 1
+            if new:
+                append_prompts(new)
             if blocks:
                 # A step opens a block for every sequence at a block boundary;
                 # when the pool cannot back them, the newest sequences are
                 # preempted (released) first.
-                need = sum(1 for s in live if length[s] % bt == 0)
-                while need > mgr.freeBlocks() and live:
-                    s = max(live, key=arrival.__getitem__)
-                    need -= 1 if length[s] % bt == 0 else 0
-                    del live[s]
-                    del length[s]
-                    assert mgr.releaseSequence(s) is None
+                need = int(np.count_nonzero(len_a[:n] % bt == 0))
+                while need > mgr.freeBlocks() and n:
+                    n -= 1
+                    need -= int(len_a[n] % bt == 0)
+                    assert mgr.releaseSequence(int(ids_a[n])) is None
                     preempted += 1
             used_sum += mgr.getUsedMemory()
-            ids = list(live)
-            if ids:
-                batch.prepare(ids, stream)
-                ctx = np.fromiter((length[s] for s in ids), dtype=np.int64, count=len(ids))
+            if n:
+                batch.prepare(ids_a[:n], stream)
                 batch.decode(0, q.data_ptr(), nk.data_ptr(), nv.data_ptr(), out.data_ptr(), scale,
                              stream)
                 batch.commit(1)
-                sb = workloads.step_bytes(ctx, Hq, Hkv, D)
+                sb = workloads.step_bytes(len_a[:n], Hq, Hkv, D)
                 if args.launch_log:
-                    log_launches(args.launch_log, 1, sb, len(ids))
+                    log_launches(args.launch_log, 1, sb, n)
                 nbytes += sb
                 attn_nbytes += sb
-            live_sum += len(ids)
-            peak = max(peak, len(ids))
-            for s in ids:
-                live[s] -= 1
-                length[s] += 1
-                if live[s] == 0 or length[s] >= M:
-                    del live[s]
-                    del length[s]
-                    assert mgr.releaseSequence(s) is None
+            live_sum += n
+            peak = max(peak, n)
+            rem_a[:n] -= 1
+            len_a[:n] += 1
+            fin = (rem_a[:n] == 0) | (len_a[:n] >= M)
+            if fin.any():
+                for s in ids_a[:n][fin]:
+                    assert mgr.releaseSequence(int(s)) is None
+                keep = ~fin
+                k = int(np.count_nonzero(keep))
+                ids_a[:k], rem_a[:k], len_a[:k] = ids_a[:n][keep], rem_a[:n][keep], len_a[:n][keep]
+                n = k
         ev1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
@@ -536,8 +563,8 @@ def churn(args, tl, torch, workloads, np):
             step_ev.append(ev1)
             per_step = np.array([step_ev[i].elapsed_time(step_ev[i + 1])
                                  for i in range(len(step_ev) - 1)]) * 1e3
-        for s in list(live):
-            mgr.releaseSequence(s)
+        for s in ids_a[:n]:
+            mgr.releaseSequence(int(s))
         ks = None
         if profile:
             tl.profile_enable(False)

@@ -529,7 +529,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     extern __shared__ __align__(16) char smem[];
 
     const int       lane = threadIdx.x & 63;
-    const int       wave = threadIdx.x >> 6;
+    const int       wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: scalar tile math
     const AttnPlan &pl = a.plan;
     // 1-D grid, kv head fastest: the Hkv workgroups reading the pieces of the
     // same token rows are dispatched together.

@@ -51,6 +51,46 @@ __global__ __launch_bounds__(kCopyThreads) void kv_append_kernel(AppendArgs a) {
     *reinterpret_cast<uint4 *>(const_cast<__half *>(a.view.v_base) + dst) = v;
 }
 
+// Token ranges of one append launch: range r writes rows tok0[r] ..
+// tok0[r+1]-1 of new_k/new_v (counted from src_tok) to cache row row[r] at
+// positions pos0[r], pos0[r]+1, ...  The table travels in the kernel
+// arguments, so the launch needs no metadata copy.
+constexpr int kAppendRanges = 64;
+constexpr int kAppendTokens = 32768; // tokens per launch (grid y)
+struct RangeArgs {
+    KvView        view;
+    int           n;
+    int           row_pieces;
+    int64_t       src_tok;
+    const __half *new_k;
+    const __half *new_v;
+    int32_t       row[kAppendRanges];
+    int32_t       pos0[kAppendRanges];
+    int32_t       tok0[kAppendRanges + 1];
+};
+
+// grid (ceil(row_pieces/256), tokens of the launch): one token row per block
+// row, the bytes of appendKV (kv_cache.cpp:226-233) for every range.
+__global__ __launch_bounds__(kCopyThreads) void kv_append_ranges_kernel(RangeArgs a) {
+    const int piece = blockIdx.x * kCopyThreads + threadIdx.x;
+    if (piece >= a.row_pieces) return;
+    const int t = blockIdx.y;
+    int       r = 0; // the range holding token t (uniform over the block)
+    while (r + 1 < a.n && a.tok0[r + 1] <= t) ++r;
+    const int     pos = a.pos0[r] + (t - a.tok0[r]);
+    const int64_t blk =
+        a.view.block_table
+            ? (int64_t)a.view.block_table[(int64_t)a.row[r] * a.view.bt_stride + (pos >> a.view.log2_blk)]
+            : (int64_t)a.row[r];
+    const int64_t dst = blk * a.view.blk_stride +
+                        (int64_t)(pos & ((1 << a.view.log2_blk) - 1)) * a.view.tok_stride + (int64_t)piece * 8;
+    const int64_t src = (a.src_tok + t) * (int64_t)a.row_pieces * 8 + (int64_t)piece * 8;
+    const uint4   k = *reinterpret_cast<const uint4 *>(a.new_k + src);
+    const uint4   v = *reinterpret_cast<const uint4 *>(a.new_v + src);
+    *reinterpret_cast<uint4 *>(const_cast<__half *>(a.view.k_base) + dst) = k;
+    *reinterpret_cast<uint4 *>(const_cast<__half *>(a.view.v_base) + dst) = v;
+}
+
 struct GatherArgs {
     KvView         view;
     const int32_t *lens;
@@ -130,6 +170,44 @@ void launch_kv_append(const KvView &view, int64_t layer_stride, const int32_t *w
     hipLaunchKernelGGL(kv_append_kernel, grid, dim3(kCopyThreads), 0, stream, a);
     HIP_CHECK(hipGetLastError());
     profile_end(KernelId::KvAppend, stream);
+}
+
+void launch_kv_append_ranges(const KvView &view, const int32_t *rows, const int32_t *pos0,
+                             const int32_t *counts, int n, int row_elems, const __half *new_k,
+                             const __half *new_v, hipStream_t stream) {
+    RangeArgs a;
+    a.view = view;
+    a.row_pieces = row_elems / 8;
+    a.new_k = new_k;
+    a.new_v = new_v;
+    a.n = 0;
+    a.tok0[0] = 0;
+    int64_t done = 0; // tokens of earlier launches
+    auto flush = [&]() {
+        if (a.n == 0) return;
+        dim3 grid((unsigned)((a.row_pieces + kCopyThreads - 1) / kCopyThreads), (unsigned)a.tok0[a.n]);
+        a.src_tok = done;
+        profile_begin(KernelId::KvAppend, stream);
+        hipLaunchKernelGGL(kv_append_ranges_kernel, grid, dim3(kCopyThreads), 0, stream, a);
+        HIP_CHECK(hipGetLastError());
+        profile_end(KernelId::KvAppend, stream);
+        done += a.tok0[a.n];
+        a.n = 0;
+        a.tok0[0] = 0;
+    };
+    for (int i = 0; i < n; ++i) {
+        int off = 0; // a range longer than a launch holds continues in the next
+        while (off < counts[i]) {
+            if (a.n == kAppendRanges || a.tok0[a.n] == kAppendTokens) flush();
+            const int take = std::min(counts[i] - off, kAppendTokens - a.tok0[a.n]);
+            a.row[a.n] = rows[i];
+            a.pos0[a.n] = pos0[i] + off;
+            a.tok0[a.n + 1] = a.tok0[a.n] + take;
+            ++a.n;
+            off += take;
+        }
+    }
+    flush();
 }
 
 void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int uniform_len, int n,

@@ -107,6 +107,15 @@ void launch_kv_append(const KvView &view, int64_t layer_stride, const int32_t *w
                       int n, int num_layers, int row_elems, const __half *new_k,
                       const __half *new_v, hipStream_t stream);
 
+// Multi-token append of n sequences for one layer: sequence i's counts[i]
+// token rows ([Hkv][D] contiguous) follow those of sequences 0..i-1 in
+// new_k/new_v and go to cache row rows[i] (view.seq_row is not read) at
+// positions pos0[i], pos0[i]+1, ...  rows/pos0/counts are host memory: they
+// travel in kernel arguments (no metadata copy).
+void launch_kv_append_ranges(const KvView &view, const int32_t *rows, const int32_t *pos0,
+                             const int32_t *counts, int n, int row_elems, const __half *new_k,
+                             const __half *new_v, hipStream_t stream);
+
 // out[b][g][t][:] = cache(b, g, t) for t < lens[b] (lens NULL: uniform_len),
 // +0.0 for lens[b] <= t < s_max.  which: 0 = K, 1 = V.
 void launch_kv_gather(const KvView &view, int which, const int32_t *lens, int uniform_len, int n,

@@ -490,7 +490,17 @@ Result<std::unique_ptr<DecodeBatch>> DecodeBatch::create(KVCacheManager &mgr, in
     if (!detail::attn_shape_supported(cfg.head_dim, num_q_heads / cfg.num_heads))
         return R::err("DecodeBatch: unsupported head_dim/group (head_dim in {32,64,128,256}, "
                       "num_q_heads/num_heads in {1,2,4,8})");
-    return R::ok(std::unique_ptr<DecodeBatch>(new DecodeBatch(mgr, max_seqs, num_q_heads)));
+    std::unique_ptr<DecodeBatch> batch(new DecodeBatch(mgr, max_seqs, num_q_heads));
+    // Size the metadata ring for a full batch now, so that no step allocates
+    // pinned or device memory: 4 words per entry and 2 per work item, with at
+    // most one item per entry plus 2 per resident workgroup slot (the planner
+    // never splits finer than the slots need), 4 MiB at most.
+    const size_t slots = 2 * static_cast<size_t>(detail::kPlanSlotsPerCU) *
+                         static_cast<size_t>(detail::device_cus());
+    const size_t n = static_cast<size_t>(max_seqs);
+    const size_t words = 4 * n + 1 + 2 * (n + slots);
+    batch->meta_->reserve(std::min<size_t>(words * 4, size_t(4) << 20));
+    return R::ok(std::move(batch));
 }
 
 Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n, bool appendable,
@@ -764,10 +774,12 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
     n_items_ = 0;
     max_keys_ = 0;
     d_work_ = nullptr;
-    d_tok_row_ = nullptr;
-    d_tok_pos_ = nullptr;
+    uploaded_ = false;
     ids_.clear();
     counts_.clear();
+    slots_.clear();
+    pos0_.clear();
+    work_.clear();
     if (n < 0 || n > max_seqs_)
         return Result<void>::err("PrefillBatch: n=" + std::to_string(n) + " outside [0, " +
                                  std::to_string(max_seqs_) + "]");
@@ -808,26 +820,11 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
         if (r.isErr()) return r;
         mgr_.syncTable(stream);
     }
-    std::vector<int32_t> work;
-    detail::plan_prefill(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads, work);
-    // Device copy: [work items (8 words each, first: 32-byte aligned) |
-    // token rows T | token positions T].
-    const size_t T = static_cast<size_t>(total);
-    const size_t words = work.size() + 2 * T;
-    int32_t     *h = static_cast<int32_t *>(meta_->begin(words * 4));
-    if (!work.empty()) std::memcpy(h, work.data(), work.size() * 4);
-    int32_t *rows = h + work.size(), *pos = rows + T;
-    size_t   k = 0;
-    for (int i = 0; i < n; ++i)
-        for (int j = 0; j < num_tokens[i]; ++j, ++k) {
-            rows[k] = slots[static_cast<size_t>(i)];
-            pos[k] = entries[static_cast<size_t>(i)].p0 + j;
-        }
-    const int32_t *d = static_cast<const int32_t *>(meta_->commit(stream));
-    d_work_ = d;
-    d_tok_row_ = d + work.size();
-    d_tok_pos_ = d_tok_row_ + T;
-    n_items_ = static_cast<int>(work.size() / detail::kPrefillItemWords);
+    detail::plan_prefill(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads, work_);
+    n_items_ = static_cast<int>(work_.size() / detail::kPrefillItemWords);
+    slots_ = std::move(slots);
+    pos0_.resize(static_cast<size_t>(n));
+    for (int i = 0; i < n; ++i) pos0_[static_cast<size_t>(i)] = entries[static_cast<size_t>(i)].p0;
     ids_.assign(seq_ids, seq_ids + n);
     counts_.assign(num_tokens, num_tokens + n);
     n_ = n;
@@ -844,17 +841,20 @@ Result<void> PrefillBatch::append(int layer_idx, const half *new_k, const half *
     if (layer_idx < 0 || layer_idx >= cfg.num_layers)
         return Result<void>::err("PrefillBatch: Invalid layer_idx: " + std::to_string(layer_idx));
     if (tokens_ == 0) return Result<void>::ok();
-    const int row = cfg.num_heads * cfg.head_dim;
-    // The append kernel's grid holds one token per y index (< 65536).
-    constexpr int kMaxY = 32768;
-    for (int t0 = 0; t0 < tokens_; t0 += kMaxY) {
-        const int nt = std::min(kMaxY, tokens_ - t0);
-        KvView    v = mgr_.layerView(layer_idx, d_tok_row_ + t0);
-        detail::launch_kv_append(v, 0, d_tok_pos_ + t0, 0, nt, 1, row,
-                                 new_k + static_cast<size_t>(t0) * row,
-                                 new_v + static_cast<size_t>(t0) * row, stream);
-    }
+    // Ranges (slot, write position, tokens) travel in kernel arguments.
+    detail::launch_kv_append_ranges(mgr_.layerView(layer_idx, nullptr), slots_.data(), pos0_.data(),
+                                    counts_.data(), n_, cfg.num_heads * cfg.head_dim, new_k, new_v,
+                                    stream);
     return Result<void>::ok();
+}
+
+void PrefillBatch::upload_device(hipStream_t stream) {
+    if (uploaded_) return;
+    // [work items (8 words each, the first 32-byte aligned)]
+    int32_t *h = static_cast<int32_t *>(meta_->begin(std::max<size_t>(work_.size(), 1) * 4));
+    if (!work_.empty()) std::memcpy(h, work_.data(), work_.size() * 4);
+    d_work_ = static_cast<const int32_t *>(meta_->commit(stream));
+    uploaded_ = true;
 }
 
 Result<void> PrefillBatch::attention(int layer_idx, const half *q, half *out, float scale,
@@ -879,6 +879,7 @@ Result<void> PrefillBatch::launch(int layer_idx, const half *q, const half *new_
          reinterpret_cast<uintptr_t>(new_k) | reinterpret_cast<uintptr_t>(new_v)) & 15u)
         return Result<void>::err("PrefillBatch: q, out, new_k and new_v must be 16-byte aligned");
     if (n_items_ == 0) return Result<void>::ok();
+    upload_device(stream);
     detail::PrefillLaunch p;
     p.q = q;
     p.out = out;

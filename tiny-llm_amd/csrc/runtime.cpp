@@ -88,6 +88,10 @@ int device_cus() {
 MetaRing::MetaRing(int slots) : slots_(static_cast<size_t>(slots)) {}
 
 MetaRing::~MetaRing() {
+    // kernels queued on callers' streams may still read the device slots
+    (void)hipDeviceSynchronize();
+    for (void *p : retired_dev_) (void)hipFree(p);
+    for (void *p : retired_host_) (void)hipHostFree(p);
     for (auto &s : slots_) {
         if (s.ev) {
             (void)hipEventSynchronize(s.ev);
@@ -106,23 +110,35 @@ void *MetaRing::begin(size_t bytes) {
         s.pending = false;
     }
     if (bytes == 0) bytes = 16;
-    if (s.cap < bytes) {
-        size_t cap = 4096;
-        while (cap < bytes) cap <<= 1;
-        if (s.host) HIP_CHECK(hipHostFree(s.host));
-        if (s.dev) {
-            HIP_CHECK(hipDeviceSynchronize()); // kernels may still read the old slot
-            HIP_CHECK(hipFree(s.dev));
-        }
-        s.host = nullptr;
-        s.dev = nullptr;
-        HIP_CHECK(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
-        HIP_CHECK(hipMalloc(&s.dev, cap));
-        s.cap = cap;
-    }
+    if (s.cap < bytes) grow(s, bytes);
     if (!s.ev) HIP_CHECK(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
     bytes_ = bytes;
     return s.host;
+}
+
+void MetaRing::grow(Slot &s, size_t bytes) {
+    size_t cap = 4096;
+    while (cap < bytes) cap <<= 1;
+    void *host = nullptr, *dev = nullptr;
+    HIP_CHECK(hipHostMalloc(&host, cap, hipHostMallocDefault));
+    HIP_CHECK(hipMalloc(&dev, cap));
+    // The old host buffer is idle (its copy completed: begin() waited on the
+    // slot's event); the old device buffer may still be read by queued kernels.
+    if (s.host) retired_host_.push_back(s.host);
+    if (s.dev) retired_dev_.push_back(s.dev);
+    s.host = host;
+    s.dev = dev;
+    s.cap = cap;
+}
+
+void MetaRing::reserve(size_t bytes) {
+    for (auto &s : slots_) {
+        if (s.pending) {
+            HIP_CHECK(hipEventSynchronize(s.ev));
+            s.pending = false;
+        }
+        if (s.cap < bytes) grow(s, bytes);
+    }
 }
 
 void *MetaRing::commit(hipStream_t stream) {
@@ -135,21 +151,22 @@ void *MetaRing::commit(hipStream_t stream) {
 
 // --------------------------------------------------------------- Workspace
 Workspace::~Workspace() {
+    if (!retired_.empty()) (void)hipDeviceSynchronize();
+    for (float *p : retired_) (void)hipFree(p);
     if (ptr_) (void)hipFree(ptr_);
 }
 
 float *Workspace::get(size_t floats) {
     if (floats == 0) return ptr_;
     if (floats > cap_) {
-        if (ptr_) {
-            HIP_CHECK(hipDeviceSynchronize());
-            HIP_CHECK(hipFree(ptr_));
-            ptr_ = nullptr;
-            cap_ = 0;
-        }
         size_t cap = 1 << 16;
         while (cap < floats) cap <<= 1;
-        HIP_CHECK(hipMalloc(&ptr_, cap * sizeof(float)));
+        float *p = nullptr;
+        HIP_CHECK(hipMalloc(&p, cap * sizeof(float)));
+        // kernels queued earlier may still use the old buffer: keep it until
+        // the workspace goes (grow-only doubling keeps the total below 2x)
+        if (ptr_) retired_.push_back(ptr_);
+        ptr_ = p;
         cap_ = cap;
     }
     return ptr_;
@@ -183,6 +200,10 @@ ProfState &prof() {
     static ProfState p;
     return p;
 }
+// Timing-only events: without the system-scope fence a record does not
+// write back and invalidate the caches, which would stretch the kernel it
+// brackets.
+constexpr unsigned kTimingEventFlags = hipEventDisableSystemFence;
 } // namespace
 
 void profile_begin(KernelId id, hipStream_t stream) {
@@ -190,7 +211,7 @@ void profile_begin(KernelId id, hipStream_t stream) {
     if (!p.on.load(std::memory_order_relaxed)) return;
     std::lock_guard<std::mutex> lk(p.mu);
     hipEvent_t                  e;
-    HIP_CHECK(hipEventCreate(&e));
+    HIP_CHECK(hipEventCreateWithFlags(&e, kTimingEventFlags));
     HIP_CHECK(hipEventRecord(e, stream));
     p.open[static_cast<size_t>(id)] = e;
 }
@@ -202,7 +223,7 @@ void profile_end(KernelId id, hipStream_t stream) {
     hipEvent_t                  start = p.open[static_cast<size_t>(id)];
     if (!start) return;
     hipEvent_t e;
-    HIP_CHECK(hipEventCreate(&e));
+    HIP_CHECK(hipEventCreateWithFlags(&e, kTimingEventFlags));
     HIP_CHECK(hipEventRecord(e, stream));
     p.done[static_cast<size_t>(id)].emplace_back(start, e);
     p.open[static_cast<size_t>(id)] = nullptr;

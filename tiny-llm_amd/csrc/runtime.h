@@ -16,7 +16,9 @@ namespace detail {
 // stream and returns the device copy.  A slot is rewritten only after its
 // previous copy has completed (event), so the host never overwrites bytes a
 // pending copy still reads; kernels that read a device slot are ordered
-// before its next copy by the stream.
+// before its next copy by the stream.  (A copy on a separate stream, to
+// overlap the previous step's kernels, ran as a blit kernel reading host
+// memory next to the attention kernel and slowed it by more than it hid.)
 class MetaRing {
   public:
     explicit MetaRing(int slots = 4);
@@ -26,6 +28,9 @@ class MetaRing {
 
     void *begin(size_t bytes);
     void *commit(hipStream_t stream);
+    // Sizes every slot for `bytes` now, so steps up to that size never
+    // allocate.
+    void reserve(size_t bytes);
 
   private:
     struct Slot {
@@ -35,9 +40,14 @@ class MetaRing {
         hipEvent_t ev = nullptr;
         bool       pending = false;
     };
+    void              grow(Slot &s, size_t bytes);
     std::vector<Slot> slots_;
-    int               cur_ = -1;
-    size_t            bytes_ = 0;
+    // Buffers replaced by a larger one: kernels queued earlier may still read
+    // a device buffer, so they are freed with the ring, not at growth (a free
+    // would synchronise the device in the middle of a step).
+    std::vector<void *> retired_dev_, retired_host_;
+    int                 cur_ = -1;
+    size_t              bytes_ = 0;
 };
 
 // Grow-only device buffer (split-K partials).
@@ -50,8 +60,9 @@ class Workspace {
     float *get(size_t floats);
 
   private:
-    float *ptr_ = nullptr;
-    size_t cap_ = 0;
+    float              *ptr_ = nullptr;
+    size_t              cap_ = 0;
+    std::vector<float *> retired_; // replaced buffers, freed with the workspace
 };
 
 // Staging + workspace of the stateless entry points, one per device.

@@ -252,6 +252,9 @@ class PrefillBatch {
     PrefillBatch(KVCacheManager &mgr, int max_seqs, int num_q_heads);
     Result<void> launch(int layer_idx, const half *q, const half *new_k, const half *new_v, half *out,
                         float scale, hipStream_t stream);
+    // Device copy of the attention work list, made on the first launch that
+    // reads it (append() needs none).
+    void upload_device(hipStream_t stream);
 
     KVCacheManager      &mgr_;
     int                  max_seqs_;
@@ -260,9 +263,10 @@ class PrefillBatch {
     int                  tokens_ = 0;
     int                  n_items_ = 0;
     int                  max_keys_ = 0;
-    std::vector<int32_t> ids_, counts_;
+    std::vector<int32_t> ids_, counts_, slots_, pos0_, work_;
+    bool                 uploaded_ = false;
     std::unique_ptr<detail::MetaRing> meta_;
-    const int32_t       *d_tok_row_ = nullptr, *d_tok_pos_ = nullptr, *d_work_ = nullptr;
+    const int32_t       *d_work_ = nullptr;
 };
 
 } // namespace tiny_llm

@@ -181,6 +181,10 @@ def _check(rc: int) -> None:
 
 
 def _int_array(vals):
+    """A C int array for the C ABI: a C-contiguous int32 numpy array is
+    passed by address (no copy); anything else is copied."""
+    if type(vals).__name__ == "ndarray" and vals.dtype.str == "<i4" and vals.flags.c_contiguous:
+        return (vals.ctypes.data if vals.size else None), int(vals.size)
     vals = list(vals)
     return (C.c_int * max(1, len(vals)))(*vals), len(vals)
 
