@@ -366,6 +366,9 @@ typedef struct tl_attn_plan_info {
     int any_empty;     /* some sequence attends to zero tokens */
     int max_len;       /* longest attended length */
     int inline_words;  /* metadata words in the kernel arguments, -1: device copy */
+    int inline_compact;/* 1: the compact encoding (one chunk per sequence; 16-bit
+                          lengths and slots: one word per sequence + 16 bits
+                          per work item) */
 } tl_attn_plan_info;
 int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
                  int waves_setting, int with_rows, tl_attn_plan_info *info, int32_t *part_base,

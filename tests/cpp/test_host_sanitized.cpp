@@ -35,7 +35,7 @@ static void planner_random() {
         const int kind = it % 4;
         for (auto &l : lens) {
             if (kind == 0) l = (int32_t)(rng() % 65536);
-            else if (kind == 1) l = (int32_t)(rng() % 3);
+            else if (kind == 1) l = (int32_t)(1 + rng() % 300);
             else if (kind == 2) l = 8193;
             else l = (int32_t)(rng() % 40000);
         }
@@ -60,11 +60,26 @@ static void planner_random() {
         }
         for (int s : seen) CHECK(s == 1);
         InlineMeta m;
-        const bool fits = pack_inline(n ? lens.data() : nullptr, wl, n ? lens.data() : nullptr, n, m);
-        CHECK(fits == (n > 0 && inline_words(wl, n, true) <= kInlineWords));
-        if (fits) {
-            CHECK(m.off_rows + n <= kInlineWords);
+        std::vector<int32_t> rows((size_t)n);
+        for (int i = 0; i < n; ++i) rows[(size_t)i] = (int32_t)(rng() % 1300);
+        const bool full = n > 0 && inline_words(wl, n, true) <= kInlineWords;
+        const int  cw = n ? inline_words_compact(lens.data(), wl, rows.data(), n) : -1;
+        const bool fits = pack_inline(n ? lens.data() : nullptr, wl, n ? rows.data() : nullptr, n, m);
+        CHECK(fits == (full || (cw > 0 && cw <= kInlineWords)));
+        if (fits && !m.compact) {
+            CHECK(full && m.off_rows + n <= kInlineWords);
             CHECK(std::equal(lens.begin(), lens.end(), m.w));
+            CHECK(std::equal(rows.begin(), rows.end(), m.w + m.off_rows));
+        }
+        if (fits && m.compact) { // decode as the kernel does
+            CHECK(!full && !wl.any_multi && !wl.any_empty && wl.n_work == n);
+            for (int k = 0; k < n; ++k) {
+                const uint32_t ord = (uint32_t)m.w[m.off_work + (k >> 1)];
+                const int      e = (int)((ord >> ((k & 1) * 16)) & 0xffffu);
+                CHECK(e == wl.work[2 * (size_t)k] && wl.work[2 * (size_t)k + 1] == 0);
+                CHECK((int)((uint32_t)m.w[e] & 0xffffu) == lens[(size_t)e]);
+                CHECK((int)((uint32_t)m.w[e] >> 16) == rows[(size_t)e]);
+            }
         }
         const int nw = plan_waves((int64_t)wl.n_work * hkv, cus, 0);
         CHECK(nw == 4 || nw == 8);

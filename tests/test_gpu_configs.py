@@ -5,7 +5,7 @@ The bench times the decode kernel on plans that small tests do not reach:
 cfg3's 8448-token chunks (17 tiles per wave of an 8-wave workgroup), cfg2's
 4096-token chunks, cfg4's 3328-token chunks over a permuted 16-token block
 map of a pool larger than 4 GiB, cfg5's ~4600-token chunks over a block pool
-with hundreds of group-8 sequences and the metadata in a device copy.  Each
+with hundreds of group-8 sequences and the compact metadata encoding.  Each
 test builds that state through appendKV, asserts the plan the bench reports
 (DecodeBatch.info and tl_attn_plan), runs the decode step (fused append +
 attention, the bench's call), and checks
@@ -282,7 +282,8 @@ def test_cfg5_block_pool_500_live_group8(tl, orc):
     (group 8), D=128, prompts U{256..4096} plus up to 600 decoded tokens, on a
     16-token block pool whose blocks interleave across sequences (prompts
     appended in 512-token rounds), max_seq_len 5120; the step's metadata
-    exceeds the kernel-argument limit and travels through the device copy."""
+    travels in the kernel arguments in the compact encoding (one word per
+    sequence, 16 bits per work item)."""
     Hq, Hkv, D, M, bt, n = 64, 8, 128, 5120, 16, 520
     rng = np.random.default_rng(workloads.seed(5, 3))
     ctx = rng.integers(256, 4097, n) + rng.integers(0, 601, n)
@@ -316,7 +317,8 @@ def test_cfg5_block_pool_500_live_group8(tl, orc):
     info = batch.info()
     plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus())
     assert info["chunk_tokens"] == plan["chunk_tokens"] and info["work_items"] == plan["work_items"]
-    assert plan["waves"] == 4 and plan["inline_words"] == -1
+    # 520 entries of one chunk each: the compact kernel-argument metadata
+    assert plan["waves"] == 4 and plan["inline_compact"] == 1 and plan["inline_words"] == 780
     assert plan["chunk_tokens"] >= 4096  # the long-chunk plan of the benchmark
     q, nk, nv = randn(gen, (n, Hq, D)), randn(gen, (n, Hkv * D)), randn(gen, (n, Hkv * D))
     out = empty_dev((n, Hq, D))

@@ -172,3 +172,58 @@ def test_decode_long_chunks_all_shapes(tl, orc, score_path, waves, monkeypatch, 
         batch.gather(0, gk.data_ptr(), gv.data_ptr(), smax, stream())
         assert np.array_equal(to_host(gk), orc.gather(view, 0, lens, Hkv, D, smax))
         assert np.array_equal(to_host(gv), orc.gather(view, 1, lens, Hkv, D, smax))
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("D,G", [(128, 4), (128, 8), (64, 2), (256, 1)])
+@pytest.mark.parametrize("path", [0, 3])
+def test_decode_compact_metadata(tl, orc, score_path, path, D, G, paged):
+    """Batches of 400 sequences that stay one work item each carry their
+    metadata in the compact encoding (16-bit length and slot per sequence,
+    16-bit launch order): 400 + 200 words instead of 2001.  Slots are taken
+    out of order (every other one released first), so slot != entry index."""
+    score_path(path)
+    rng = np.random.default_rng(9100 + D + G + (50 if paged else 0) + path)
+    Hkv, M, n = 2, 320, 400
+    Hq = Hkv * G
+    slots = 2 * n
+    g = tl.KVCacheManager(1, Hkv, D, M, slots)
+    o = orc.KVCacheOracle(1, Hkv, D, M, slots)
+    if paged:
+        assert g.setBlockMap(16, rng.permutation(slots * (M // 16)).astype(np.int32)) is None
+    sids = [g.allocateSequence(M)[0] for _ in range(slots)]
+    for _ in range(slots):
+        o.allocate(M)
+    for s in sids[::2]:  # free every other slot; the batch uses the rest
+        assert g.releaseSequence(s) is None and o.release(s) is None
+    ids = sids[1::2]
+    lens = rng.integers(1, M - 8, n)
+    keep = []
+    for s, S in zip(ids, lens):
+        k, v = f16bits(rng, int(S) * Hkv * D), f16bits(rng, int(S) * Hkv * D)
+        dk, dv = to_dev(k), to_dev(v)
+        keep += [dk, dv]
+        assert g.appendKV(s, 0, dk.data_ptr(), dv.data_ptr(), int(S), stream()) is None
+        o.append(s, 0, k, v, int(S))
+        g.advanceSeqLen(s, int(S))
+        o.advance(s, int(S))
+    plan = tl.attn_plan((lens + 1).astype(np.int32), Hkv,
+                        num_cus=__import__("torch").cuda.get_device_properties(0).multi_processor_count)
+    assert plan["inline_compact"] == 1 and plan["work_items"] == n
+    batch = tl.DecodeBatch(g, n, Hq)
+    batch.prepare(ids, stream())
+    q = f16bits(rng, (n, Hq, D))
+    nk, nv = f16bits(rng, (n, Hkv * D)), f16bits(rng, (n, Hkv * D))
+    dq, dnk, dnv = to_dev(q), to_dev(nk), to_dev(nv)
+    out = empty_dev((n, Hq, D))
+    scale = 1.0 / np.sqrt(D)
+    batch.decode(0, dq.data_ptr(), dnk.data_ptr(), dnv.data_ptr(), out.data_ptr(), scale, stream())
+    for i, s in enumerate(ids):
+        o.append(s, 0, nk[i], nv[i], 1)
+    if not paged:
+        assert np.array_equal(read_dev(g.pool(), o.pool().size), o.pool())
+    view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(s) for s in ids])
+    ref32, _ = orc.attn_decode_gqa(q, view, lens + 1, Hq, Hkv, D, scale, nthreads=8)
+    got = to_host(out).view(np.float16).astype(np.float32)
+    errs = [rel_err(got[i], ref32[i]) for i in range(n)]
+    assert max(errs) <= 1e-3, max(errs)

@@ -56,8 +56,10 @@ EXPECTED = {
     # cfg4: lognormal lengths up to 27370 split into 3328-token chunks
     "cfg4": dict(chunk_tokens=3328, work_items=195, waves=4, any_multi=1, inline_words=775),
     # cfg5: ~585 live sequences: one chunk each (the longest, 4601 tokens,
-    # rounded up), metadata through a device copy
-    "cfg5": dict(chunk_tokens=4608, work_items=585, waves=4, any_multi=0, inline_words=-1),
+    # rounded up); the full metadata (2926 words) would need a device copy,
+    # the compact encoding fits: 585 + 293 words
+    "cfg5": dict(chunk_tokens=4608, work_items=585, waves=4, any_multi=0, inline_words=878,
+                 inline_compact=1),
 }
 
 
@@ -154,11 +156,22 @@ def test_waves_setting_and_empty_sequences(tl):
 
 def test_inline_metadata_limit(tl):
     """896 words travel in the kernel arguments: lens n, part_base n+1, the
-    work list 2 per item, the slot row n."""
+    work list 2 per item, the slot row n -- or, when every sequence is one
+    work item, the compact encoding: one word per sequence (16-bit length and
+    slot) and 16 bits per work item."""
     fits = np.full(223, 100, dtype=np.int32)      # 223 + 224 + 446 + 0 = 893
     p = tl.attn_plan(fits, 8, num_cus=CUS, with_rows=False)
-    assert p["inline_words"] == 893
-    assert tl.attn_plan(fits, 8, num_cus=CUS, with_rows=True)["inline_words"] == -1
+    assert (p["inline_words"], p["inline_compact"]) == (893, 0)
+    p = tl.attn_plan(fits, 8, num_cus=CUS, with_rows=True)  # 1116 full words
+    assert (p["inline_words"], p["inline_compact"]) == (223 + 112, 1)
+    big = np.full(597, 100, dtype=np.int32)       # 597 + 299 = 896: the most that fits
+    assert tl.attn_plan(big, 8, num_cus=CUS)["inline_words"] == 896
+    assert tl.attn_plan(np.full(598, 100, np.int32), 8, num_cus=CUS)["inline_words"] == -1
+    split = np.array([30000] + [100] * 300, dtype=np.int32)  # a split sequence: full only
+    p = tl.attn_plan(split, 8, num_cus=CUS)
+    assert p["any_multi"] == 1 and (p["inline_words"], p["inline_compact"]) == (-1, 0)
+    long_ = np.full(300, 70000, dtype=np.int32)   # lengths beyond 16 bits: full only
+    assert tl.attn_plan(long_, 1, num_cus=CUS, forced_chunk=70144)["inline_compact"] == 0
 
 
 def test_plan_rejects_bad_arguments(tl):

@@ -98,11 +98,40 @@ int inline_words(const WorkList &plan, int n, bool with_rows) {
     return n + (n + 1) + 2 * plan.n_work + (with_rows ? n : 0);
 }
 
+int inline_words_compact(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n) {
+    if (n <= 0 || n > 0xffff || plan.any_multi || plan.any_empty || plan.n_work != n) return -1;
+    for (int i = 0; i < n; ++i) {
+        if (lens[i] < 0 || lens[i] > 0xffff) return -1;
+        const int r = rows ? rows[i] : i;
+        if (r < 0 || r > 0xffff) return -1;
+    }
+    return n + (n + 1) / 2;
+}
+
 bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
                  InlineMeta &out) {
     const int words = inline_words(plan, n, rows != nullptr);
-    if (n <= 0 || words > kInlineWords) return false;
+    if (n > 0 && words > kInlineWords) {
+        const int cw = inline_words_compact(lens, plan, rows, n);
+        if (cw < 0 || cw > kInlineWords) return false;
+        out.n = n;
+        out.compact = 1;
+        out.has_rows = 1;
+        out.off_part = 0;
+        out.off_rows = 0;
+        out.off_work = n;
+        for (int i = 0; i < n; ++i)
+            out.w[i] = (int32_t)((uint32_t)lens[i] | ((uint32_t)(rows ? rows[i] : i) << 16));
+        for (int k = 0; k < (n + 1) / 2; ++k) out.w[n + k] = 0;
+        for (int k = 0; k < n; ++k) {
+            const uint32_t e = (uint32_t)plan.work[2 * (size_t)k]; // chunk 0 of entry e
+            out.w[n + k / 2] = (int32_t)((uint32_t)out.w[n + k / 2] | (e << ((k & 1) * 16)));
+        }
+        return true;
+    }
+    if (n <= 0) return false;
     out.n = n;
+    out.compact = 0;
     out.has_rows = rows ? 1 : 0;
     out.off_part = n;
     out.off_work = 2 * n + 1;

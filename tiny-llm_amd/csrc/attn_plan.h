@@ -51,9 +51,13 @@ int plan_waves(int64_t workgroups, int cus, int setting);
 int chunk_override_from_env();
 
 // Plan metadata small enough to travel in the kernel arguments, so that a
-// launch needs no separate host-to-device copy.  Words:
+// launch needs no separate host-to-device copy.  Full encoding, words:
 //   [lens n | part_base n+1 | work 2*n_work | rows n (if has_rows)]
 // rows[b] is the cache row (slot) of entry b, replacing KvView::seq_row.
+// Compact encoding (compact = 1), for plans where every entry is one work
+// item (no split, no empty entry) and lengths and rows fit in 16 bits:
+//   [len_b | row_b << 16, n words | launch order of the entries, 16 bits each]
+// -- n + ceil(n/2) words, so up to 597 entries fit instead of 223.
 constexpr int kInlineWords = 896;
 struct InlineMeta {
     int32_t n = 0; // entries; 0 = metadata comes through the AttnPlan pointers
@@ -61,11 +65,15 @@ struct InlineMeta {
     int32_t off_part = 0;
     int32_t off_work = 0;
     int32_t off_rows = 0;
+    int32_t compact = 0;
     int32_t w[kInlineWords];
 };
-// Words the inline metadata of this plan needs.
+// Words the full inline encoding of this plan needs.
 int inline_words(const WorkList &plan, int n, bool with_rows);
-// Packs lens / plan / rows (rows may be NULL) into out; false if they do not fit.
+// Words of the compact encoding, or -1 when the plan does not allow it.
+int inline_words_compact(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n);
+// Packs lens / plan / rows (rows may be NULL) into out, in the full encoding
+// when it fits, else in the compact one; false if neither fits.
 bool pack_inline(const int32_t *lens, const WorkList &plan, const int32_t *rows, int n,
                  InlineMeta &out);
 

@@ -527,7 +527,15 @@ int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, 
         info->any_empty = wl.any_empty ? 1 : 0;
         info->max_len = wl.max_len;
         const int words = d::inline_words(wl, n, with_rows != 0);
-        info->inline_words = (n > 0 && words <= d::kInlineWords) ? words : -1;
+        info->inline_compact = 0;
+        if (n > 0 && words <= d::kInlineWords) {
+            info->inline_words = words;
+        } else {
+            // the compact encoding stores a row per entry either way
+            const int cw = d::inline_words_compact(seq_lens, wl, nullptr, n);
+            info->inline_compact = (cw > 0 && cw <= d::kInlineWords) ? 1 : 0;
+            info->inline_words = info->inline_compact ? cw : -1;
+        }
         if (part_base) std::memcpy(part_base, wl.part_base.data(), wl.part_base.size() * 4);
         if (work && wl.n_work) std::memcpy(work, wl.work.data(), wl.work.size() * 4);
         g_last_error.clear();

@@ -112,6 +112,47 @@ struct AttnArgs {
     InlineMeta    meta;       // used when meta.n > 0
 };
 
+// Work item `item` of the launch: entry b, chunk c of nch, attended length
+// S, partial row widx and cache row (slot) row, from the inline metadata
+// (full or compact encoding, see InlineMeta) or the plan's device arrays.
+// A macro, expanded in each kernel body on the by-value kernel argument `a`:
+// passing the argument by reference to a function makes the compiler copy
+// the whole 3.7 KB struct into per-lane scratch memory.
+#define ATTN_WORK_ITEM(a, item, b, c, S, nch, widx, row)                                           \
+    do {                                                                                           \
+        if ((a).meta.n && (a).meta.compact) { /* one chunk per entry */                            \
+            const uint32_t ord_ = (uint32_t)(a).meta.w[(a).meta.off_work + ((item) >> 1)];         \
+            b = (int)((ord_ >> (((item) & 1) * 16)) & 0xffffu);                                    \
+            const uint32_t e_ = (uint32_t)(a).meta.w[b];                                           \
+            S = (int)(e_ & 0xffffu);                                                               \
+            row = (int)(e_ >> 16);                                                                 \
+            c = 0;                                                                                 \
+            nch = 1;                                                                               \
+            widx = b;                                                                              \
+        } else if ((a).meta.n) { /* full encoding */                                               \
+            b = (a).meta.w[(a).meta.off_work + 2 * (item)];                                        \
+            c = (a).meta.w[(a).meta.off_work + 2 * (item) + 1];                                    \
+            S = (a).meta.w[b];                                                                     \
+            const int pb_ = (a).meta.w[(a).meta.off_part + b];                                     \
+            nch = (a).meta.w[(a).meta.off_part + b + 1] - pb_;                                     \
+            widx = pb_ + c;                                                                        \
+            row = (a).meta.has_rows ? (a).meta.w[(a).meta.off_rows + b] : b;                       \
+        } else {                                                                                   \
+            if ((a).plan.work) {                                                                   \
+                b = (a).plan.work[2 * (item)];                                                     \
+                c = (a).plan.work[2 * (item) + 1];                                                 \
+            } else {                                                                               \
+                b = (item) / (a).plan.nchunk;                                                      \
+                c = (item) - b * (a).plan.nchunk;                                                  \
+            }                                                                                      \
+            S = (a).plan.seq_lens ? (a).plan.seq_lens[b] : (a).plan.uniform_len;                   \
+            nch = (a).plan.part_base ? (a).plan.part_base[b + 1] - (a).plan.part_base[b]           \
+                                     : (a).plan.nchunk;                                            \
+            widx = (a).plan.part_base ? (a).plan.part_base[b] + c : (item);                        \
+            row = (a).kv.seq_row ? (a).kv.seq_row[b] : b;                                          \
+        }                                                                                          \
+    } while (0)
+
 // Byte addressing of the token rows of one (entry, kv head).
 template <bool PAGED>
 struct RowAddr {
@@ -536,28 +577,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     const int item = blockIdx.x / a.Hkv;
     const int g = blockIdx.x - item * a.Hkv;
     int       b, c, S, nch, widx, row;
-    if (a.meta.n) { // metadata in the kernel arguments
-        const int32_t *w = a.meta.w;
-        b = w[a.meta.off_work + 2 * item];
-        c = w[a.meta.off_work + 2 * item + 1];
-        S = w[b];
-        const int pb = w[a.meta.off_part + b];
-        nch = w[a.meta.off_part + b + 1] - pb;
-        widx = pb + c;
-        row = a.meta.has_rows ? w[a.meta.off_rows + b] : b;
-    } else {
-        if (pl.work) {
-            b = pl.work[2 * item];
-            c = pl.work[2 * item + 1];
-        } else {
-            b = item / pl.nchunk;
-            c = item - b * pl.nchunk;
-        }
-        S = pl.seq_lens ? pl.seq_lens[b] : pl.uniform_len;
-        nch = pl.part_base ? pl.part_base[b + 1] - pl.part_base[b] : pl.nchunk;
-        widx = pl.part_base ? pl.part_base[b] + c : item;
-        row = a.kv.seq_row ? a.kv.seq_row[b] : b;
-    }
+    ATTN_WORK_ITEM(a, item, b, c, S, nch, widx, row);
     const int t0 = c * pl.chunk;
     const int n = min(pl.chunk, S - t0); // >= 1 by construction of the plan
 
@@ -836,28 +856,7 @@ __global__ __launch_bounds__(kNW * 64) void attn_decode_mma_kernel(AttnArgs a) {
     const int       item = blockIdx.x / a.Hkv;
     const int       g = blockIdx.x - item * a.Hkv;
     int             b, c, S, nch, widx, row;
-    if (a.meta.n) {
-        const int32_t *w = a.meta.w;
-        b = w[a.meta.off_work + 2 * item];
-        c = w[a.meta.off_work + 2 * item + 1];
-        S = w[b];
-        const int pb = w[a.meta.off_part + b];
-        nch = w[a.meta.off_part + b + 1] - pb;
-        widx = pb + c;
-        row = a.meta.has_rows ? w[a.meta.off_rows + b] : b;
-    } else {
-        if (pl.work) {
-            b = pl.work[2 * item];
-            c = pl.work[2 * item + 1];
-        } else {
-            b = item / pl.nchunk;
-            c = item - b * pl.nchunk;
-        }
-        S = pl.seq_lens ? pl.seq_lens[b] : pl.uniform_len;
-        nch = pl.part_base ? pl.part_base[b + 1] - pl.part_base[b] : pl.nchunk;
-        widx = pl.part_base ? pl.part_base[b] + c : item;
-        row = a.kv.seq_row ? a.kv.seq_row[b] : b;
-    }
+    ATTN_WORK_ITEM(a, item, b, c, S, nch, widx, row);
     const int t0 = c * pl.chunk;
     const int n = __builtin_amdgcn_readfirstlane(min(pl.chunk, S - t0));
     const RowAddr<PAGED> ra(a.kv, row, g);
@@ -1326,6 +1325,8 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
                                     std::string(paged ? "block" : "slot") + " * row bytes)");
     if (plan.any_multi && !part)
         throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
+    if (inl && inl->compact && (plan.any_multi || plan.any_empty || plan.n_work != inl->n))
+        throw std::invalid_argument("attention: compact metadata needs one chunk per entry");
     AttnArgs args;
     args.q = q;
     args.out = out;
