@@ -309,6 +309,8 @@ def fixed_batch(args, tl, torch, workloads, np):
     ctx = cfg.contexts.astype(np.int64)
     bt = cfg.block_tokens
     M = int((ctx.max() + K + 1 + 63) // 64 * 64)
+    if cfg.cfg == 3:  # the configuration's pool: max_seq_len 8448 (8192 + 256 decode steps)
+        M = max(M, 8448)
     if args.max_seq_len:
         if args.max_seq_len < ctx.max() + K + 1 or (bt and args.max_seq_len % bt):
             raise SystemExit(f"--max-seq-len {args.max_seq_len} cannot hold the context and "

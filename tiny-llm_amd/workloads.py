@@ -61,7 +61,7 @@ def config(cfg: int, steps: int | None = None) -> DecodeConfig:
     elif cfg == 3:
         ctx = np.full(64, 8192, dtype=np.int32)
         c = DecodeConfig("cfg3_llama3_8b_gqa_b64_ctx8k", 3, 1, 64, 32, 8, 128, 0, steps or 100)
-        c.max_seq_len = _round_up(8192 + c.steps, 64)
+        c.max_seq_len = max(8448, _round_up(8192 + c.steps + 1, 64))
     elif cfg == 4:
         ctx = lognormal_lengths(128, median=2048, sigma=1.0, lo=1, hi=32768, seed_=seed(4, 3))
         c = DecodeConfig("cfg4_ragged_paged_b128", 4, 1, 128, 32, 8, 128, 0, steps or 3,
