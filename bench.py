@@ -700,7 +700,14 @@ def gemm_bench(args, tl, torch, np):
     16 layers rotate, so that every call streams its weights from HBM (16 x 25
     MB > the 256 MB MALL).  project: one launch computes Q into a buffer and K/V
     straight into the cache at each sequence's write position; oproj: hidden +=
-    fp16(attn_out @ W_o)."""
+    fp16(attn_out @ W_o).
+
+    Two timings: `back_to_back` queues the calls behind a GPU sleep so that
+    they run one after another as in a decode step (the batch's metadata is
+    prepared once, as once per step for every layer), and `isolated` issues
+    each call (project: with its prepare and commit) from the host and waits
+    several microseconds of host work between kernels, so each starts cold.
+    `value`, `kernels_us` and the roofline are the back-to-back ones."""
     B, hidden, Hq, Hkv, D, gs, sets = 64, 4096, 32, 8, 128, 128, 16
     K = args.steps or 100
     dev = torch.device("cuda", 0)
@@ -724,18 +731,22 @@ def gemm_bench(args, tl, torch, np):
     if args.path == "project":
         nq, nkv = Hq * D, Hkv * D
         W = [(weights(nq), weights(nkv), weights(nkv)) for _ in range(sets)]
-        M = ((16 + K + args.warmup + 10 + 63) // 64) * 64
+        M = ((16 + 2 * K + args.warmup + 10 + 63) // 64) * 64
         mgr = tl.KVCacheManager(1, Hkv, D, M, B)
         ids = [mgr.allocateSequence(M)[0] for _ in range(B)]
         q_out = torch.empty((B, nq), device=dev, dtype=torch.float16)
         batch = tl.DecodeBatch(mgr, B, Hq)
 
-        def call(i):
+        def kernel(i):
             (wq, sq), (wk, sk), (wv, sv) = W[i % sets]
-            batch.prepare(ids, stream)
             batch.project(0, x.data_ptr(), hidden, gs, wk.data_ptr(), sk.data_ptr(), wv.data_ptr(),
                           sv.data_ptr(), wq.data_ptr(), sq.data_ptr(), q_out.data_ptr(), stream,
                           packed=packed)
+
+        def begin():
+            batch.prepare(ids, stream)
+
+        def end():
             batch.commit(1)
         n_out = nq + 2 * nkv
         nbytes = hidden * n_out + ((hidden + gs - 1) // gs) * n_out * 2 + B * hidden * 2 + B * n_out * 2
@@ -745,30 +756,55 @@ def gemm_bench(args, tl, torch, np):
         h = torch.randn((B, hidden), generator=gen, device=dev, dtype=torch.float16)
         n_out = hidden
 
-        def call(i):
+        def kernel(i):
             w, sc = W[i % sets]
             tl.w8a16_matmul_residual(x.data_ptr(), w.data_ptr(), sc.data_ptr(), h.data_ptr(), B,
                                      hidden, hidden, gs, stream, packed=packed)
+
+        def begin():
+            pass
+
+        def end():
+            pass
         nbytes = hidden * hidden + ((hidden + gs - 1) // gs) * hidden * 2 + B * hidden * 2 + 2 * B * hidden * 2
         desc = "o_proj + residual: hidden += fp16(attn_out @ W_o)"
-    for i in range(args.warmup):
-        call(i)
-    torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(args.warmup):
+        begin()
+        kernel(i)
+        end()
+    torch.cuda.synchronize()
+    # isolated: each call from the host, with its prepare / commit
     t_wall = time.perf_counter()
     ev0.record()
     for i in range(K):
-        call(i)
+        begin()
+        kernel(i)
+        end()
     ev1.record()
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall
-    ms = ev0.elapsed_time(ev1) / K
-    tl.profile_reset()
-    tl.profile_enable(True)
-    for i in range(min(K, 32)):
-        call(i)
-    torch.cuda.synchronize()
-    tl.profile_enable(False)
+    iso_ms = ev0.elapsed_time(ev1) / K
+
+    def burst(profile):
+        """K calls queued behind a GPU sleep: the kernels run back to back."""
+        begin()
+        torch.cuda.synchronize()
+        if profile:
+            tl.profile_reset()
+            tl.profile_enable(True)
+        torch.cuda._sleep(200_000_000)  # ~0.1 s of GPU cycles: the host queues every call meanwhile
+        ev0.record()
+        for i in range(K):
+            kernel(i)
+        ev1.record()
+        torch.cuda.synchronize()
+        if profile:
+            tl.profile_enable(False)
+        end()
+        return ev0.elapsed_time(ev1) / K
+    ms = burst(False)
+    burst(True)
     g_ms, g_n = tl.profile_query("w8a16")
     r_ms, r_n = tl.profile_query("w8a16_reduce")
     tl.profile_reset()
@@ -777,6 +813,7 @@ def gemm_bench(args, tl, torch, np):
     flops = 2.0 * B * hidden * n_out
     kern_ms = g_avg + r_avg
     gbps = nbytes / (kern_ms * 1e-3) / 1e9
+    kname = "w8a16_dec_kernel" if r_n == 0 else "w8a16_sk_kernel + w8a16_reduce_kernel"
     return {
         "metric": f"W8A16 {args.path} µs/call and achieved HBM GB/s, Llama-3-8B layer, batch 64",
         "value": round(nbytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": K,
@@ -786,10 +823,11 @@ def gemm_bench(args, tl, torch, np):
                 "U(0.001, 0.021) (torch, seeded)",
         "config": {"workload": f"llama3_8b_{args.path}_b64", "batch": B, "hidden": hidden,
                    "out_columns": n_out, "group_size": gs, "weight_sets": sets,
-                   "weights": args.weights, "what": desc},
+                   "weights": args.weights, "what": desc, "timing": "back_to_back"},
         "kernels_us": {"w8a16": round(g_avg * 1e3, 2), "w8a16_reduce": round(r_avg * 1e3, 2)},
-        "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
-        "roofline": {"kernel": "w8a16_sk_kernel + w8a16_reduce_kernel", "bound": "hbm",
+        "isolated_us_per_call": round(iso_ms * 1e3, 2),
+        "host_wall_us_per_call_isolated": round(t_wall / K * 1e6, 2),
+        "roofline": {"kernel": kname, "bound": "hbm",
                      "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "tflops": round(flops / (kern_ms * 1e-3) / 1e12, 2),

@@ -38,9 +38,17 @@ def stream() -> int:
 
 def rel_err(a: np.ndarray, b: np.ndarray) -> float:
     """Normwise max|a-b| / max(|a|,|b|): computeRelativeError of
-    tests/test_transformer.cu:80-92."""
+    tests/test_transformer.cu:80-92.  A non-finite value in one array that the
+    other does not hold at the same place gives inf (never NaN, which every
+    `<= tol` comparison would let through unnoticed in a max())."""
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
+    fa, fb = np.isfinite(a), np.isfinite(b)
+    if not (fa.all() and fb.all()):
+        same = np.array_equal(fa, fb) and np.array_equal(a[~fa], b[~fb], equal_nan=True)
+        if not same:
+            return float("inf")
+        a, b = a[fa], b[fb]
     mx = max(np.abs(a).max(initial=0.0), np.abs(b).max(initial=0.0))
     return float(np.abs(a - b).max(initial=0.0) / mx) if mx > 0 else 0.0
 

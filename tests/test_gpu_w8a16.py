@@ -41,6 +41,13 @@ SHAPES = [  # (M, N, K, gs, mfma-eligible)
     (17, 48, 96, 64, True),        # K % 64 == 32 with a partial last scale group
     (5, 32, 160, 128, True),
     (9, 64, 1056, 256, True),      # several batches, the last one short
+    # the decode kernel (M <= 64, K % 128 == 0, K <= 4096): row halves, waves
+    # without a chunk (K = 384: 3 chunks for 8 waves), every fold width
+    (33, 112, 384, 64, True),      # two row halves, M past the first by one
+    (48, 4096, 4096, 32, True),    # a fold per k step
+    (64, 6144, 4096, 256, True),   # a group over two chunks, three-block tiles
+    (20, 3072, 2048, 512, True),   # one row half
+    (64, 16, 128, 128, True),      # one block, one chunk
     (4, 8, 16, 8, False),          # the reference's test shapes (reference-order kernel)
     (17, 33, 65, 32, False),
     (64, 1, 128, 32, False),
@@ -302,3 +309,48 @@ def test_project_rejects_bad_calls(tl):
         batch.project(0, 16, 64, 32, 16, 16, 16, 16, wq=16)
     with pytest.raises(tl.TinyLLMError, match="layer"):
         batch.project(3, 16, 64, 32, 16, 16, 16, 16)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_project_fused_append_llama_layer(tl, orc, packed):
+    """The benchmarked shape: a Llama-3-8B layer (hidden 4096, 8 KV heads and
+    32 query heads of 128, group 128) for a decode batch of 64.  The fused
+    projection's column tiles span the K|V and V|Q segment boundaries; cache
+    bytes and q_out equal w8a16_matmul + appendKV(n=1) bit for bit (both
+    weight layouts), and the K, V and Q rows stay within 1e-3 of the oracle."""
+    rng = np.random.default_rng(4096 + packed)
+    L, Hkv, G, D, hidden, gs = 1, 8, 4, 128, 4096, 128
+    Hq, row = Hkv * G, Hkv * D
+    lens = [int(v) for v in np.random.default_rng(77).integers(1, 48, size=64)]
+    M = 64
+    g, o, ids, keep = _cache(tl, orc, rng, L, Hkv, D, M, lens, False)
+    g2, _, ids2, keep2 = _cache(tl, orc, np.random.default_rng(4096 + packed), L, Hkv, D, M, lens, False)
+    B = len(ids)
+    x = orc.f2h(rng.standard_normal((B, hidden)).astype(np.float32))
+    _, wk, sk = operands(orc, rng, 1, row, hidden, gs)
+    _, wv, sv = operands(orc, rng, 1, row, hidden, gs)
+    _, wq, sq = operands(orc, rng, 1, Hq * D, hidden, gs)
+    dx, dsk, dsv, dsq = to_dev(x), to_dev(sk), to_dev(sv), to_dev(sq)
+    if packed:
+        dwk, dwv, dwq = packed_dev(tl, wk), packed_dev(tl, wv), packed_dev(tl, wq)
+    else:
+        dwk, dwv, dwq = to_dev_raw(wk), to_dev_raw(wv), to_dev_raw(wq)
+    batch = tl.DecodeBatch(g, B, Hq)
+    batch.prepare(ids, stream())
+    q_out = empty_dev((B, Hq * D))
+    batch.project(0, dx.data_ptr(), hidden, gs, dwk.data_ptr(), dsk.data_ptr(), dwv.data_ptr(),
+                  dsv.data_ptr(), dwq.data_ptr(), dsq.data_ptr(), q_out.data_ptr(), stream(), packed=packed)
+    kb, vb, qb = empty_dev((B, row)), empty_dev((B, row)), empty_dev((B, Hq * D))
+    for w_, s_, out_, n_ in ((dwk, dsk, kb, row), (dwv, dsv, vb, row), (dwq, dsq, qb, Hq * D)):
+        out_.zero_()
+        tl.w8a16_matmul_residual(dx.data_ptr(), w_.data_ptr(), s_.data_ptr(), out_.data_ptr(), B, n_,
+                                 hidden, gs, stream(), packed=packed)
+    batch2 = tl.DecodeBatch(g2, B, Hq)
+    batch2.prepare(ids2, stream())
+    batch2.append(0, 1, kb.data_ptr(), vb.data_ptr(), stream())
+    pool_elems = g.slot_bytes() // 2 * (B + 1)
+    assert np.array_equal(read_dev(g.pool(), pool_elems), read_dev(g2.pool(), pool_elems))
+    assert np.array_equal(to_host(q_out), to_host(qb))
+    for got, (w, s, n) in ((kb, (wk, sk, row)), (vb, (wv, sv, row)), (qb, (wq, sq, Hq * D))):
+        ref32, _ = orc.w8a16_matmul(x, w, s, B, n, hidden, gs)
+        assert rows_close(to_host(got), ref32) <= TOL

@@ -67,3 +67,16 @@ def test_default_decode_kernels_spill_little(tmp_path):
             continue
         g = int(m.group(2))
         assert r["vgpr_spill_count"] <= (4 if g == 8 else 0), (name, r)
+
+
+def test_w8a16_kernels_use_no_scratch(tmp_path):
+    """The W8A16 kernels keep their register rings, accumulators and the
+    epilogue operands in registers: no per-lane scratch (a segment field
+    picked by a run-time index, or a struct indexed the same way, would put
+    the kernel argument block there), no VGPR spills."""
+    ks = kernels("w8a16_gemm.o", tmp_path)
+    dec = {n: r for n, r in ks.items() if "w8a16_dec_kernel" in n}
+    assert len(dec) == 16, sorted(dec)
+    for name, r in ks.items():
+        assert r["private_segment_fixed_size"] == 0, (name, r)
+        assert r["vgpr_spill_count"] == 0, (name, r)

@@ -42,7 +42,8 @@ struct CacheRows {
 // segment's n % 16 == 0); other shapes take the reference-order kernel.
 bool w8a16_mfma_ok(int K, int gs, const W8A16Seg *segs, int nseg);
 
-// fp32 workspace (elements) that launch_w8a16 needs for split-K partials.
+// fp32 workspace (elements) that launch_w8a16 needs for split-K partials
+// (none for M <= 64: that kernel runs over the whole of K).
 size_t w8a16_workspace_floats(int M, int K, int gs, const W8A16Seg *segs, int nseg);
 
 // out = x @ dequant(W_i, s_i) for each segment i, with its epilogue.  x [M][K]

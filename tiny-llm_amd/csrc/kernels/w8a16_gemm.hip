@@ -5,29 +5,28 @@
 // [ceil(K/gs)][N] fp16.
 //
 // MFMA path (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
-// N % 16 == 0).  It splits K across workgroups for decode-sized M (the split
-// count depends on (M, K) only, so an output element's value does not depend
-// on which other weight matrices share the launch) and sums the splits in a
-// fixed order, so results are deterministic.
+// N % 16 == 0), two kernels, each for both weight layouts (packed: the
+// launch_w8a16_pack layout, B fragments of 8 bytes per lane; reference:
+// [K][N] row-major, staged in LDS and read as B fragments by the transposing
+// ds_read_b64_tr_b8).  Both layouts give the same fragments and the same
+// summation order, hence the same bits.  The int8 weights become fp16
+// exactly and multiply on v_mfma_f32_16x16x32_f16; each scale group's
+// product is folded into the fp32 accumulator with its scale.
 //
-// One kernel, w8a16_sk_kernel, for both weight layouts: one workgroup = 4
-// waves = a 64x64 output tile over one split; wave w takes every fourth group
-// of 4 k steps for the whole tile (16 MFMAs per step: 4 row blocks x 4
-// column blocks of v_mfma_f32_16x16x32_f16 on the integer weights, converted
-// to fp16 exactly; each scale group's product folded into the fp32
-// accumulator with its scale).  x is staged two k steps at a time in the
-// wave's own LDS by the LDS DMA load (coalesced rows).  W:
-//   packed (layout of launch_w8a16_pack): B fragments, 8 bytes per lane,
-//     loaded straight into registers;
-//   reference ([K][N] row-major): two k steps of the tile's 64 columns staged
-//     in LDS by the DMA load and read as B fragments by the transposing
-//     ds_read_b64_tr_b8.
-// Both layouts give the same fragments and the same summation order, hence
-// the same bits.  No barrier until the waves' tiles are summed through LDS.
+//   w8a16_dec_kernel (M <= 64, K a multiple of 128 up to 4096: the decode
+//     projections): one launch over the whole of K, no partials (described
+//     at the kernel).
+//   w8a16_sk_kernel (every other MFMA shape): one workgroup = 4 waves = a
+//     64x64 output tile over one K split; wave w takes every fourth group of
+//     4 k steps for the whole tile; x staged two k steps at a time in the
+//     wave's own LDS by the LDS DMA load.  The split count depends on (M, K)
+//     only.  With one split the kernel applies the epilogue; otherwise it
+//     writes fp32 partials and w8a16_reduce_kernel sums the splits in split
+//     order and applies it.
 //
-// With one split the GEMM kernel applies the epilogue directly; otherwise it
-// writes fp32 partials and w8a16_reduce_kernel sums the splits in split order
-// and applies the epilogue.
+// The summation order of an output element depends on (M, K) only -- never
+// on which other weight matrices share the launch -- so results are
+// deterministic and the fused projection equals the unfused products.
 //
 // Generic path (any shape): one thread per output, the reference formula
 // sum = fma(x, w * s, sum) over k in order.
@@ -67,6 +66,7 @@ constexpr int kWaitLgkm0 = 0xC07F; // s_waitcnt lgkmcnt(0)
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
 typedef int      v2i32 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
     const __half *x; // [M][K]
@@ -404,6 +404,373 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-sized M (<= 64 rows; K a multiple of 128 up to 4096):
+// w8a16_dec_kernel, one launch over the whole of K (no split-K partials, no
+// second kernel).
+//
+// A workgroup of 8 waves owns a tile of CB 16-column blocks (numbered over all
+// segments, so a tile may span two segments) for one half of the rows (32
+// rows, two MFMA row blocks).  K is cut into 128-row chunks (4 k steps); wave
+// w takes chunks w, w + 8, w + 16, w + 24 through a two-deep register ring:
+// x in whole 128-byte lines (4 rows x 256 bytes per load) and packed W
+// fragments (8 bytes per lane) load into registers, so the compiler's own
+// load counters order each use after exactly the data it needs, and the next
+// chunks' loads are in flight while one is multiplied.  (The LDS DMA load
+// would not do: this compiler waits for every outstanding load before the
+// first LDS read that follows one.)  x reaches the MFMA A layout through the
+// wave's own LDS stage.  Reference-layout W ([K][N] row-major) is loaded as
+// 16-byte row pieces, written to the wave's W stage and read back as B
+// fragments with the transposing ds_read_b64_tr_b8 -- the same fragments as
+// the packed layout.
+// Each fold group's product (a chunk for gs >= 128, else gs / 32 steps) is
+// folded into the fp32 accumulator with its scale; the 8 waves' tiles are
+// summed through LDS in wave order and the epilogue is applied.
+//
+// The two row halves of a tile run on the same XCD (workgroups b and b + 8 of
+// the round-robin dispatch) at the same time, so the second reads the tile's
+// weights from that XCD's L2; each XCD takes a contiguous range of tiles.
+// The summation order of an output depends on K alone (chunks, waves), never
+// on the column tiling or the segments sharing the launch, so the fused
+// projection's cache bytes equal the unfused product's, and both weight
+// layouts give the same bits.
+constexpr int kDecRows = 64;   // the kernel's M limit
+constexpr int kDecMaxK = 4096; // and K limit (a multiple of 128): 4 chunks per wave
+constexpr int kDecHalf = 32;   // rows per workgroup
+constexpr int kDecWaves = 8;
+
+struct DecArgs {
+    const __half *x; // [M][K]
+    int64_t       ldx;
+    int           M, K, gs;
+    int           nseg;
+    int           tiles;  // column tiles of CB blocks
+    int           tpx;    // tiles per XCD: ceil(tiles / 8)
+    int           halves; // row halves (1 when M <= 32)
+    int           blocks; // 16-column blocks over all segments
+    W8A16Seg      seg[kMaxSegs];
+    int           col0[kMaxSegs + 1];
+    CacheRows     cache;
+};
+
+// Field f of segment si (uniform), with static indices only.
+#define TL_DEC_SEG(a, si, f) ((si) == 0 ? (a).seg[0].f : (si) == 1 ? (a).seg[1].f : (a).seg[2].f)
+
+// Segment of global 16-column block gb.
+__device__ __forceinline__ int dec_seg_of(const DecArgs &a, int gb) {
+    const int c = 16 * gb;
+    return (a.nseg > 1 && c >= a.col0[1]) ? ((a.nseg > 2 && c >= a.col0[2]) ? 2 : 1) : 0;
+}
+
+// Rotation of the reference-layout LDS stage: piece p of stage row r sits in
+// slot (p + dec_rot(r)) % CB of the row, so that the 8 rows a
+// ds_read_b64_tr_b8 group reads fall on distinct 16-byte bank slots (odd
+// widths need none: rows 16 * CB bytes apart already do).
+template <int CB> __device__ __forceinline__ int dec_rot(int r) {
+    return CB == 2 ? (r >> 2) : CB == 4 ? (r >> 1) : 0;
+}
+
+// Buffer resource of a raw byte range (stride 0, the gfx9 data format word).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dec_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// FS: k steps per scale fold (gs / 32, at most 4 = one chunk).  CB: column
+// blocks per tile.  PACKED: W in the launch_w8a16_pack layout.
+template <int FS, int CB, bool PACKED>
+__global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
+    static_assert(FS == 1 || FS == 2 || FS == 4, "fold");
+    static_assert(CB >= 1 && CB <= 4, "column blocks");
+    constexpr int NF = 4 / FS;                                  // folds per chunk
+    constexpr int RED = kDecWaves * 2 * CB * 64 * 4;            // floats: every wave's tile
+    constexpr int XST = kDecHalf * 256;                         // bytes: a wave's x stage (one chunk)
+    constexpr int WST = PACKED ? 0 : 128 * CB * 16;             // bytes: its W stage (reference layout)
+    constexpr int STAGE = kDecWaves * (XST + WST) / 4;          // floats
+    __shared__ __align__(16) float lds[RED > STAGE ? RED : STAGE];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch).  XCD x takes the
+    // contiguous tiles [x * tpx, (x + 1) * tpx), both row halves of a tile
+    // (workgroups b and b + 8): the halves share the tile's weights, and
+    // column-adjacent tiles the 128-byte lines of row-major weights, in that
+    // XCD's L2.  (Another placement costs speed, never correctness.)
+    const int slot = blockIdx.x >> 3;
+    const int half = a.halves == 2 ? (slot & 1) : 0;
+    const int tile = (int)(blockIdx.x & 7) * a.tpx + (a.halves == 2 ? slot >> 1 : slot);
+    if (tile >= a.tiles) return; // uniform for the workgroup
+    const int ksteps = a.K >> 5;
+    const int nchunks = (ksteps + 3) >> 2;
+    const int ngroups = (a.K + a.gs - 1) / a.gs;
+    const int mine = wave < nchunks ? (nchunks - wave + kDecWaves - 1) / kDecWaves : 0; // this wave's chunks
+
+    // The tile's column blocks: segment, local block, and the buffer
+    // resources of their weights and scales (uniform: the loads take the
+    // chunk and group offsets in scalar registers and a lane offset fixed for
+    // the whole kernel, so they cost no vector address arithmetic).
+    int                    si[CB], nb[CB], sn[CB];
+    const int8_t          *wb[CB]; // reference layout: column base
+    __amdgpu_buffer_rsrc_t rw[CB], rs[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const int gb = min(tile * CB + cb, a.blocks - 1);
+        si[cb] = dec_seg_of(a, gb);
+        nb[cb] = gb - ((si[cb] == 0 ? 0 : si[cb] == 1 ? a.col0[1] : a.col0[2]) >> 4);
+        sn[cb] = TL_DEC_SEG(a, si[cb], n);
+        wb[cb] = TL_DEC_SEG(a, si[cb], w) + (int64_t)16 * nb[cb];
+        rw[cb] = dec_rsrc(TL_DEC_SEG(a, si[cb], w), (uint32_t)sn[cb] * (uint32_t)a.K);
+        rs[cb] = dec_rsrc(TL_DEC_SEG(a, si[cb], s), (uint32_t)ngroups * (uint32_t)sn[cb] * 2u);
+    }
+    const uint32_t sv = 2u * (lane & 15); // scale lane offset (+ 32 nb)
+    // This wave's output block (waves < 2 CB): row block wave & 1, column
+    // block wave >> 1.  Its epilogue operands -- the cache rows and write
+    // positions, or the residual -- are loaded now, so that the stores at the
+    // end do not wait a round trip for them.
+    const int erb = wave & 1, ecb = wave >> 1;
+    int       esi = 0, en = 0;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) // static indices
+        if (cb == ecb) {
+            esi = si[cb];
+            en = 16 * nb[cb] + (lane & 15);
+        }
+    const bool eact = wave < 2 * CB && tile * CB + ecb < a.blocks; // (a block past the last segment: none)
+    const int  ekind = TL_DEC_SEG(a, esi, kind);
+    int        erow[4] = {0, 0, 0, 0}, epos[4] = {0, 0, 0, 0};
+    __half     eres[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) eres[i] = __float2half(0.0f);
+    if (eact) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = min(kDecHalf * half + 16 * erb + 4 * (lane >> 4) + i, a.M - 1);
+            if (ekind == kEpiCache) {
+                erow[i] = a.cache.seq_row[m];
+                epos[i] = a.cache.wpos[m];
+            } else if (ekind == kEpiResidual) {
+                eres[i] = TL_DEC_SEG(a, esi, res)[(int64_t)m * TL_DEC_SEG(a, esi, ld) + en];
+            }
+        }
+    }
+    // x is loaded in whole 128-byte lines -- 4 rows x 256 bytes (one chunk)
+    // per load -- and rearranged into MFMA A fragments through the wave's LDS
+    // stage: the A layout itself (16 rows x 64 bytes per load) touches every
+    // line twice and ran at less than half the rate.  Load i: row 4i + lane
+    // / 16 of the half (clamped to M - 1; rows >= M are never stored).
+    const __amdgpu_buffer_rsrc_t rx = dec_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.ldx * 2u);
+    uint32_t                     xv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        xv[i] = (uint32_t)min(kDecHalf * half + 4 * i + (lane >> 4), a.M - 1) * (uint32_t)a.ldx * 2u + 16u * (lane & 15);
+
+    // A chunk's x (XSlot) and its weights and scales (WSlot), in registers.
+    struct XSlot {
+        u32x4 x[8]; // 4 rows x 256 bytes of x per load
+    };
+    struct WSlot {
+        uint2  w[PACKED ? 4 * CB : 1]; // [k step][cb]
+        u32x4  r[PACKED ? 1 : 2 * CB]; // row pieces (reference layout)
+        __half s[NF][CB];              // converted at the fold: a conversion here would wait for the load
+    };
+    auto load_x = [&](XSlot &sl, int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            sl.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xv[i], 256 * c, 0));
+    };
+    auto load_w = [&](WSlot &sl, int c) __attribute__((always_inline)) {
+        if constexpr (PACKED) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+                    sl.w[s * CB + cb] = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[cb], 8 * lane, (nb[cb] * ksteps + 4 * c + s) * 512, 0));
+        } else {
+            // stage slot q = t * 64 + lane (16 bytes): row q / CB, slot q % CB
+            // of the row, which holds piece (q % CB - dec_rot(row)) mod CB
+#pragma unroll
+            for (int t = 0; t < 2 * CB; ++t) {
+                const int q = t * 64 + lane;
+                const int r = q / CB;
+                const int p = (q % CB + CB * 64 - dec_rot<CB>(r)) % CB;
+                const int k = 128 * c + r;
+                const int8_t *src = wb[0];
+                int64_t       pitch = sn[0];
+#pragma unroll
+                for (int cb = 1; cb < CB; ++cb) {
+                    src = p == cb ? wb[cb] : src;
+                    pitch = p == cb ? (int64_t)sn[cb] : pitch;
+                }
+                sl.r[t] = *reinterpret_cast<const u32x4 *>(src + k * pitch);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int g = (128 * c + 32 * FS * f) / a.gs;
+                sl.s[f][cb] = __builtin_bit_cast(
+                    __half, __builtin_amdgcn_raw_buffer_load_b16(rs[cb], sv + 32u * nb[cb], 2 * g * sn[cb], 0));
+            }
+    };
+
+    f32x4 acc[2][CB], P[2][CB];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            acc[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            P[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    // The wave's stages (one chunk each; LDS operations of a wave run in
+    // order, so the next chunk's writes follow this chunk's reads).  x stage:
+    // 32 rows of 256 bytes, 16-byte piece p of row r in slot p ^ (r & 15), so
+    // that the stores (8 lanes = 8 pieces of a row) and the A-fragment reads
+    // (8 lanes = 8 rows, one piece) touch distinct banks.
+    uint8_t *const xst = reinterpret_cast<uint8_t *>(lds) + (size_t)wave * (XST + WST);
+    uint8_t *const wst = xst + XST;
+    auto compute = [&](const XSlot &xs, const WSlot &sl, int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 4 * i + (lane >> 4);
+            *reinterpret_cast<u32x4 *>(xst + r * 256 + 16 * ((lane & 15) ^ (r & 15))) = xs.x[i];
+        }
+        if constexpr (!PACKED) {
+#pragma unroll
+            for (int t = 0; t < 2 * CB; ++t) *reinterpret_cast<u32x4 *>(wst + (t * 64 + lane) * 16) = sl.r[t];
+        }
+        const int steps = min(4, ksteps - 4 * c);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s >= steps) break; // uniform
+            f16x8 xa[2]; // A fragments: row 16 rb + lane % 16, piece 4 s + lane / 16
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                const int r = 16 * rb + (lane & 15);
+                xa[rb] = *reinterpret_cast<const f16x8 *>(xst + r * 256 + 16 * ((4 * s + (lane >> 4)) ^ (r & 15)));
+            }
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                uint2 raw;
+                if constexpr (PACKED) {
+                    raw = sl.w[s * CB + cb];
+                } else {
+                    const int   i = lane & 15;
+                    const int   r = 32 * s + 8 * (lane >> 4) + (i >> 1);
+                    const int   pos = (cb + dec_rot<CB>(r)) % CB;
+                    const v2i32 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                        (__attribute__((address_space(3))) v2i32 *)(wst + (r * CB + pos) * 16 + 8 * (i & 1)));
+                    raw = make_uint2((uint32_t)t[0], (uint32_t)t[1]);
+                }
+                const uint2 lo = i8x4_to_f16x4(raw.x), hi = i8x4_to_f16x4(raw.y);
+                const f16x8 bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+                    P[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rb], bop, P[rb][cb], 0, 0, 0);
+            }
+            if ((s + 1) % FS == 0 || s + 1 == steps) { // end of a fold group
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[rb][cb][i] = fmaf(P[rb][cb][i], h2f(sl.s[s / FS][cb]), acc[rb][cb][i]);
+                        P[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+            }
+        }
+    };
+
+    // This wave's chunks wave, wave + 8, wave + 16, wave + 24 (K <= 4096),
+    // fully unrolled.  The weights of all four are requested first (the HBM
+    // stream never waits for arithmetic: issuing a chunk's weights only after
+    // multiplying an earlier one left the stream at half rate), x through a
+    // two-deep ring behind them.  Every load is issued on every path, so the
+    // compiler's load counters see the same loads in flight at each wait
+    // whichever way a branch went (after a conditional load it would wait
+    // for all of them); a chunk past the wave's last one re-reads that last
+    // one (cache hits, never multiplied).
+    // (A wave without chunks -- K of fewer than 8 chunks -- loads the last
+    // chunk of K: every offset below stays inside its operand only for
+    // chunks < nchunks.)
+    auto chunk_of = [&](int j) __attribute__((always_inline)) {
+        return mine > 0 ? wave + kDecWaves * min(j, mine - 1) : nchunks - 1;
+    };
+    if constexpr (CB <= 3) {
+        WSlot ws[4];
+        XSlot xs[2];
+        load_w(ws[0], chunk_of(0));
+        load_x(xs[0], chunk_of(0));
+        load_w(ws[1], chunk_of(1));
+        load_x(xs[1], chunk_of(1));
+        load_w(ws[2], chunk_of(2));
+        load_w(ws[3], chunk_of(3));
+        if (mine > 0) compute(xs[0], ws[0], chunk_of(0));
+        load_x(xs[0], chunk_of(2));
+        if (mine > 1) compute(xs[1], ws[1], chunk_of(1));
+        load_x(xs[1], chunk_of(3));
+        if (mine > 2) compute(xs[0], ws[2], chunk_of(2));
+        if (mine > 3) compute(xs[1], ws[3], chunk_of(3));
+    } else { // four blocks: registers hold two chunks' weights
+        WSlot ws[2];
+        XSlot xs[2];
+        load_w(ws[0], chunk_of(0));
+        load_x(xs[0], chunk_of(0));
+        load_w(ws[1], chunk_of(1));
+        load_x(xs[1], chunk_of(1));
+        if (mine > 0) compute(xs[0], ws[0], chunk_of(0));
+        load_w(ws[0], chunk_of(2));
+        load_x(xs[0], chunk_of(2));
+        if (mine > 1) compute(xs[1], ws[1], chunk_of(1));
+        load_w(ws[1], chunk_of(3));
+        load_x(xs[1], chunk_of(3));
+        if (mine > 2) compute(xs[0], ws[0], chunk_of(2));
+        if (mine > 3) compute(xs[1], ws[1], chunk_of(3));
+    }
+
+    // The 8 waves' tiles, summed in wave order: block (rb, cb) by wave 2cb + rb.
+    __syncthreads(); // the sums overwrite the other waves' stages
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            *reinterpret_cast<f32x4 *>(&lds[(((wave * 2 + rb) * CB + cb) * 64 + lane) * 4]) = acc[rb][cb];
+    __syncthreads();
+    if (!eact) return;
+    f32x4 v = *reinterpret_cast<const f32x4 *>(&lds[(((0 * 2 + erb) * CB + ecb) * 64 + lane) * 4]);
+#pragma unroll
+    for (int src = 1; src < kDecWaves; ++src) {
+        const f32x4 u = *reinterpret_cast<const f32x4 *>(&lds[(((src * 2 + erb) * CB + ecb) * 64 + lane) * 4]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += u[i];
+    }
+    // Epilogue: dense out[m][n] = fp16(v); residual fp16(res + fp16(v));
+    // cache: the K or V row of entry m at its write position.
+    __half *const out = TL_DEC_SEG(a, esi, out);
+    const int64_t ld = TL_DEC_SEG(a, esi, ld);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = kDecHalf * half + 16 * erb + 4 * (lane >> 4) + i;
+        if (m >= a.M) continue;
+        const __half o = __float2half(v[i]);
+        if (ekind == kEpiCache) {
+            const CacheRows &c = a.cache;
+            int64_t          off;
+            if (c.block_table) {
+                const int blk = c.block_table[(int64_t)erow[i] * c.bt_stride + (epos[i] >> c.log2_blk)];
+                off = (int64_t)blk * c.blk_stride + (int64_t)(epos[i] & ((1 << c.log2_blk) - 1)) * c.tok_stride;
+            } else {
+                off = (int64_t)erow[i] * c.blk_stride + (int64_t)epos[i] * c.tok_stride;
+            }
+            out[off + en] = o;
+        } else if (ekind == kEpiResidual) {
+            out[(int64_t)m * ld + en] = __float2half(h2f(eres[i]) + h2f(o));
+        } else {
+            out[(int64_t)m * ld + en] = o;
+        }
+    }
+}
+
 // Repacks W [K][N] int8 (K % 32 == 0, N % 16 == 0) so that the B fragment of
 // v_mfma_f32_16x16x32_f16 for column block nb and k step ks is 512
 // contiguous bytes: packed[((nb * K/32 + ks) * 64 + l) * 8 + j] =
@@ -537,13 +904,91 @@ int split_plan(int M, int K, int *chunks_per_split) {
 }
 } // namespace
 
+namespace {
+// Shapes w8a16_dec_kernel takes: M <= 64, K a multiple of 128 up to 4096
+// (whole chunks, four per wave), byte ranges within its 32-bit buffer offsets.
+bool dec_ok(int M, int K, const W8A16Seg *segs, int nseg) {
+    if (M > kDecRows || K > kDecMaxK || K % 128 != 0) return false;
+    for (int i = 0; i < nseg; ++i)
+        if ((int64_t)segs[i].n * K >= ((int64_t)1 << 31)) return false;
+    return true;
+}
+
+// Plan of w8a16_dec_kernel (M <= kDecRows): row halves, and the smallest
+// column-tile width (1..4 blocks; 1..2 for gs < 128) whose tiles x halves fit
+// one workgroup per CU.
+struct DecPlan {
+    int halves = 1, cb = 1, tiles = 0, blocks = 0;
+};
+DecPlan dec_plan(int M, int gs, const W8A16Seg *segs, int nseg) {
+    DecPlan p;
+    for (int i = 0; i < nseg; ++i) p.blocks += segs[i].n / 16;
+    p.halves = M > kDecHalf ? 2 : 1;
+    const int cus = device_cus();
+    const int cbmax = gs >= 128 ? 4 : 2; // (several folds per chunk hold more registers)
+    p.cb = 1;
+    while (p.cb < cbmax && (int64_t)((p.blocks + p.cb - 1) / p.cb) * p.halves > cus) ++p.cb;
+    p.tiles = (p.blocks + p.cb - 1) / p.cb;
+    return p;
+}
+} // namespace
+
 size_t w8a16_workspace_floats(int M, int K, int gs, const W8A16Seg *segs, int nseg) {
-    if (!w8a16_mfma_ok(K, gs, segs, nseg)) return 0;
+    if (!w8a16_mfma_ok(K, gs, segs, nseg) || dec_ok(M, K, segs, nseg)) return 0;
     int ntot = 0;
     for (int i = 0; i < nseg; ++i) ntot += segs[i].n;
     const int splits = split_plan(M, K, nullptr);
     return splits > 1 ? (size_t)splits * M * ntot : 0;
 }
+
+namespace {
+// The decode-sized launch: g's x, shape, segments and cache rows are set.
+void launch_dec(const GemmArgs &g, int gs, hipStream_t stream, bool packed) {
+    DecArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = g.x;
+    a.ldx = g.ldx;
+    a.M = g.M;
+    a.K = g.K;
+    a.gs = gs;
+    a.nseg = g.nseg;
+    for (int i = 0; i < g.nseg; ++i) a.seg[i] = g.seg[i];
+    for (int i = 0; i <= g.nseg; ++i) a.col0[i] = g.col0[i];
+    a.cache = g.cache;
+    const DecPlan p = dec_plan(g.M, gs, g.seg, g.nseg);
+    a.tiles = p.tiles;
+    a.tpx = (p.tiles + 7) / 8;
+    a.halves = p.halves;
+    a.blocks = p.blocks;
+    const unsigned grid = (unsigned)(8 * a.tpx * p.halves);
+    const int      fs = gs >= 128 ? 4 : gs / 32;
+    profile_begin(KernelId::W8A16, stream);
+#define TL_W8_DEC(FS, CB)                                                                                  \
+    do {                                                                                                   \
+        if (packed)                                                                                        \
+            hipLaunchKernelGGL((w8a16_dec_kernel<FS, CB, true>), dim3(grid), dim3(512), 0, stream, a);     \
+        else                                                                                               \
+            hipLaunchKernelGGL((w8a16_dec_kernel<FS, CB, false>), dim3(grid), dim3(512), 0, stream, a);    \
+    } while (0)
+    if (fs == 4) {
+        switch (p.cb) {
+        case 1: TL_W8_DEC(4, 1); break;
+        case 2: TL_W8_DEC(4, 2); break;
+        case 3: TL_W8_DEC(4, 3); break;
+        default: TL_W8_DEC(4, 4); break;
+        }
+    } else if (fs == 2) {
+        if (p.cb == 1) TL_W8_DEC(2, 1);
+        else TL_W8_DEC(2, 2);
+    } else {
+        if (p.cb == 1) TL_W8_DEC(1, 1);
+        else TL_W8_DEC(1, 2);
+    }
+#undef TL_W8_DEC
+    HIP_CHECK(hipGetLastError());
+    profile_end(KernelId::W8A16, stream);
+}
+} // namespace
 
 void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A16Seg *segs, int nseg,
                   const CacheRows *cache, float *workspace, hipStream_t stream, bool packed) {
@@ -582,6 +1027,10 @@ void launch_w8a16(const __half *x, int64_t ldx, int M, int K, int gs, const W8A1
                            stream, a);
         HIP_CHECK(hipGetLastError());
         profile_end(KernelId::W8A16, stream);
+        return;
+    }
+    if (dec_ok(M, K, segs, nseg)) {
+        launch_dec(a, gs, stream, packed);
         return;
     }
     const int mt = (M + kBM - 1) / kBM;
