@@ -65,7 +65,10 @@ __device__ __forceinline__ __attribute__((address_space(3))) s16x4 *lds_ptr(cons
 
 // Threads per workgroup: 8 waves (two per SIMD, one workgroup per CU) up to
 // head_dim 128, so each K/V tile in LDS serves 256 query rows; 4 waves for
-// head_dim 256, whose register file allows one wave per SIMD.
+// head_dim 256, whose register file allows one wave per SIMD.  (Head_dim 128
+// with 4 waves of three 16-row groups each -- a third less LDS read traffic
+// per flop, one wave per SIMD -- was 1.5x slower: the second wave on each
+// SIMD hides the LDS and MFMA latencies.)
 template <int D>
 constexpr int kPThreads = D <= 128 ? 512 : 256;
 // Lazy rescaling threshold of the online softmax, in log2 units.
@@ -147,6 +150,7 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
     constexpr int NT = kPThreads<D>;        // threads
     constexpr int NW = NT / 64;             // waves
     constexpr int ROWS = NW * 16 * NQG;     // query rows per workgroup
+    static_assert(ROWS == prefill_rows(D), "the planner's query tile");
     constexpr int BQ = ROWS / G;            // query tokens per workgroup
     constexpr int KS = D / 32;              // k steps of S^T
     constexpr int DT = D / 16;              // dim tiles of O^T
@@ -159,10 +163,20 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
     // not wait for it before computing.
     __shared__ __align__(16) uint16_t ks0[kKeyTile * ROWH], ks1[kKeyTile * ROWH];
     __shared__ __align__(16) uint16_t vt0[kKeyTile * ROWH], vt1[kKeyTile * ROWH];
-    // 16-byte piece x of key row r sits at slot x ^ (r % KP) of the row: the
-    // 16 rows a fragment read touches then fall on distinct banks without
+    // 16-byte piece x of key row r sits at slot x ^ swz(r) of the row, where
+    // swz is the XOR-linear map r -> 2 r0 ^ 4 r1 ^ 9 r2 ^ 8 r3 of the row's
+    // low four bits (mod KP; r mod 4 for KP 4).  Reads then touch distinct
+    // banks whether the LDS serves 128 or 256 bytes a cycle: the 8 or 16
+    // rows of a K fragment read (one piece each), and the two adjacent
+    // pieces of the 4 or 8 rows a transposing V read touches (with
+    // x ^ (r % KP), rows r and r ^ 1 put that pair on the same banks).  No
     // padding, so each wave's DMA of 1 KB lands contiguous.
-    auto slot = [](int r, int x) { return r * KP + (x ^ (r & (KP - 1))); };
+    auto swz = [](int r) {
+        if constexpr (KP <= 4) return r & (KP - 1);
+        const int f = ((r & 3) << 1) ^ (((r >> 2) & 1) * 9) ^ (((r >> 3) & 1) << 3);
+        return f & (KP - 1);
+    };
+    auto slot = [&](int r, int x) { return r * KP + (x ^ swz(r)); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int item = blockIdx.x / a.Hkv;
@@ -227,7 +241,7 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
     // Tile kt of K and V straight from global memory into LDS buffer buf
     // (global_load_lds, 16 bytes per lane): thread t fills slots
     // u*256 + t, i.e. every wave instruction one contiguous 1 KB of the tile;
-    // slot s holds row s / KP, piece (s % KP) ^ (row % KP).  Completion is
+    // slot s holds row s / KP, piece (s % KP) ^ swz(row).  Completion is
     // tracked by vmcnt.
     auto issue_tile = [&](int kt, uint16_t *kdst, uint16_t *vdst) {
         const int t0 = kt * kKeyTile;
@@ -235,7 +249,7 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
         for (int u = 0; u < NKI; ++u) {
             const int sl = u * NT + tid;
             if (NKI * NT > PIECES && sl >= PIECES) break; // whole waves (PIECES % 64 == 0)
-            const int r = sl / KP, x = (sl % KP) ^ (r & (KP - 1));
+            const int r = sl / KP, x = (sl % KP) ^ swz(r);
             const int t = min(t0 + r, kend - 1);
             const char *ks, *vs;
             if (a.new_k && t >= p0) { // a new token: its row in the fused append's input

@@ -31,9 +31,11 @@ struct PrefillEntry {
 
 static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
 
-// Query tokens per workgroup: 256 query rows (8 waves; 64 rows, 4 waves, for
-// head_dim 256) of (token, head) pairs, G heads of one kv group per token.
-inline int prefill_block_tokens(int D, int G) { return (D <= 128 ? 256 : 64) / G; }
+// Query rows (token, head) per workgroup: 256 up to head_dim 128 (8 waves x
+// 2 groups of 16), 64 at 256 (4 waves x 1).
+constexpr int prefill_rows(int D) { return D <= 128 ? 256 : 64; }
+// Query tokens per workgroup: G heads of one kv group per token.
+inline int prefill_block_tokens(int D, int G) { return prefill_rows(D) / G; }
 
 // Work items (entry, query tile), most keys first (LPT order for the
 // hardware dispatcher), each a self-contained record of kPrefillItemWords
