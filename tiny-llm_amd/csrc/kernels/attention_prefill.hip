@@ -63,6 +63,23 @@ __device__ __forceinline__ __attribute__((address_space(3))) s16x4 *lds_ptr(cons
     return (__attribute__((address_space(3))) s16x4 *)(p);
 }
 
+// max(x of lane l, x of lane l ^ S) for S = 16 or 32, on the VALU: the
+// gfx950 lane swaps (v_permlane16_swap / v_permlane32_swap) of x with itself
+// give every lane its own value in one result and its partner's in the other
+// (rows of 16 lanes: odd rows with even ones, or the two halves of the wave).
+template <int S>
+__device__ __forceinline__ float xor_lane_max(float x) {
+    static_assert(S == 16 || S == 32, "a row or half-wave swap");
+    const unsigned u = __float_as_uint(x);
+    if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+}
+
 // Threads per workgroup: 8 waves (two per SIMD, one workgroup per CU) up to
 // head_dim 128, so each K/V tile in LDS serves 256 query rows; 4 waves for
 // head_dim 256, whose register file allows one wave per SIMD.  (Head_dim 128
@@ -346,8 +363,8 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
                                fmaxf(fmaxf(s[j][1][0], s[j][1][1]), fmaxf(s[j][1][2], s[j][1][3])));
             mloc = fmaxf(mloc, fmaxf(fmaxf(fmaxf(s[j][2][0], s[j][2][1]), fmaxf(s[j][2][2], s[j][2][3])),
                                      fmaxf(fmaxf(s[j][3][0], s[j][3][1]), fmaxf(s[j][3][2], s[j][3][3]))));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            mloc = xor_lane_max<16>(mloc);
+            mloc = xor_lane_max<32>(mloc);
             // Key 0 lies in tile 0 and every query attends it, so the max is
             // finite from the first tile on.  The reference point m_run only
             // moves when the max passes it by more than kLazyMax (log2
