@@ -229,6 +229,65 @@ __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float acc) {
                                   false);
 }
 
+// The G heads' scores over the lane's 8 fp16 pairs of k, accumulated in fp32
+// in pair order: d[h] = dot2(q_h.w, k.w, dot2(q_h.z, k.z, dot2(q_h.y, k.y,
+// dot2(q_h.x, k.x, 0)))), as the builtin chains give.  Written out so that
+// each chain starts with the three-operand v_dot2_f32_f16 and an inline zero:
+// from the builtin the compiler starts every chain with a v_mov of 0 for the
+// two-operand accumulating v_dot2c_f32_f16 (one VALU instruction per chain).
+// One statement per pair position, the G chains interleaved: a v_dot2c may
+// read the v_dot2 result it accumulates only 3 wait states after it, which
+// G - 1 >= 3 other instructions provide (an s_nop for G = 2); same-opcode
+// v_dot2c chains need none; the closing s_nop covers the compiler's next
+// reader of d, which does not see what the statement holds.
+template <int G>
+__device__ __forceinline__ void dot_heads(const uint4 (&q)[G], const uint4 &k, float (&d)[G]);
+template <>
+__device__ __forceinline__ void dot_heads<2>(const uint4 (&q)[2], const uint4 &k, float (&d)[2]) {
+    asm("v_dot2_f32_f16 %0, %2, %4, 0\n\tv_dot2_f32_f16 %1, %3, %4, 0\n\ts_nop 1"
+        : "=&v"(d[0]), "=&v"(d[1])
+        : "v"(q[0].x), "v"(q[1].x), "v"(k.x));
+    asm("v_dot2c_f32_f16 %0, %2, %4\n\tv_dot2c_f32_f16 %1, %3, %4"
+        : "+v"(d[0]), "+v"(d[1])
+        : "v"(q[0].y), "v"(q[1].y), "v"(k.y));
+    asm("v_dot2c_f32_f16 %0, %2, %4\n\tv_dot2c_f32_f16 %1, %3, %4"
+        : "+v"(d[0]), "+v"(d[1])
+        : "v"(q[0].z), "v"(q[1].z), "v"(k.z));
+    asm("v_dot2c_f32_f16 %0, %2, %4\n\tv_dot2c_f32_f16 %1, %3, %4\n\ts_nop 2"
+        : "+v"(d[0]), "+v"(d[1])
+        : "v"(q[0].w), "v"(q[1].w), "v"(k.w));
+}
+template <>
+__device__ __forceinline__ void dot_heads<4>(const uint4 (&q)[4], const uint4 &k, float (&d)[4]) {
+    asm("v_dot2_f32_f16 %0, %4, %8, 0\n\tv_dot2_f32_f16 %1, %5, %8, 0\n\tv_dot2_f32_f16 %2, %6, %8, 0\n\tv_dot2_f32_f16 %3, %7, %8, 0"
+        : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3])
+        : "v"(q[0].x), "v"(q[1].x), "v"(q[2].x), "v"(q[3].x), "v"(k.x));
+    asm("v_dot2c_f32_f16 %0, %4, %8\n\tv_dot2c_f32_f16 %1, %5, %8\n\tv_dot2c_f32_f16 %2, %6, %8\n\tv_dot2c_f32_f16 %3, %7, %8"
+        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3])
+        : "v"(q[0].y), "v"(q[1].y), "v"(q[2].y), "v"(q[3].y), "v"(k.y));
+    asm("v_dot2c_f32_f16 %0, %4, %8\n\tv_dot2c_f32_f16 %1, %5, %8\n\tv_dot2c_f32_f16 %2, %6, %8\n\tv_dot2c_f32_f16 %3, %7, %8"
+        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3])
+        : "v"(q[0].z), "v"(q[1].z), "v"(q[2].z), "v"(q[3].z), "v"(k.z));
+    asm("v_dot2c_f32_f16 %0, %4, %8\n\tv_dot2c_f32_f16 %1, %5, %8\n\tv_dot2c_f32_f16 %2, %6, %8\n\tv_dot2c_f32_f16 %3, %7, %8\n\ts_nop 2"
+        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3])
+        : "v"(q[0].w), "v"(q[1].w), "v"(q[2].w), "v"(q[3].w), "v"(k.w));
+}
+template <>
+__device__ __forceinline__ void dot_heads<8>(const uint4 (&q)[8], const uint4 &k, float (&d)[8]) {
+    asm("v_dot2_f32_f16 %0, %8, %16, 0\n\tv_dot2_f32_f16 %1, %9, %16, 0\n\tv_dot2_f32_f16 %2, %10, %16, 0\n\tv_dot2_f32_f16 %3, %11, %16, 0\n\tv_dot2_f32_f16 %4, %12, %16, 0\n\tv_dot2_f32_f16 %5, %13, %16, 0\n\tv_dot2_f32_f16 %6, %14, %16, 0\n\tv_dot2_f32_f16 %7, %15, %16, 0"
+        : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]), "=&v"(d[6]), "=&v"(d[7])
+        : "v"(q[0].x), "v"(q[1].x), "v"(q[2].x), "v"(q[3].x), "v"(q[4].x), "v"(q[5].x), "v"(q[6].x), "v"(q[7].x), "v"(k.x));
+    asm("v_dot2c_f32_f16 %0, %8, %16\n\tv_dot2c_f32_f16 %1, %9, %16\n\tv_dot2c_f32_f16 %2, %10, %16\n\tv_dot2c_f32_f16 %3, %11, %16\n\tv_dot2c_f32_f16 %4, %12, %16\n\tv_dot2c_f32_f16 %5, %13, %16\n\tv_dot2c_f32_f16 %6, %14, %16\n\tv_dot2c_f32_f16 %7, %15, %16"
+        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]), "+v"(d[6]), "+v"(d[7])
+        : "v"(q[0].y), "v"(q[1].y), "v"(q[2].y), "v"(q[3].y), "v"(q[4].y), "v"(q[5].y), "v"(q[6].y), "v"(q[7].y), "v"(k.y));
+    asm("v_dot2c_f32_f16 %0, %8, %16\n\tv_dot2c_f32_f16 %1, %9, %16\n\tv_dot2c_f32_f16 %2, %10, %16\n\tv_dot2c_f32_f16 %3, %11, %16\n\tv_dot2c_f32_f16 %4, %12, %16\n\tv_dot2c_f32_f16 %5, %13, %16\n\tv_dot2c_f32_f16 %6, %14, %16\n\tv_dot2c_f32_f16 %7, %15, %16"
+        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]), "+v"(d[6]), "+v"(d[7])
+        : "v"(q[0].z), "v"(q[1].z), "v"(q[2].z), "v"(q[3].z), "v"(q[4].z), "v"(q[5].z), "v"(q[6].z), "v"(q[7].z), "v"(k.z));
+    asm("v_dot2c_f32_f16 %0, %8, %16\n\tv_dot2c_f32_f16 %1, %9, %16\n\tv_dot2c_f32_f16 %2, %10, %16\n\tv_dot2c_f32_f16 %3, %11, %16\n\tv_dot2c_f32_f16 %4, %12, %16\n\tv_dot2c_f32_f16 %5, %13, %16\n\tv_dot2c_f32_f16 %6, %14, %16\n\tv_dot2c_f32_f16 %7, %15, %16\n\ts_nop 2"
+        : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]), "+v"(d[6]), "+v"(d[7])
+        : "v"(q[0].w), "v"(q[1].w), "v"(q[2].w), "v"(q[3].w), "v"(q[4].w), "v"(q[5].w), "v"(q[6].w), "v"(q[7].w), "v"(k.w));
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
@@ -373,13 +432,7 @@ struct ValuScorer {
     __device__ __forceinline__ void step(int s, uint4 k, bool valid, float scale_log2) {
         if constexpr (XP) {
             float d[G];
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                d[h] = fdot2(qv[h].x, k.x, 0.0f);
-                d[h] = fdot2(qv[h].y, k.y, d[h]);
-                d[h] = fdot2(qv[h].z, k.z, d[h]);
-                d[h] = fdot2(qv[h].w, k.w, d[h]);
-            }
+            dot_heads<G>(qv, k, d);
             constexpr int N0 = LPR == 16 ? G : 2 * G; // slots before the p ^ 7 step
             if constexpr (LPR == 16) xpose_step<0x140, G>(d); // row_mirror: p ^ 15
             xpose_step<0x141, (N0 / 2 > 1 ? N0 / 2 : 1)>(d);     // row_half_mirror: p ^ 7
