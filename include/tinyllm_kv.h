@@ -347,11 +347,29 @@ int tl_attn_get_score_path(void);
 int tl_attn_set_waves(int waves);
 int tl_attn_get_waves(void);
 
+/* Head-fused decode plans, process-wide: 0 = auto, 1 = off, 2 / 4 / 8 =
+ * that many kv heads per workgroup where a plan with it applies.  A
+ * head-fused plan (head_dim 128, the VALU score path, waves not forced to 4,
+ * lengths within 10% of the longest, kv heads a multiple of H, at most one
+ * (sequence, H-head block) per CU) gives one 8-wave workgroup H kv heads of
+ * a work item -- wave w head w % H, tile slice w / H -- so it reads H heads'
+ * pieces of each token row at once, and a sequence's work items interleave
+ * its 64-token tiles.  Auto takes the H in {8, 4, 2} with the fewest items
+ * per sequence (one item: no merge launch), the larger H on a tie.  Initial
+ * value from the environment variable TL_ATTN_HF ("0" = off, "2" / "4" /
+ * "8", else auto).  Every setting gives results within the same 1e-3 gate.
+ * No reference counterpart (tuning knob). */
+int tl_attn_set_head_fuse(int mode);
+int tl_attn_get_head_fuse(void);
+
 /* The launch plan the decode attention entry points (tl_kv_batch_attention,
  * tl_kv_batch_decode, tl_attn_decode_gqa) make for attended lengths
  * seq_lens[0..n) on a device of num_cus compute units -- host only, no GPU
  * needed.  forced_chunk: 0, or a multiple of 256 tokens as TL_ATTN_CHUNK
- * would force; waves_setting: 0 (auto), 4 or 8 as tl_attn_set_waves.
+ * would force; waves_setting: 0 (auto), 4 or 8 as tl_attn_set_waves;
+ * head_fuse: 0 (per-head plans only), 1 (head-fused where it applies, as the
+ * entry points do for head_dim 128 on the VALU score path), or 2 / 4 / 8
+ * (that many kv heads per workgroup).
  * with_rows != 0 counts the slot row per entry that DecodeBatch passes.
  * Optional outputs: part_base[n + 1] (first partial row of each entry) and
  * work[2 * work_items] ((entry, chunk) pairs in launch order, longest
@@ -369,10 +387,14 @@ typedef struct tl_attn_plan_info {
     int inline_compact;/* 1: the compact encoding (one chunk per sequence; 16-bit
                           lengths and slots: one word per sequence + 16 bits
                           per work item) */
+    int head_fused;    /* kv heads per workgroup of a head-fused plan (2, 4 or 8;
+                          a sequence's work items interleave its tiles,
+                          chunk_tokens is the longest length rounded up, work
+                          is in chunk-major order), 0: per-head plan */
 } tl_attn_plan_info;
 int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
-                 int waves_setting, int with_rows, tl_attn_plan_info *info, int32_t *part_base,
-                 int32_t *work);
+                 int waves_setting, int head_fuse, int with_rows, tl_attn_plan_info *info,
+                 int32_t *part_base, int32_t *work);
 
 /* ------------------------------------------------------------------------
  * Kernel timing (the reference has only an unused CudaEvent wrapper,

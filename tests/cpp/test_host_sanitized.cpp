@@ -29,24 +29,48 @@ using namespace tiny_llm::detail;
 
 static void planner_random() {
     std::mt19937_64 rng(20261201);
-    for (int it = 0; it < 400; ++it) {
-        const int n = (int)(rng() % 700);
+    int             fused = 0;
+    for (int it = 0; it < 600; ++it) {
+        // every fifth plan: near-uniform lengths, up to one 8-head group per CU
+        const int n = it % 5 == 4 ? 1 + (int)(rng() % 128) : (int)(rng() % 700);
         std::vector<int32_t> lens((size_t)n);
         const int kind = it % 4;
         for (auto &l : lens) {
-            if (kind == 0) l = (int32_t)(rng() % 65536);
+            if (it % 5 == 4) l = (int32_t)(7400 + rng() % 800);
+            else if (kind == 0) l = (int32_t)(rng() % 65536);
             else if (kind == 1) l = (int32_t)(1 + rng() % 300);
             else if (kind == 2) l = 8193;
             else l = (int32_t)(rng() % 40000);
         }
-        const int hkv = 1 << (rng() % 6);
-        const int cus = 1 + (int)(rng() % 300);
+        int hkv = 1 << (rng() % 6);
+        int cus = 1 + (int)(rng() % 300);
+        if (it % 5 == 4) { // CUs a multiple of the 8-head groups, or a few more
+            hkv = 8 << (rng() % 2);
+            const int groups = n * hkv / 8;
+            cus = groups * (1 + (int)(rng() % 4)) + (int)(rng() % 3);
+        }
         const int forced = (rng() % 3 == 0) ? 256 * (1 + (int)(rng() % 40)) : 0;
+        const int fuse = (int)(rng() % 2) ? 1 << (rng() % 4) : 0; // 0, or 1 (auto), 2, 4, 8
         WorkList wl;
-        plan_work_list(n ? lens.data() : nullptr, n, hkv, cus, forced, wl);
+        plan_work_list(n ? lens.data() : nullptr, n, hkv, cus, forced, fuse, wl);
         CHECK(wl.chunk % kPlanQuantum == 0 && wl.chunk >= kPlanQuantum);
         CHECK((int)wl.part_base.size() == n + 1);
         CHECK((int)wl.work.size() == 2 * wl.n_work);
+        if (wl.fused_heads) { // interleaved items, chunk-major order
+            const int hpw = wl.fused_heads;
+            CHECK(fuse && !forced && n > 0 && hkv % hpw == 0 && !wl.any_empty);
+            CHECK(hpw == 2 || hpw == 4 || hpw == 8);
+            const int nch = wl.n_work / n;
+            CHECK(nch >= 1 && nch <= kPlanFusedMaxItems && wl.n_work == n * nch);
+            CHECK(wl.any_multi == (nch > 1));
+            CHECK((int64_t)n * (hkv / hpw) * nch <= cus);
+            for (int w = 0; w < wl.n_work; ++w)
+                CHECK(wl.work[2 * (size_t)w] == w % n && wl.work[2 * (size_t)w + 1] == w / n);
+            for (int i = 0; i <= n; ++i) CHECK(wl.part_base[(size_t)i] == i * nch);
+            for (int i = 0; i < n; ++i) CHECK(lens[(size_t)i] >= 1 && lens[(size_t)i] <= wl.chunk);
+            ++fused;
+            continue;
+        }
         std::vector<int> seen((size_t)wl.n_work, 0);
         int prev = INT32_MAX;
         for (int w = 0; w < wl.n_work; ++w) {
@@ -84,7 +108,8 @@ static void planner_random() {
         const int nw = plan_waves((int64_t)wl.n_work * hkv, cus, 0);
         CHECK(nw == 4 || nw == 8);
     }
-    std::printf("ok planner_random\n");
+    CHECK(fused > 10);
+    std::printf("ok planner_random (%d head-fused plans)\n", fused);
 }
 
 static uint16_t rnd_h(std::mt19937_64 &rng) {

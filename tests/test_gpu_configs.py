@@ -2,7 +2,8 @@
 against the oracle.
 
 The bench times the decode kernel on plans that small tests do not reach:
-cfg3's 8448-token chunks (17 tiles per wave of an 8-wave workgroup), cfg2's
+cfg3's head-fused plan (an 8-wave workgroup per sequence and kv head pair,
+each wave a quarter of the sequence's tiles of one head), cfg2's
 4096-token chunks, cfg4's 3328-token chunks over a permuted 16-token block
 map of a pool larger than 4 GiB, cfg5's ~4600-token chunks over a block pool
 with hundreds of group-8 sequences and the compact metadata encoding.  Each
@@ -113,9 +114,12 @@ def test_cfg3_full_size(tl, orc):
         S = ctx + 1  # attended: the context plus the token this step appends
         batch.prepare(ids, stream())
         info = batch.info()
+        # head-fused: one 8-wave workgroup per (sequence, kv head pair), 256
+        # in all, one per CU; the whole sequence per workgroup, no merge
         assert info["chunk_tokens"] == 8448 and info["work_items"] == 64
-        plan = tl.attn_plan(np.full(B, S, np.int32), Hkv, num_cus=cus())
-        assert (plan["chunk_tokens"], plan["work_items"], plan["waves"]) == (8448, 64, 8)
+        plan = tl.attn_plan(np.full(B, S, np.int32), Hkv, num_cus=cus(), head_fuse=True)
+        assert (plan["chunk_tokens"], plan["work_items"], plan["waves"], plan["head_fused"],
+                plan["any_multi"]) == (8448, 64, 8, 2, 0)
         q = randn(gen, (B, Hq, D))
         nk = randn(gen, (B, Hkv * D))
         nv = randn(gen, (B, Hkv * D))

@@ -1,0 +1,165 @@
+"""GPU: head-fused decode plans.  One 8-wave workgroup takes H kv heads of a
+work item (wave w: head w % H, tile slice w / H), so it reads H heads'
+pieces of each token row at once, and a sequence's work items interleave its
+64-token tiles; split sequences are combined by the merge launch.
+
+Checked for H = 2, 4 and 8 and the planner's own choice, every group size,
+contiguous and paged caches, one to eight items per sequence:
+  - one decode step (append + attention) against the oracle: attention
+    <= 1e-3 normwise (test_transformer.cu:80-92), cache bytes bit-exact;
+  - the same step on the per-head kernel (head fusing off) within the same
+    1e-3 of the oracle, and the head-fused step run twice giving the same
+    bits;
+  - tl_attn_decode_gqa (the library's shared workspace) over two head-fused
+    plans in a row."""
+import zlib
+
+import numpy as np
+import pytest
+
+from devutil import empty_dev, read_dev, rel_err, stream, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+@pytest.fixture
+def head_fuse(tl):
+    before = tl.get_head_fuse()
+    yield tl.set_head_fuse
+    tl.set_head_fuse(before)
+
+
+def cus():
+    import torch
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def f16bits(rng, n):
+    return rng.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+# (heads per workgroup setting: 0 = the planner's choice, kv heads, batch,
+#  context range, group, paged) -> (heads per workgroup, items per sequence)
+# on 256 CUs
+RUNS = [
+    ((2, 8, 64, (2048, 2250), 4, False), (2, 1)),
+    ((2, 8, 64, (2048, 2250), 8, True), (2, 1)),
+    ((2, 8, 32, (4096, 4300), 2, False), (2, 2)),
+    ((4, 8, 128, (1024, 1100), 4, True), (4, 1)),
+    ((4, 8, 64, (2048, 2250), 1, False), (4, 2)),
+    ((8, 8, 256, (200, 220), 4, False), (8, 1)),
+    ((8, 8, 64, (2048, 2250), 2, True), (8, 4)),
+    ((8, 16, 16, (4096, 4400), 4, False), (8, 8)),
+    ((0, 8, 80, (1600, 1700), 4, True), (8, 3)),
+    ((0, 8, 64, (2048, 2250), 8, False), (2, 1)),
+]
+
+
+@pytest.mark.parametrize("run,expect", RUNS, ids=[
+    "h{}-hkv{}-b{}-g{}-{}".format(r[0], r[1], r[2], r[4], "paged" if r[5] else "slots")
+    for r, _ in RUNS])
+def test_head_fused_decode_step(tl, orc, head_fuse, run, expect):
+    setting, Hkv, B, (lo, hi), G, paged = run
+    rng = np.random.default_rng(zlib.crc32(repr(run).encode()))
+    ctx = rng.integers(lo, hi + 1, B)
+    M = -(-(hi + 1) // 64) * 64
+    slots = B + 1
+    lens = (ctx + 1).astype(np.int32)
+    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or 1)
+    nch = plan["work_items"] // B
+    if cus() == 256:
+        assert (plan["head_fused"], nch) == expect
+    assert plan["head_fused"] in (2, 4, 8) and nch * B == plan["work_items"]
+
+    g = tl.KVCacheManager(1, Hkv, D, M, slots)
+    o = orc.KVCacheOracle(1, Hkv, D, M, slots)
+    if paged:
+        perm = rng.permutation(slots * (M // 16)).astype(np.int32)
+        assert g.setBlockMap(16, perm) is None
+    ids = []
+    for S in ctx:
+        sid, err = g.allocateSequence(M)
+        assert err is None, err
+        o.allocate(M)
+        k, v = f16bits(rng, int(S) * Hkv * D), f16bits(rng, int(S) * Hkv * D)
+        dk, dv = to_dev(k), to_dev(v)
+        assert g.appendKV(sid, 0, dk.data_ptr(), dv.data_ptr(), int(S), stream()) is None
+        del dk, dv
+        o.append(sid, 0, k, v, int(S))
+        g.advanceSeqLen(sid, int(S))
+        o.advance(sid, int(S))
+        ids.append(sid)
+    Hq = Hkv * G
+    q = f16bits(rng, B * Hq * D).reshape(B, Hq, D)
+    nk, nv = f16bits(rng, B * Hkv * D).reshape(B, -1), f16bits(rng, B * Hkv * D).reshape(B, -1)
+    dq, dnk, dnv = to_dev(q), to_dev(nk), to_dev(nv)
+    scale = 1.0 / np.sqrt(D)
+    batch = tl.DecodeBatch(g, B, Hq)
+
+    def step(mode):
+        head_fuse(mode)
+        batch.prepare(ids, stream())
+        if mode != 1:
+            assert batch.info()["work_items"] == plan["work_items"]
+        out = empty_dev((B, Hq, D))
+        out.fill_(float("nan"))
+        batch.decode(0, dq.data_ptr(), dnk.data_ptr(), dnv.data_ptr(), out.data_ptr(), scale,
+                     stream())
+        return to_host(out)
+
+    fused = step(setting)
+    again = step(setting)  # the same step again: the append rewrites the same bytes
+    per_head = step(1)
+    assert np.array_equal(fused, again), "head-fused step not deterministic"
+
+    for i, sid in enumerate(ids):
+        o.append(sid, 0, nk[i], nv[i], 1)
+    if not paged:
+        assert np.array_equal(read_dev(g.pool(), o.pool().size), o.pool())
+    view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(s) for s in ids])
+    ref32, _ = orc.attn_decode_gqa(q, view, lens, Hq, Hkv, D, scale, nthreads=8)
+    for name, got in (("head-fused", fused), ("per-head", per_head)):
+        g32 = got.view(np.float16).astype(np.float32)
+        errs = [rel_err(g32[b], ref32[b]) for b in range(B)]
+        assert max(errs) <= 1e-3, (name, max(errs))
+    if paged:  # the appended token landed where the block map says
+        smax = int(lens.max())
+        gk = empty_dev((B, Hkv, smax, D))
+        batch.gather(0, gk.data_ptr(), 0, smax, stream())
+        assert np.array_equal(to_host(gk), orc.gather(view, 0, lens, Hkv, D, smax))
+
+
+def test_head_fused_stateless_two_plans_in_a_row(tl, orc, head_fuse):
+    """tl_attn_decode_gqa over a paged view with one slot per block: two
+    items per sequence (partials and the merge launch), then one."""
+    import torch
+    head_fuse(0)
+    Hkv, G = 8, 4
+    Hq = Hkv * G
+    for B, (lo, hi), seed, nch in ((32, (4200, 4400), 1, 2), (64, (2100, 2300), 2, 1)):
+        rng = np.random.default_rng(seed)
+        lens = rng.integers(lo, hi + 1, B).astype(np.int32)
+        p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse=True)
+        assert p["head_fused"] in (2, 4, 8)
+        assert p["work_items"] == B * nch or cus() != 256
+        M = int(hi)
+        pool = f16bits(rng, 2 * B * M * Hkv * D)
+        dpool = to_dev(pool)
+        base = dpool.data_ptr()
+        v_off = B * M * Hkv * D
+        bt = torch.arange(B, dtype=torch.int32, device="cuda").reshape(B, 1)
+        view = tl.KVView(base, base + 2 * v_off, bt.data_ptr(), 1, 30, M * Hkv * D, Hkv * D, D)
+        q = f16bits(rng, B * Hq * D).reshape(B, Hq, D)
+        dq = to_dev(q)
+        out = empty_dev((B, Hq, D))
+        out.fill_(float("nan"))
+        scale = 1.0 / np.sqrt(D)
+        tl.attn_decode_gqa(dq.data_ptr(), view, lens, Hq, Hkv, D, scale, out.data_ptr(), stream())
+        got = to_host(out).view(np.float16).astype(np.float32)
+        oview = orc.View(pool, 0, v_off, np.arange(B, dtype=np.int32).reshape(B, 1), 30,
+                         M * Hkv * D, Hkv * D, D)
+        ref32, _ = orc.attn_decode_gqa(q, oview, lens, Hq, Hkv, D, scale, nthreads=8)
+        errs = [rel_err(got[b], ref32[b]) for b in range(B)]
+        assert max(errs) <= 1e-3, (B, max(errs))

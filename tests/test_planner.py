@@ -73,6 +73,119 @@ def test_benchmark_config_plans(tl, name):
     check_invariants(p, lens, hkv, CUS)
 
 
+# Head-fused plans, which the entry points allow for head_dim 128 on the VALU
+# score path (every benchmark configuration's shape).  cfg3: 64 sequences of
+# 8 kv heads; 2 heads per workgroup gives 256 (sequence, head pair) blocks,
+# one per CU, so one item per sequence (4 heads: 2 items, 8 heads: 4) -- 64
+# items, no merge, metadata 64 + 65 + 2 * 64 + 64 words.  The ragged
+# configurations keep their chunk plans.
+EXPECTED_FUSED = {
+    "cfg3": dict(chunk_tokens=8448, work_items=64, waves=8, any_multi=0, inline_words=321,
+                 head_fused=2),
+    **{k: dict(EXPECTED[k], head_fused=0) for k in ("cfg1", "cfg2", "cfg4", "cfg5")},
+}
+
+
+@pytest.mark.parametrize("name", sorted(EXPECTED_FUSED))
+def test_benchmark_config_plans_head_fused(tl, name):
+    lens, hkv = cases()[name]
+    p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse=True)
+    got = {k: p[k] for k in EXPECTED_FUSED[name]}
+    assert got == EXPECTED_FUSED[name]
+    if p["head_fused"]:
+        check_fused(p, lens, hkv, CUS, *fused_choice(lens, hkv, CUS))
+    else:
+        check_invariants(p, lens, hkv, CUS)
+
+
+def fused_items(lens, hkv, cus, h):
+    """Items per sequence with h kv heads per workgroup, 0 if h does not apply."""
+    if hkv % h:
+        return 0
+    groups = lens.size * hkv // h
+    if groups > cus:
+        return 0
+    nch = min(cus // groups, 8, max(1, int(lens.min()) // (512 * (8 // h))))
+    return nch if groups * nch * 10 >= cus * 9 else 0
+
+
+def fused_choice(lens, hkv, cus, force=1):
+    """(heads per workgroup, items per sequence) of the head-fused plan, or
+    None: lengths within 10% of the longest; forced h, or the h in (8, 4, 2)
+    with the fewest items, the larger h on a tie."""
+    lens = np.asarray(lens, dtype=np.int64)
+    mx, mn = int(lens.max()), int(lens.min())
+    if mn < 1 or mn < mx - mx // 10:
+        return None
+    if force in (2, 4, 8):
+        c = fused_items(lens, hkv, cus, force)
+        return (force, c) if c else None
+    best = None
+    for h in (8, 4, 2):
+        c = fused_items(lens, hkv, cus, h)
+        if c and (best is None or c < best[1]):
+            best = (h, c)
+    return best
+
+
+def check_fused(p, lens, hkv, cus, hpw, nch):
+    lens = np.asarray(lens, dtype=np.int64)
+    n = lens.size
+    assert p["head_fused"] == hpw and p["work_items"] == n * nch
+    assert n * (hkv // hpw) * nch <= cus
+    assert p["chunk_tokens"] == -(-int(lens.max()) // 256) * 256
+    assert p["waves"] == 8 and p["any_multi"] == int(nch > 1) and p["any_empty"] == 0
+    assert np.array_equal(p["part_base"], np.arange(n + 1) * nch)
+    # chunk-major: (0, 0), (1, 0), ..., (n-1, 0), (0, 1), ...
+    want = np.array([(i, c) for c in range(nch) for i in range(n)], dtype=np.int32).reshape(-1, 2)
+    assert np.array_equal(p["work"], want)
+    # slice s of item c takes tiles u, u + nch * S, ... (u = c * S + s, S = 8 / hpw
+    # waves per head): every tile exactly once
+    S = 8 // hpw
+    for L in {int(lens.min()), int(lens.max())}:
+        tiles = -(-L // 64)
+        covered = sorted(t for u in range(nch * S) for t in range(u, tiles, nch * S))
+        assert covered == list(range(tiles))
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_plans_head_fused(tl, seed):
+    rng = np.random.default_rng(1000 + seed)
+    hkv = int(rng.choice([2, 4, 8, 16, 32]))
+    cus = int(rng.choice([80, 256, 304]))
+    groups_max = max(1, cus * 4 // hkv)
+    n = int(rng.integers(1, min(300, groups_max + 20)))
+    top = int(rng.integers(1, 20000))
+    spread = top // 10 if seed % 3 else top // 4  # within 10%, or ragged
+    lens = (top - rng.integers(0, spread + 1, n)).astype(np.int32)
+    force = int(rng.choice([1, 1, 2, 4, 8]))
+    p = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force)
+    choice = fused_choice(lens, hkv, cus, force)
+    if choice:
+        check_fused(p, lens, hkv, cus, *choice)
+    else:
+        assert p["head_fused"] == 0
+        check_invariants(p, lens, hkv, cus)
+    # a forced chunk or forced 4-wave workgroups keep the chunk plan
+    assert tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, forced_chunk=512)["head_fused"] == 0
+    assert tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, waves=4)["head_fused"] == 0
+
+
+def test_head_fused_choice_examples(tl):
+    """Fewest items per sequence, then more heads per workgroup (256 CUs)."""
+    def pick(B, hkv, L):
+        p = tl.attn_plan(np.full(B, L, np.int32), hkv, num_cus=CUS, head_fuse=True)
+        return p["head_fused"], p["work_items"] // B
+    assert pick(64, 8, 8193) == (2, 1)     # cfg3: 256 head-pair blocks
+    assert pick(128, 8, 8193) == (4, 1)    # 256 blocks of 4 heads
+    assert pick(256, 8, 8193) == (8, 1)    # 256 blocks of 8 heads
+    assert pick(32, 8, 8193) == (2, 2)     # 128 head-pair blocks, 2 items each
+    assert pick(80, 8, 8193) == (8, 3)     # only 8 heads fill 90%: 3 x 80 = 240
+    assert pick(64, 4, 8193) == (2, 2)     # 4 kv heads: pairs, 2 items
+    assert pick(64, 8, 600) == (2, 1)      # short sequences: one item still fills
+    assert pick(100, 8, 8193)[0] == 0      # no h fills 90%: per-head plan
+
+
 def check_invariants(p, lens, hkv, cus, forced=0):
     lens = np.asarray(lens, dtype=np.int64)
     n = lens.size

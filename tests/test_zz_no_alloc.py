@@ -77,6 +77,21 @@ def test_noalloc_matches_decode_gqa_twice_then_smaller(tl, orc):
     run_pair(tl, orc, rng, lens2, Hq, Hkv, D)
 
 
+def test_noalloc_head_fused_twice_then_smaller(tl, orc):
+    """Head-fused plans (several kv heads per workgroup): two items per
+    sequence interleaving its tiles (partials in the scratch), then a smaller
+    call with one item per sequence."""
+    rng = np.random.default_rng(20261203)
+    Hq, Hkv, D = 32, 8, 128
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    for B, lo, hi, nch in ((32, 4200, 4400, 2), (64, 2048, 2100, 1)):
+        lens = rng.integers(lo, hi + 1, B).astype(np.int32)
+        p = tl.attn_plan(lens, Hkv, num_cus=ncu, with_rows=False, head_fuse=True)
+        assert p["head_fused"] == 2 or ncu != 256
+        assert p["work_items"] == B * nch or ncu != 256
+        run_pair(tl, orc, rng, lens, Hq, Hkv, D)
+
+
 def test_noalloc_rejects_calls_beyond_the_scratch(tl, monkeypatch):
     """400 split items of 64 heads x (256 + 2) fp32 need 26 MB of partials,
     more than the 16 MiB array: rejected with a clear error, nothing runs."""

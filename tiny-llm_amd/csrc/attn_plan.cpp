@@ -46,8 +46,67 @@ int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, in
     return (int)std::min<int64_t>(std::max<int64_t>(chunk, kPlanQuantum), cap);
 }
 
+namespace {
+
+// Items per entry of a head-fused plan with hpw heads per workgroup, or 0
+// when it does not apply (see plan_head_fused).
+int fused_items(int n, int num_kv_heads, int cus, int mn, int hpw) {
+    if (num_kv_heads % hpw != 0) return 0;
+    const int64_t groups = (int64_t)n * (num_kv_heads / hpw);
+    if (groups > cus) return 0;
+    const int slices = kPlanFusedWaves / hpw; // waves per head
+    const int nch = (int)std::min<int64_t>(std::min<int64_t>(cus / groups, kPlanFusedMaxItems),
+                                           std::max(1, mn / (8 * kPlanTile * slices)));
+    return groups * nch * 10 >= (int64_t)cus * 9 ? nch : 0;
+}
+
+} // namespace
+
+bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int head_fuse,
+                     WorkList &out) {
+    if (!head_fuse || !lens || n <= 0 || cus <= 0) return false;
+    int mx = 0, mn = INT_MAX;
+    for (int i = 0; i < n; ++i) {
+        mx = std::max(mx, (int)lens[i]);
+        mn = std::min(mn, (int)lens[i]);
+    }
+    if (mn < 1 || mn < mx - mx / 10) return false;
+    int hpw = 0, nch = 0;
+    if (head_fuse == 2 || head_fuse == 4 || head_fuse == 8) {
+        hpw = head_fuse;
+        nch = fused_items(n, num_kv_heads, cus, mn, hpw);
+    } else {
+        for (const int h : {8, 4, 2}) { // fewest items; more heads on a tie
+            const int c = fused_items(n, num_kv_heads, cus, mn, h);
+            if (c && (!nch || c < nch)) {
+                hpw = h;
+                nch = c;
+            }
+        }
+    }
+    if (!nch) return false;
+    out.fused_heads = hpw;
+    out.chunk = std::max(kPlanQuantum, (mx + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum);
+    out.max_len = mx;
+    out.any_multi = nch > 1;
+    out.any_empty = false;
+    out.n_work = n * nch;
+    out.part_base.resize((size_t)n + 1);
+    for (int i = 0; i <= n; ++i) out.part_base[(size_t)i] = i * nch;
+    out.work.resize(2 * (size_t)out.n_work);
+    size_t w = 0;
+    for (int c = 0; c < nch; ++c)
+        for (int i = 0; i < n; ++i) {
+            out.work[w++] = i;
+            out.work[w++] = c;
+        }
+    return true;
+}
+
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
-                    WorkList &out) {
+                    int head_fuse, WorkList &out) {
+    if (forced_chunk == 0 && plan_head_fused(lens, n, num_kv_heads, cus, head_fuse, out)) return;
+    out.fused_heads = 0;
     out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
     out.part_base.assign((size_t)std::max(n, 0) + 1, 0);
     out.any_multi = false;

@@ -14,17 +14,25 @@ namespace detail {
 constexpr int kPlanTile = 64;                  // tokens per wave tile
 constexpr int kPlanQuantum = 4 * kPlanTile;    // chunk lengths are multiples of this
 constexpr int kPlanSlotsPerCU = 2;             // resident 4-wave workgroups per CU
+constexpr int kPlanFusedWaves = 8;             // waves of a head-fused workgroup
+constexpr int kPlanFusedMaxItems = 8;          // head-fused items per entry, at most
 
 // Host side of a ragged plan: chunk length, per-entry partial-row bases and
 // the (entry, chunk) work list in longest-first order, so the hardware
 // dispatcher, which hands workgroups to CUs as they free up, schedules the
 // longest items first (LPT list scheduling).
+// Head-fused plans (fused_heads = H > 0): an 8-wave workgroup takes H kv
+// heads of an item (wave w: head w % H, tile slice w / H), and the nch items
+// of an entry interleave its 64-token tiles in nch * 8 / H slices instead of
+// taking chunks; `chunk` is then the longest length rounded up to the
+// quantum and the work list is in chunk-major order.
 struct WorkList {
     int                  chunk = 256;
     int                  n_work = 0;
     int                  max_len = 0;
     bool                 any_multi = false;
     bool                 any_empty = false;
+    int                  fused_heads = 0;
     std::vector<int32_t> part_base; // n + 1
     std::vector<int32_t> work;      // 2 * n_work
 };
@@ -37,9 +45,26 @@ struct WorkList {
 int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int cus,
                int forced_chunk);
 
-// The whole ragged plan (chunk, part_base, work list) for lens[0..n).
+// The head-fused plan when it applies: head_fuse != 0 (the kernel has a
+// head-fused form for this shape; 2, 4 or 8 force that many kv heads per
+// workgroup, 1 lets the planner choose), lengths within 10% of the longest
+// and at least 1.  With H heads per workgroup (H dividing num_kv_heads) and
+// g = n * num_kv_heads / H (entry, head block) pairs, at most `cus`, each
+// entry gets nch = cus / g interleaved items (one workgroup per CU, the
+// launch one round), fewer if the shortest length has under 8 tiles per
+// wave, at most kPlanFusedMaxItems; H applies only when g * nch fills at
+// least 90% of the CUs.  The planner's choice is the H in {8, 4, 2} with the
+// fewest items per entry (one: no merge launch), the larger H on a tie.
+// Items are listed chunk-major, (entry 0, item 0), (entry 1, item 0), ...;
+// the launch deals the head blocks of the item list out item-fastest.
+// Returns false (out untouched) when no H applies.
+bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int head_fuse,
+                     WorkList &out);
+
+// The whole ragged plan (chunk, part_base, work list) for lens[0..n): the
+// head-fused plan when it applies and no chunk is forced, else chunks.
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
-                    WorkList &out);
+                    int head_fuse, WorkList &out);
 
 // Waves per workgroup for a launch of `workgroups` workgroups: setting 4 or 8
 // forces it; 0 (auto) gives 8 when every CU gets at most two workgroups in

@@ -503,9 +503,19 @@ int tl_attn_set_waves(int waves) {
 
 int tl_attn_get_waves(void) { return tiny_llm::detail::waves(); }
 
+int tl_attn_set_head_fuse(int mode) {
+    if (mode != 0 && mode != 1 && mode != 2 && mode != 4 && mode != 8)
+        return fail(TL_ERR_INVALID,
+                    "tl_attn_set_head_fuse: mode must be 0 (auto), 1 (off), 2, 4 or 8 (heads per workgroup)");
+    tiny_llm::detail::set_head_fuse(mode);
+    return TL_OK;
+}
+
+int tl_attn_get_head_fuse(void) { return tiny_llm::detail::head_fuse(); }
+
 int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
-                 int waves_setting, int with_rows, tl_attn_plan_info *info, int32_t *part_base,
-                 int32_t *work) {
+                 int waves_setting, int head_fuse, int with_rows, tl_attn_plan_info *info,
+                 int32_t *part_base, int32_t *work) {
     if (!info) return fail(TL_ERR_INVALID, "tl_attn_plan: info is null");
     if (n < 0 || (n > 0 && !seq_lens)) return fail(TL_ERR_INVALID, "tl_attn_plan: invalid lengths");
     if (num_kv_heads <= 0 || num_cus <= 0)
@@ -517,12 +527,17 @@ int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, 
     return guarded([&] {
         namespace d = tiny_llm::detail;
         d::WorkList wl;
-        d::plan_work_list(seq_lens, n, num_kv_heads, num_cus, forced_chunk, wl);
+        const int fuse = waves_setting == 4 || head_fuse == 0 ? 0
+                         : head_fuse == 2 || head_fuse == 4 || head_fuse == 8 ? head_fuse
+                                                                              : 1;
+        d::plan_work_list(seq_lens, n, num_kv_heads, num_cus, forced_chunk, fuse, wl);
         info->chunk_tokens = wl.chunk;
         info->work_items = wl.n_work;
-        info->waves = wl.n_work ? d::plan_waves((int64_t)wl.n_work * num_kv_heads, num_cus,
-                                                waves_setting)
-                                : 0;
+        info->waves = !wl.n_work       ? 0
+                      : wl.fused_heads ? 8
+                                      : d::plan_waves((int64_t)wl.n_work * num_kv_heads, num_cus,
+                                                      waves_setting);
+        info->head_fused = wl.fused_heads;
         info->any_multi = wl.any_multi ? 1 : 0;
         info->any_empty = wl.any_empty ? 1 : 0;
         info->max_len = wl.max_len;

@@ -22,6 +22,16 @@
 // tile to tile.  The G query heads of the group share every K/V byte: each
 // K/V row is loaded once into VGPRs and used for all G heads.
 //
+// Head-fused plans (head_dim 128, near-uniform lengths, planner's choice): an
+// 8-wave workgroup takes H = 2, 4 or 8 kv heads of an entry instead of one,
+// wave w head w % H and tile slice w / H, so the workgroup reads H heads'
+// 256-byte pieces of each token row together (per-head workgroups read them
+// from H different CUs).  An entry's nch work items interleave its tiles
+// (slice s of item c: tiles c*NS+s, + nch*NS, ... with NS = 8 / H) instead of
+// taking chunks, and the planner picks H and nch so that the launch is one
+// workgroup per CU; for 64 entries of 8 kv heads on 256 CUs that is H = 2
+// and one item per entry, so no partials and no merge launch.
+//
 // Per tile:
 //   loads    K and V rows are read with LPR = D/8 lanes per token row, 16
 //            contiguous bytes per lane, TPI = 64/LPR rows per instruction,
@@ -44,13 +54,15 @@
 //   P.V      v_dot2_f32_f16 on token pairs: a lane holds 8 dims of tokens t
 //            and t+TPI, v_perm_b32 interleaves them into half2
 //            (v[t][d], v[t+TPI][d]); one dot2 per (head, dim) takes two tokens.
-// End: per-wave (m, l, o) combined across the NW waves in LDS; a work item that
+// End: per-wave (m, l, o) combined across the NW waves (head-fused: the NS
+// waves of each head) in LDS; a work item that
 // covers its whole sequence is normalised and written as fp16, otherwise
 // (m, l, o[D]) partials go to the workspace and attn_merge_kernel combines
 // the chunks: m* = max m_c, l = sum l_c 2^(m_c-m*), o = sum o_c 2^(m_c-m*)/(l+1e-6).
-// Append (decode calls): the workgroup holding the last chunk of entry b first
-// copies the new token's K/V row of head g into the cache at position S_b - 1
-// -- the bytes of appendKV(n=1) -- then reads it like any other token.
+// Append (decode calls): the workgroup holding the last chunk (head-fused: the
+// last tile) of entry b first copies the new token's K/V row of head g into
+// the cache at position S_b - 1 -- the bytes of appendKV(n=1) -- then reads it
+// like any other token.
 //
 // Every global load uses a token index clamped into its tile's valid range,
 // so no load leaves the attended range; masked tokens get p = 0.
@@ -81,6 +93,7 @@ namespace {
 // expressed in 4-wave workgroups.
 constexpr int kWavesPerEU = 2;
 constexpr int kTile = 64;             // tokens per wave tile
+constexpr int kVmcntAll = 0x0F70;     // s_waitcnt vmcnt(0)
 constexpr int kQuantum = kPlanQuantum; // chunk lengths are multiples of this
 static_assert(kTile == kPlanTile && kPlanSlotsPerCU == kWavesPerEU, "planner geometry");
 
@@ -601,12 +614,17 @@ struct MfmaScorer {
 };
 
 // ------------------------------------------------------------------ kernel
-template <int D, int G, bool PAGED, bool MFMA, int kNW>
+template <int D, int G, bool PAGED, bool MFMA, int kNW, int HPW>
 __global__ __launch_bounds__(kNW * 64)
 __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnArgs a) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
     static_assert(kNW == 4 || kNW == 8, "waves per workgroup");
+    static_assert(HPW == 0 || (kNW % HPW == 0 && (HPW == 2 || HPW == 4 || HPW == 8)), "head block");
+    constexpr bool HF = HPW > 0;                // head-fused
+    constexpr int  H1 = HF ? HPW : 1;           // heads per workgroup
+    constexpr int  NS = kNW / H1;               // waves sharing one kv head (tile slices)
+    constexpr bool SOLO = HF && NS == 1;        // one wave per head: no cross-wave combine
     constexpr int kThreads = kNW * 64;
     using SM = Smem<D, G, MFMA, kNW>;
     using Scorer = typename std::conditional<MFMA, MfmaScorer<D, G>, ValuScorer<D, G>>::type;
@@ -625,22 +643,44 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     const int       lane = threadIdx.x & 63;
     const int       wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: scalar tile math
     const AttnPlan &pl = a.plan;
-    // 1-D grid, kv head fastest: the Hkv workgroups reading the pieces of the
-    // same token rows are dispatched together.
-    const int item = blockIdx.x / a.Hkv;
-    const int g = blockIdx.x - item * a.Hkv;
+    // 1-D grid.  Per head (HPW = 0): kv head fastest, so the Hkv workgroups
+    // reading the pieces of the same token rows are dispatched together.
+    // Head-fused: block hb * n_work + item takes kv heads hb * HPW .. + HPW - 1
+    // of the item, wave w head hb * HPW + w % HPW and tile slice w / HPW, so
+    // the workgroup reads HPW heads' pieces of each token row at once; items
+    // fastest, so that an entry's head blocks are dealt to one XCD when
+    // n_work is a multiple of the XCD count.
+    const int item = HF ? (int)(blockIdx.x % (unsigned)pl.n_work) : blockIdx.x / a.Hkv;
+    const int hb = HF ? (int)(blockIdx.x / (unsigned)pl.n_work) : 0;
+    const int slice = wave / H1;
+    const int g = HF ? hb * HPW + wave % H1 : blockIdx.x - item * a.Hkv;
     int       b, c, S, nch, widx, row;
     ATTN_WORK_ITEM(a, item, b, c, S, nch, widx, row);
-    const int t0 = c * pl.chunk;
-    const int n = min(pl.chunk, S - t0); // >= 1 by construction of the plan
+    // HF: the nch items of an entry interleave its tiles in slices: slice s
+    // of item c takes tiles u, u + nch * NS, ... with u = c * NS + s, instead
+    // of contiguous chunks.
+    const int t0 = HF ? 0 : c * pl.chunk;
+    const int n = HF ? S : min(pl.chunk, S - t0); // >= 1 by construction of the plan
+    const int ntiles = (n + kTile - 1) / kTile;
+    // Tile order: wave w walks tiles tile_of(j), j = w, w + NW, ... (head-fused:
+    // j = c * NS + slice, + nch * NS, ...) -- every tile once, rotated by an
+    // offset that depends on the entry.  Entries of
+    // equal length stream in lockstep; without the rotation their concurrent
+    // reads sit a multiple of the slot stride apart, which for some strides
+    // (max_seq_len 8256 or 8704 at 8 kv heads x 128 dims) maps them onto the
+    // same HBM channels and cost 5% of the stream.
+    const int rot = ntiles > 1 ? (int)((((uint32_t)b * 2654435761u) >> 8) % (uint32_t)ntiles) : 0;
+    auto tile_of = [&](int j_) { const int x = j_ + rot; return x < ntiles ? x : x - ntiles; };
+    // HF: the item holding the last tile appends (it reads token S-1).
+    const int app_c = HF ? ((ntiles - 1 - rot + ntiles) % ntiles) % (nch * NS) / NS : nch - 1;
 
     const RowAddr<PAGED> ra(a.kv, row, g);
 
-    if (a.new_k && c == nch - 1) {
+    if (a.new_k && c == app_c) {
         // Fused appendKV(n=1) of head g at position S-1 (same bytes as the
-        // D2D copies of kv_cache.cpp:230-233).
+        // D2D copies of kv_cache.cpp:230-233); HF: each slice-0 wave its own head.
         constexpr int P = D / 8; // 16-byte pieces per head row
-        const int     tid = threadIdx.x;
+        const int     tid = !HF ? (int)threadIdx.x : slice == 0 ? lane : kThreads;
         if (tid < 2 * P) {
             const int     which = tid / P, e = tid - which * P;
             const __half *src = (which ? a.new_v : a.new_k) + ((int64_t)b * a.Hkv + g) * D + e * 8;
@@ -666,7 +706,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
-    const int ntiles = (n + kTile - 1) / kTile;
     uint4     kb[2][KB];
     uint4     va[2][VB], vb[2][VB];
     // Tile at chunk offset ts; tokens below tend are valid; q: the tile's
@@ -702,28 +741,21 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
         return ra.tile_blocks(t0 + ti_ * kTile, t0 + min(n, ti_ * kTile + kTile) - 1, lane);
     };
 
-    // Tile order: wave w walks tiles tile_of(j), j = w, w + NW, ... -- every
-    // tile once, rotated by an offset that depends on the entry.  Entries of
-    // equal length stream in lockstep; without the rotation their concurrent
-    // reads sit a multiple of the slot stride apart, which for some strides
-    // (max_seq_len 8256 or 8704 at 8 kv heads x 128 dims) maps them onto the
-    // same HBM channels and cost 5% of the stream.
-    const int rot = ntiles > 1 ? (int)((((uint32_t)b * 2654435761u) >> 8) % (uint32_t)ntiles) : 0;
-    auto tile_of = [&](int j_) { const int x = j_ + rot; return x < ntiles ? x : x - ntiles; };
-
-    int j = wave;
-    int bt_cur = 0, bt_next = 0;
+    const int JS = HF ? nch * NS : kNW;        // tile stride of a wave
+    const int j0 = HF ? c * NS + slice : wave; // its first tile
+    int       j = j0;
+    int       bt_cur = 0, bt_next = 0;
     if (j < ntiles) {
         const int tf = tile_of(j);
         bt_cur = tile_bt(tf);
         kload(tf * kTile, min(n, tf * kTile + kTile), 0, kb[0], ra.quarters(bt_cur));
     }
-    for (; j < ntiles; j += kNW) {
+    for (; j < ntiles; j += JS) {
         const int      ts = tile_of(j) * kTile;
         const int      tend = min(n, ts + kTile);
         const int      nt = tend - ts;
         const Quarters qc = ra.quarters(bt_cur);
-        if (PAGED && j + kNW < ntiles) bt_next = tile_bt(tile_of(j + kNW)); // consumed one tile later
+        if (PAGED && j + JS < ntiles) bt_next = tile_bt(tile_of(j + JS)); // consumed one tile later
         // ---- scores
 #pragma unroll
         for (int bi = 0; bi < NKB; ++bi) {
@@ -758,8 +790,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
         for (int bj = 0; bj < NVB; ++bj) {
             if (bj + 1 < NVB) {
                 vload(ts, tend, bj + 1, va[(bj + 1) & 1], vb[(bj + 1) & 1], qc);
-            } else if (j + kNW < ntiles) {
-                const int tn = tile_of(j + kNW) * kTile;
+            } else if (j + JS < ntiles) {
+                const int tn = tile_of(j + JS) * kTile;
                 kload(tn, min(n, tn + kTile), 0, kb[0], ra.quarters(bt_next));
             }
 #pragma unroll
@@ -811,7 +843,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
     float *sm = SM::m(smem), *sl = SM::l(smem);
-    if (wave < ntiles) {
+    if (j0 < ntiles) {
         sco.finish(sm + wave * G, sl + wave * G);
     } else if (lane < G) {
         sm[wave * G + lane] = -INFINITY;
@@ -826,28 +858,37 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
             *reinterpret_cast<float4 *>(dst + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
         }
     }
-    __syncthreads();
+    if constexpr (SOLO) wave_sync_lds(); // the wave's own head: no other wave to wait for
+    else __syncthreads();
 
-    // ---- combine the waves, emit
-    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-        const int h = idx / D;
-        const int d = idx - h * D;
+    // ---- combine the waves of each head (SOLO: the wave alone), emit
+    constexpr int NH = SOLO || !HF ? 1 : HPW; // heads this loop covers
+    for (int idx = SOLO ? lane : (int)threadIdx.x; idx < NH * G * D; idx += SOLO ? 64 : kThreads) {
+        const int hs = SOLO ? wave : idx / (G * D); // head slot in the workgroup (HF)
+        const int e = SOLO || !HF ? idx : idx - hs * (G * D);
+        const int h = e / D;
+        const int d = e - h * D;
+        const int gh = HF ? hb * HPW + hs : g; // kv head of this output
         float     mh = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kNW; ++w) mh = fmaxf(mh, sm[w * G + h]);
+        for (int w0 = 0; w0 < NS; ++w0) {
+            const int w = HF ? hs + HPW * w0 : w0;
+            mh = fmaxf(mh, sm[w * G + h]);
+        }
         float o = 0.0f, lh = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kNW; ++w) {
+        for (int w0 = 0; w0 < NS; ++w0) {
+            const int   w = HF ? hs + HPW * w0 : w0;
             const float mw = sm[w * G + h];
             const float wgt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mh);
-            o = fmaf(wgt, reinterpret_cast<const float *>(SM::wave(smem, w))[idx], o);
+            o = fmaf(wgt, reinterpret_cast<const float *>(SM::wave(smem, w))[e], o);
             lh = fmaf(wgt, sl[w * G + h], lh);
         }
-        const int64_t row = (int64_t)b * a.Hq + (int64_t)g * G + h;
+        const int64_t row = (int64_t)b * a.Hq + (int64_t)gh * G + h;
         if (nch == 1) {
             a.out[row * D + d] = __float2half(o * (1.0f / (lh + 1e-6f)));
         } else {
-            const int64_t prow = (int64_t)widx * a.Hq + (int64_t)g * G + h;
+            const int64_t prow = (int64_t)widx * a.Hq + (int64_t)gh * G + h;
             a.part_o[prow * D + d] = o;
             if (d == 0) {
                 a.part_ml[prow * 2] = mh;
@@ -875,7 +916,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 // The combine across waves, the partials and the fused append are those of
 // attn_decode_kernel.
 constexpr float kMmaLazy = 8.0f;
-constexpr int   kVmcntAll = 0x0F70; // s_waitcnt vmcnt(0)
 
 typedef _Float16 f16x4m __attribute__((ext_vector_type(4)));
 typedef short    s16x4m __attribute__((ext_vector_type(4)));
@@ -1223,21 +1263,36 @@ void launch_mma_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, 
     }
 }
 
-template <int D, int G, bool PAGED, bool MFMA, int NW>
+template <int D, int G, bool PAGED, bool MFMA, int NW, int HPW = 0>
 void launch_one(const AttnArgs &args, int n_work, int Hkv, hipStream_t stream) {
     using SM = Smem<D, G, MFMA, NW>;
-    auto                 *fn = attn_decode_kernel<D, G, PAGED, MFMA, NW>;
+    auto                 *fn = attn_decode_kernel<D, G, PAGED, MFMA, NW, HPW>;
     static std::once_flag once;
     std::call_once(once, [&] {
         HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, SM::kBytes));
     });
-    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * (unsigned)Hkv), dim3(NW * 64), SM::kBytes, stream,
-                       args);
+    const unsigned per = (unsigned)(Hkv / (HPW ? HPW : 1));
+    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * per), dim3(NW * 64), SM::kBytes, stream, args);
+}
+
+template <int D, int G, int HPW>
+void launch_fused(const AttnArgs &args, int n_work, int Hkv, bool paged, hipStream_t stream) {
+    if (paged) launch_one<D, G, true, false, 8, HPW>(args, n_work, Hkv, stream);
+    else launch_one<D, G, false, false, 8, HPW>(args, n_work, Hkv, stream);
 }
 
 template <int D, int G, bool MFMA>
-void launch_dgm(const AttnArgs &args, int n_work, int Hkv, bool paged, int nw, hipStream_t stream) {
+void launch_dgm(const AttnArgs &args, int n_work, int Hkv, bool paged, int nw, int hpw,
+                hipStream_t stream) {
+    if constexpr (!MFMA && D == 128) { // the head-fused forms (VALU scores, head_dim 128)
+        switch (hpw) {
+        case 2: launch_fused<D, G, 2>(args, n_work, Hkv, paged, stream); return;
+        case 4: launch_fused<D, G, 4>(args, n_work, Hkv, paged, stream); return;
+        case 8: launch_fused<D, G, 8>(args, n_work, Hkv, paged, stream); return;
+        default: break;
+        }
+    }
     if (nw == 8) {
         if (paged) launch_one<D, G, true, MFMA, 8>(args, n_work, Hkv, stream);
         else launch_one<D, G, false, MFMA, 8>(args, n_work, Hkv, stream);
@@ -1248,25 +1303,25 @@ void launch_dgm(const AttnArgs &args, int n_work, int Hkv, bool paged, int nw, h
 }
 
 template <int D, int G>
-void launch_dg(const AttnArgs &args, int n_work, int Hkv, bool paged, bool mfma, int nw,
+void launch_dg(const AttnArgs &args, int n_work, int Hkv, bool paged, bool mfma, int nw, int hpw,
                hipStream_t stream) {
     if constexpr (D <= 128) { // the MFMA score path exists for head_dim <= 128
         if (mfma) {
-            launch_dgm<D, G, true>(args, n_work, Hkv, paged, nw, stream);
+            launch_dgm<D, G, true>(args, n_work, Hkv, paged, nw, 0, stream);
             return;
         }
     }
-    launch_dgm<D, G, false>(args, n_work, Hkv, paged, nw, stream);
+    launch_dgm<D, G, false>(args, n_work, Hkv, paged, nw, hpw, stream);
 }
 
 template <int D>
 void launch_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, bool mfma, int nw,
-              hipStream_t stream) {
+              int hpw, hipStream_t stream) {
     switch (G) {
-    case 1: launch_dg<D, 1>(args, n_work, Hkv, paged, mfma, nw, stream); break;
-    case 2: launch_dg<D, 2>(args, n_work, Hkv, paged, mfma, nw, stream); break;
-    case 4: launch_dg<D, 4>(args, n_work, Hkv, paged, mfma, nw, stream); break;
-    case 8: launch_dg<D, 8>(args, n_work, Hkv, paged, mfma, nw, stream); break;
+    case 1: launch_dg<D, 1>(args, n_work, Hkv, paged, mfma, nw, hpw, stream); break;
+    case 2: launch_dg<D, 2>(args, n_work, Hkv, paged, mfma, nw, hpw, stream); break;
+    case 4: launch_dg<D, 4>(args, n_work, Hkv, paged, mfma, nw, hpw, stream); break;
+    case 8: launch_dg<D, 8>(args, n_work, Hkv, paged, mfma, nw, hpw, stream); break;
     default: break;
     }
 }
@@ -1331,12 +1386,32 @@ int waves_setting() {
 
 int waves_for(int64_t workgroups) { return plan_waves(workgroups, device_cus(), waves_setting()); }
 
+// Head-fused plans: TL_ATTN_HF ("0": off, "2" / "4" / "8": that many kv
+// heads per workgroup where a plan with it applies, else auto) at first use;
+// tl_attn_set_head_fuse overrides it.  0 = auto, 1 = off, 2 / 4 / 8 = forced.
+std::atomic<int> g_head_fuse{-1};
+
+int head_fuse_setting() {
+    int v = g_head_fuse.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char *e = std::getenv("TL_ATTN_HF");
+        v = 0;
+        if (e && std::strcmp(e, "0") == 0) v = 1;
+        if (e && (std::strcmp(e, "2") == 0 || std::strcmp(e, "4") == 0 || std::strcmp(e, "8") == 0))
+            v = std::atoi(e);
+        g_head_fuse.store(v);
+    }
+    return v;
+}
+
 } // namespace
 
 void set_score_path(int path) { g_score_path.store(path); }
 void set_waves(int waves) { g_waves.store(waves); }
+void set_head_fuse(int mode) { g_head_fuse.store(mode); }
 int  waves() { return waves_setting(); }
 int  score_path() { return score_path_setting(); }
+int  head_fuse() { return head_fuse_setting(); }
 
 bool attn_shape_supported(int D, int G) {
     return (D == 32 || D == 64 || D == 128 || D == 256) && (G == 1 || G == 2 || G == 4 || G == 8);
@@ -1351,9 +1426,16 @@ int choose_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, 
     return plan_chunk(lens, n, num_kv_heads, uniform_len, device_cus(), chunk_override_from_env());
 }
 
+bool head_fused_kernel(int head_dim) {
+    return head_dim == 128 && head_fuse_setting() != 1 && waves_setting() != 4 &&
+           !use_mfma_scores(head_dim, 0) && !use_mma_path(head_dim, 0);
+}
+
 void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out) {
-    (void)head_dim;
-    plan_work_list(lens, n, num_kv_heads, device_cus(), chunk_override_from_env(), out);
+    // planner argument: 0 = per head, 1 = auto, 2 / 4 / 8 = forced heads per workgroup
+    const int mode = head_fuse_setting();
+    const int fuse = !head_fused_kernel(head_dim) ? 0 : mode == 0 ? 1 : mode;
+    plan_work_list(lens, n, num_kv_heads, device_cus(), chunk_override_from_env(), fuse, out);
 }
 
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
@@ -1378,6 +1460,12 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
                                     std::string(paged ? "block" : "slot") + " * row bytes)");
     if (plan.any_multi && !part)
         throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
+    const int  hpw = plan.fused_heads;
+    const bool hf = hpw != 0;
+    if (hf && (D != 128 || (hpw != 2 && hpw != 4 && hpw != 8) || Hkv % hpw != 0 || plan.any_empty))
+        throw std::invalid_argument("attention: a head-fused plan needs head_dim 128, 2, 4 or 8 "
+                                    "kv heads per workgroup dividing the kv heads, and no empty "
+                                    "sequence");
     if (inl && inl->compact && (plan.any_multi || plan.any_empty || plan.n_work != inl->n))
         throw std::invalid_argument("attention: compact metadata needs one chunk per entry");
     AttnArgs args;
@@ -1395,7 +1483,7 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     if (inl) std::memcpy(&args.meta, inl, sizeof(InlineMeta));
     else args.meta.n = 0;
 
-    if (plan.n_work > 0 && use_mma_path(D, G)) {
+    if (plan.n_work > 0 && !hf && use_mma_path(D, G)) {
         const int nw = waves_for((int64_t)plan.n_work * Hkv);
         if (hooks) profile_begin(KernelId::AttnChunk, stream);
         if (D == 64) launch_mma_d<64>(args, plan.n_work, Hkv, G, paged, nw, stream);
@@ -1403,13 +1491,15 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         HIP_CHECK(hipGetLastError());
         if (hooks) profile_end(KernelId::AttnChunk, stream);
     } else if (plan.n_work > 0) {
-        const int nw = waves_for((int64_t)plan.n_work * Hkv);
+        // head-fused: 8-wave workgroups, VALU scores, whatever the settings
+        const int nw = hf ? 8 : waves_for((int64_t)plan.n_work * Hkv);
+        const bool mf = mfma && !hf;
         if (hooks) profile_begin(KernelId::AttnChunk, stream);
         switch (D) {
-        case 32: launch_d<32>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
-        case 64: launch_d<64>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
-        case 128: launch_d<128>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
-        case 256: launch_d<256>(args, plan.n_work, Hkv, G, paged, mfma, nw, stream); break;
+        case 32: launch_d<32>(args, plan.n_work, Hkv, G, paged, mf, nw, 0, stream); break;
+        case 64: launch_d<64>(args, plan.n_work, Hkv, G, paged, mf, nw, 0, stream); break;
+        case 128: launch_d<128>(args, plan.n_work, Hkv, G, paged, mf, nw, hpw, stream); break;
+        case 256: launch_d<256>(args, plan.n_work, Hkv, G, paged, mf, nw, 0, stream); break;
         default: break;
         }
         HIP_CHECK(hipGetLastError());

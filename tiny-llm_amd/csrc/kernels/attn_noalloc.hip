@@ -113,6 +113,7 @@ std::string attn_decode_view_noalloc(const __half *q, const KvView &kv,
     plan.any_multi = wl.any_multi;
     plan.any_empty = wl.any_empty;
     plan.max_len = wl.max_len;
+    plan.fused_heads = wl.fused_heads;
     if (!in_args) {
         words.resize(meta_words);
         std::memcpy(words.data(), seq_lens_host, nb * 4);

@@ -52,6 +52,9 @@ struct AttnPlan {
     bool           any_multi = false;  // some entry spans more than one chunk
     bool           any_empty = false;  // some entry attends to zero tokens
     int            max_len = 0;        // longest attended length (offset-width check)
+    // Head-fused plan (WorkList::fused_heads): 8-wave workgroups of
+    // fused_heads kv heads, an entry's items interleaving its tiles; 0: per head.
+    int            fused_heads = 0;
 };
 
 // Chunk length for the current device (TL_ATTN_CHUNK overrides), see
@@ -138,6 +141,11 @@ int  score_path();
 // Waves per attention workgroup: 0 = auto, 4 or 8.
 void set_waves(int waves);
 int  waves();
+
+// Head-fused decode plans: 0 = auto, 1 = off, 2 / 4 / 8 = that many kv
+// heads per workgroup where a plan with it applies.
+void set_head_fuse(int mode);
+int  head_fuse();
 
 // Compute units of the current device (cached per device).
 int device_cus();

@@ -87,7 +87,8 @@ class KVView(C.Structure):
 
 class AttnPlanInfo(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("chunk_tokens", "work_items", "waves", "any_multi",
-                                       "any_empty", "max_len", "inline_words", "inline_compact")]
+                                       "any_empty", "max_len", "inline_words", "inline_compact",
+                                       "head_fused")]
 
 
 def _declare(L: C.CDLL) -> None:
@@ -153,7 +154,9 @@ def _declare(L: C.CDLL) -> None:
         "tl_attn_get_score_path": (i, []),
         "tl_attn_set_waves": (i, [i]),
         "tl_attn_get_waves": (i, []),
-        "tl_attn_plan": (i, [vp, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
+        "tl_attn_set_head_fuse": (i, [i]),
+        "tl_attn_get_head_fuse": (i, []),
+        "tl_attn_plan": (i, [vp, i, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
         "tl_profile_enable": (None, [i]),
         "tl_profile_reset": (None, []),
         "tl_profile_query": (i, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
@@ -473,20 +476,35 @@ def get_waves() -> int:
     return load().tl_attn_get_waves()
 
 
-def attn_plan(seq_lens, num_kv_heads, num_cus=256, forced_chunk=0, waves=0, with_rows=True):
+def set_head_fuse(mode: int):
+    """Head-fused decode plans: 0 = auto, 1 = off, 2 / 4 / 8 = that many kv
+    heads per workgroup where a plan with it applies."""
+    _check(load().tl_attn_set_head_fuse(mode))
+
+
+def get_head_fuse() -> int:
+    return load().tl_attn_get_head_fuse()
+
+
+def attn_plan(seq_lens, num_kv_heads, num_cus=256, forced_chunk=0, waves=0, with_rows=True,
+              head_fuse=False):
     """The decode attention launch plan for these attended lengths (host
     only): a dict of tl_attn_plan_info plus part_base and the work list as
-    (entry, chunk) pairs in launch order."""
+    (entry, chunk) pairs in launch order.  head_fuse: False / 0 = per-head
+    plans only; True / 1 = head-fused where it applies, as the entry points do
+    for head_dim 128 on the VALU score path; 2 / 4 / 8 = that many kv heads
+    per workgroup."""
     import numpy as np
     lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
     n = lens.size
     info = AttnPlanInfo()
     _check(load().tl_attn_plan(lens.ctypes.data if n else None, n, num_kv_heads, num_cus,
-                               forced_chunk, waves, int(with_rows), C.byref(info), None, None))
+                               forced_chunk, waves, int(head_fuse), int(with_rows), C.byref(info),
+                               None, None))
     part = np.zeros(n + 1, dtype=np.int32)
     work = np.zeros(max(1, 2 * info.work_items), dtype=np.int32)
     _check(load().tl_attn_plan(lens.ctypes.data if n else None, n, num_kv_heads, num_cus,
-                               forced_chunk, waves, int(with_rows), C.byref(info),
+                               forced_chunk, waves, int(head_fuse), int(with_rows), C.byref(info),
                                part.ctypes.data, work.ctypes.data))
     out = {name: getattr(info, name) for name, _ in AttnPlanInfo._fields_}
     out["part_base"] = part
