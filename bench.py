@@ -381,6 +381,14 @@ def fixed_batch(args, tl, torch, workloads, np):
     t_wall = time.perf_counter() - t_wall
     elapsed_ms = ev0.elapsed_time(ev1)
     info = batch.info()
+    # kv heads per attention workgroup of the last timed step's plan (1: per
+    # head; 2, 4, 8: head-fused), as the library's planner makes it
+    att_last = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int32)
+    hf_mode = tl.get_head_fuse()
+    hf_ok = D == 128 and hf_mode != 1 and tl.get_waves() != 4 and tl.get_score_path() in (0, 2)
+    plan = tl.attn_plan(att_last, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
+                        head_fuse=(hf_mode or 1) if hf_ok else 0)
+    heads_per_wg = plan["head_fused"] or 1
 
     # Per-step pass: the same steps (lengths not advanced) with one event
     # between consecutive steps, for the spread of the step time.
@@ -419,7 +427,7 @@ def fixed_batch(args, tl, torch, workloads, np):
             "block_tokens": args.block_tokens if blocks else bt, "kv_std": cfg.kv_std,
             "alloc": "blocks" if blocks else ("permuted blocks" if bt else "full-length slots"),
             "chunk_tokens": info["chunk_tokens"], "work_items": info["work_items"],
-            "parallelism": "single GPU"}
+            "kv_heads_per_workgroup": heads_per_wg, "parallelism": "single GPU"}
     data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) (torch.randn, seeded), prefilled "
             f"via appendKV" + (", 16-token blocks behind a seeded random permutation" if bt else ""))
     cpu = None
@@ -908,7 +916,8 @@ def main():
                        "kv_append": round(app_ms / max(1, app_n) * 1e3, 2)},
         "kernel_launches": {"attn_chunk": chunk_n, "attn_merge": merge_n, "kv_append": app_n},
         "host_wall_us_per_step": round(r["t_wall"] / K * 1e6, 2),
-        "roofline": {"kernel": f"attn_decode_kernel<D={D},G={Hq // Hkv},{score_kind}>",
+        "roofline": {"kernel": (f"attn_decode_kernel<D={D},G={Hq // Hkv},{score_kind},"
+                               f"kv_heads_per_wg={conf.get('kv_heads_per_workgroup', 1)}>"),
                      "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic,
