@@ -389,6 +389,7 @@ def fixed_batch(args, tl, torch, workloads, np):
     plan = tl.attn_plan(att_last, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
                         head_fuse=(hf_mode or 1) if hf_ok else 0)
     heads_per_wg = plan["head_fused"] or 1
+    fused_items = ("chunks" if plan["fused_chunked"] else "interleaved tiles") if plan["head_fused"] else None
 
     # Per-step pass: the same steps (lengths not advanced) with one event
     # between consecutive steps, for the spread of the step time.
@@ -427,7 +428,8 @@ def fixed_batch(args, tl, torch, workloads, np):
             "block_tokens": args.block_tokens if blocks else bt, "kv_std": cfg.kv_std,
             "alloc": "blocks" if blocks else ("permuted blocks" if bt else "full-length slots"),
             "chunk_tokens": info["chunk_tokens"], "work_items": info["work_items"],
-            "kv_heads_per_workgroup": heads_per_wg, "parallelism": "single GPU"}
+            "kv_heads_per_workgroup": heads_per_wg, "head_fused_items": fused_items,
+            "parallelism": "single GPU"}
     data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) (torch.randn, seeded), prefilled "
             f"via appendKV" + (", 16-token blocks behind a seeded random permutation" if bt else ""))
     cpu = None

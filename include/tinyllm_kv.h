@@ -355,7 +355,9 @@ int tl_attn_get_waves(void);
  * a work item -- wave w head w % H, tile slice w / H -- so it reads H heads'
  * pieces of each token row at once, and a sequence's work items interleave
  * its 64-token tiles.  Auto takes the H in {8, 4, 2} with the fewest items
- * per sequence (one item: no merge launch), the larger H on a tie.  Initial
+ * per sequence (one item: no merge launch), the larger H on a tie.  Other
+ * lengths keep the chunk plan, with H = 2 over its items where per-head
+ * workgroups would have 4 waves (forced: the forced H).  Initial
  * value from the environment variable TL_ATTN_HF ("0" = off, "2" / "4" /
  * "8", else auto).  Every setting gives results within the same 1e-3 gate.
  * No reference counterpart (tuning knob). */
@@ -387,10 +389,12 @@ typedef struct tl_attn_plan_info {
     int inline_compact;/* 1: the compact encoding (one chunk per sequence; 16-bit
                           lengths and slots: one word per sequence + 16 bits
                           per work item) */
-    int head_fused;    /* kv heads per workgroup of a head-fused plan (2, 4 or 8;
-                          a sequence's work items interleave its tiles,
-                          chunk_tokens is the longest length rounded up, work
-                          is in chunk-major order), 0: per-head plan */
+    int head_fused;    /* kv heads per 8-wave workgroup of a head-fused plan (2, 4
+                          or 8), 0: per-head plan */
+    int fused_chunked; /* 1: head-fused over the chunk plan's items (ragged
+                          lengths); 0 with head_fused: a sequence's work items
+                          interleave its tiles, chunk_tokens is the longest
+                          length rounded up, work is in chunk-major order */
 } tl_attn_plan_info;
 int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
                  int waves_setting, int head_fuse, int with_rows, tl_attn_plan_info *info,

@@ -56,7 +56,14 @@ static void planner_random() {
         CHECK(wl.chunk % kPlanQuantum == 0 && wl.chunk >= kPlanQuantum);
         CHECK((int)wl.part_base.size() == n + 1);
         CHECK((int)wl.work.size() == 2 * wl.n_work);
-        if (wl.fused_heads) { // interleaved items, chunk-major order
+        if (wl.fused_chunked) { // head-fused over the chunk plan's items
+            if (fuse == 1)
+                CHECK(wl.fused_heads == 2 && hkv % 2 == 0 &&
+                      plan_waves((int64_t)wl.n_work * hkv, cus, 0) == 4);
+            else
+                CHECK((fuse == 2 || fuse == 4 || fuse == 8) && wl.fused_heads == fuse && hkv % fuse == 0);
+        }
+        if (wl.fused_heads && !wl.fused_chunked) { // interleaved items, chunk-major order
             const int hpw = wl.fused_heads;
             CHECK(fuse && !forced && n > 0 && hkv % hpw == 0 && !wl.any_empty);
             CHECK(hpw == 2 || hpw == 4 || hpw == 8);

@@ -3,8 +3,12 @@ work item (wave w: head w % H, tile slice w / H), so it reads H heads'
 pieces of each token row at once, and a sequence's work items interleave its
 64-token tiles; split sequences are combined by the merge launch.
 
+Ragged lengths keep the chunk plan's items (longest first), with 2 heads per
+workgroup where per-head workgroups would have 4 waves.
+
 Checked for H = 2, 4 and 8 and the planner's own choice, every group size,
-contiguous and paged caches, one to eight items per sequence:
+contiguous and paged caches, one to eight interleaved items per sequence and
+chunk items of ragged lengths:
   - one decode step (append + attention) against the oracle: attention
     <= 1e-3 normwise (test_transformer.cu:80-92), cache bytes bit-exact;
   - the same step on the per-head kernel (head fusing off) within the same
@@ -64,15 +68,47 @@ def test_head_fused_decode_step(tl, orc, head_fuse, run, expect):
     setting, Hkv, B, (lo, hi), G, paged = run
     rng = np.random.default_rng(zlib.crc32(repr(run).encode()))
     ctx = rng.integers(lo, hi + 1, B)
-    M = -(-(hi + 1) // 64) * 64
-    slots = B + 1
     lens = (ctx + 1).astype(np.int32)
     plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or 1)
     nch = plan["work_items"] // B
     if cus() == 256:
         assert (plan["head_fused"], nch) == expect
-    assert plan["head_fused"] in (2, 4, 8) and nch * B == plan["work_items"]
+    assert plan["head_fused"] in (2, 4, 8) and plan["fused_chunked"] == 0
+    assert nch * B == plan["work_items"]
+    decode_step_checks(tl, orc, head_fuse, rng, setting, Hkv, G, paged, ctx, plan)
 
+
+# Ragged lengths keep the chunk plan; where per-head workgroups would have 4
+# waves the planner runs its items with 2 heads per 8-wave workgroup (setting
+# 0), or with a forced number.  (setting, kv heads, batch, group, paged)
+CHUNKED = [(0, 8, 128, 4, True), (0, 8, 160, 8, False), (0, 16, 64, 2, False),
+           (4, 8, 96, 2, False), (8, 8, 64, 4, True), (2, 16, 48, 1, True)]
+
+
+@pytest.mark.parametrize("run", CHUNKED, ids=[
+    "h{}-hkv{}-b{}-g{}-{}".format(r[0], r[1], r[2], r[3], "paged" if r[4] else "slots")
+    for r in CHUNKED])
+def test_head_fused_chunk_items_decode_step(tl, orc, head_fuse, run):
+    setting, Hkv, B, G, paged = run
+    rng = np.random.default_rng(zlib.crc32(repr(run).encode()))
+    # ragged: mostly short, a few long enough to split into several chunks
+    ctx = np.where(rng.random(B) < 0.1, rng.integers(3000, 4000, B), rng.integers(20, 1500, B))
+    lens = (ctx + 1).astype(np.int32)
+    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or 1)
+    assert plan["fused_chunked"] == 1 and plan["head_fused"] == (setting or 2)
+    assert plan["waves"] == 8
+    per_head = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True)
+    assert plan["work_items"] == per_head["work_items"] and per_head["waves"] == 4
+    decode_step_checks(tl, orc, head_fuse, rng, setting, Hkv, G, paged, ctx, plan)
+
+
+def decode_step_checks(tl, orc, head_fuse, rng, setting, Hkv, G, paged, ctx, plan):
+    """One decode step on a cache holding contexts ctx: head-fused (setting)
+    twice, bit-identical; per-head; both against the oracle."""
+    B = len(ctx)
+    M = -(-(int(ctx.max()) + 1) // 64) * 64
+    slots = B + 1
+    lens = (ctx + 1).astype(np.int32)
     g = tl.KVCacheManager(1, Hkv, D, M, slots)
     o = orc.KVCacheOracle(1, Hkv, D, M, slots)
     if paged:
@@ -133,18 +169,27 @@ def test_head_fused_decode_step(tl, orc, head_fuse, run, expect):
 
 def test_head_fused_stateless_two_plans_in_a_row(tl, orc, head_fuse):
     """tl_attn_decode_gqa over a paged view with one slot per block: two
-    items per sequence (partials and the merge launch), then one."""
+    interleaved items per sequence (partials and the merge launch), then one,
+    then ragged lengths with an empty sequence (chunk items, 2 heads per
+    workgroup; the empty sequence's zero row from the merge launch)."""
     import torch
     head_fuse(0)
     Hkv, G = 8, 4
     Hq = Hkv * G
-    for B, (lo, hi), seed, nch in ((32, (4200, 4400), 1, 2), (64, (2100, 2300), 2, 1)):
+    for B, (lo, hi), seed, nch in ((32, (4200, 4400), 1, 2), (64, (2100, 2300), 2, 1),
+                                   (128, (0, 2000), 3, 0)):
         rng = np.random.default_rng(seed)
         lens = rng.integers(lo, hi + 1, B).astype(np.int32)
         p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse=True)
         assert p["head_fused"] in (2, 4, 8)
-        assert p["work_items"] == B * nch or cus() != 256
-        M = int(hi)
+        if nch:  # items interleaving tiles
+            assert p["fused_chunked"] == 0
+            assert p["work_items"] == B * nch or cus() != 256
+        else:  # ragged, an empty sequence included: chunk items, 2 heads per workgroup
+            lens[7] = 0
+            p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse=True)
+            assert p["fused_chunked"] == 1 and p["any_empty"] == 1
+        M = max(1, int(lens.max()))
         pool = f16bits(rng, 2 * B * M * Hkv * D)
         dpool = to_dev(pool)
         base = dpool.data_ptr()

@@ -78,11 +78,13 @@ def test_benchmark_config_plans(tl, name):
 # 8 kv heads; 2 heads per workgroup gives 256 (sequence, head pair) blocks,
 # one per CU, so one item per sequence (4 heads: 2 items, 8 heads: 4) -- 64
 # items, no merge, metadata 64 + 65 + 2 * 64 + 64 words.  The ragged
-# configurations keep their chunk plans.
+# configurations keep their chunk plans; cfg4 and cfg5, whose per-head
+# workgroups would have 4 waves, run them with 2 heads per 8-wave workgroup.
 EXPECTED_FUSED = {
     "cfg3": dict(chunk_tokens=8448, work_items=64, waves=8, any_multi=0, inline_words=321,
-                 head_fused=2),
-    **{k: dict(EXPECTED[k], head_fused=0) for k in ("cfg1", "cfg2", "cfg4", "cfg5")},
+                 head_fused=2, fused_chunked=0),
+    **{k: dict(EXPECTED[k], head_fused=0, fused_chunked=0) for k in ("cfg1", "cfg2")},
+    **{k: dict(EXPECTED[k], waves=8, head_fused=2, fused_chunked=1) for k in ("cfg4", "cfg5")},
 }
 
 
@@ -92,7 +94,7 @@ def test_benchmark_config_plans_head_fused(tl, name):
     p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse=True)
     got = {k: p[k] for k in EXPECTED_FUSED[name]}
     assert got == EXPECTED_FUSED[name]
-    if p["head_fused"]:
+    if p["head_fused"] and not p["fused_chunked"]:
         check_fused(p, lens, hkv, CUS, *fused_choice(lens, hkv, CUS))
     else:
         check_invariants(p, lens, hkv, CUS)
@@ -163,12 +165,30 @@ def test_random_plans_head_fused(tl, seed):
     choice = fused_choice(lens, hkv, cus, force)
     if choice:
         check_fused(p, lens, hkv, cus, *choice)
+        assert p["fused_chunked"] == 0
     else:
-        assert p["head_fused"] == 0
+        # the chunk plan, over 2 (auto, where per-head workgroups would have 4
+        # waves) or the forced number of heads per workgroup
+        per_head = tl.attn_plan(lens, hkv, num_cus=cus)
+        if force in (2, 4, 8):
+            want = force if hkv % force == 0 else 0
+        else:
+            want = 2 if hkv % 2 == 0 and per_head["waves"] == 4 else 0
+        assert (p["head_fused"], p["fused_chunked"]) == (want, int(want > 0))
+        assert {k: p[k] for k in ("chunk_tokens", "work_items", "any_multi")} == \
+            {k: per_head[k] for k in ("chunk_tokens", "work_items", "any_multi")}
         check_invariants(p, lens, hkv, cus)
-    # a forced chunk or forced 4-wave workgroups keep the chunk plan
-    assert tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, forced_chunk=512)["head_fused"] == 0
+    # forced 4-wave workgroups keep the per-head plan; a forced chunk the
+    # chunk plan, head-fused over its items by the same rule
     assert tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, waves=4)["head_fused"] == 0
+    pf = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, forced_chunk=512)
+    per_head = tl.attn_plan(lens, hkv, num_cus=cus, forced_chunk=512)
+    if force in (2, 4, 8):
+        want = force if hkv % force == 0 else 0
+    else:
+        want = 2 if hkv % 2 == 0 and per_head["waves"] == 4 else 0
+    assert (pf["head_fused"], pf["fused_chunked"]) == (want, int(want > 0))
+    assert pf["work_items"] == per_head["work_items"]
 
 
 def test_head_fused_choice_examples(tl):
@@ -183,7 +203,8 @@ def test_head_fused_choice_examples(tl):
     assert pick(80, 8, 8193) == (8, 3)     # only 8 heads fill 90%: 3 x 80 = 240
     assert pick(64, 4, 8193) == (2, 2)     # 4 kv heads: pairs, 2 items
     assert pick(64, 8, 600) == (2, 1)      # short sequences: one item still fills
-    assert pick(100, 8, 8193)[0] == 0      # no h fills 90%: per-head plan
+    p = tl.attn_plan(np.full(100, 8193, np.int32), 8, num_cus=CUS, head_fuse=True)
+    assert (p["head_fused"], p["fused_chunked"]) == (2, 1)  # no h fills 90%: chunk plan, 2 heads
 
 
 def check_invariants(p, lens, hkv, cus, forced=0):
@@ -210,17 +231,21 @@ def check_invariants(p, lens, hkv, cus, forced=0):
     for k in range(len(item_len) - 1):
         if item_len[k] == item_len[k + 1]:
             assert tuple(work[k]) < tuple(work[k + 1])
-    # waves: 8 when every CU gets at most two workgroups in turn
+    # waves: 8 when every CU gets at most two workgroups in turn (head-fused
+    # over the items: 8-wave workgroups of several heads, one per CU)
+    fused = p.get("fused_chunked", 0) == 1
     if p["work_items"]:
-        assert p["waves"] == (8 if p["work_items"] * hkv <= 2 * cus else 4)
-    # list scheduling of the items (x hkv heads) on 2 slots per CU, longest
-    # first, finishes within one item of the ideal makespan
+        assert p["waves"] == (8 if fused or p["work_items"] * hkv <= 2 * cus else 4)
+    # list scheduling of the items (x hkv heads, or head blocks) on 2 slots
+    # per CU (one per CU for head blocks), longest first, finishes within one
+    # item of the ideal makespan
     if p["work_items"]:
-        slots = [0] * (2 * cus)
+        units = hkv // p["head_fused"] if fused else hkv
+        slots = [0] * (cus if fused else 2 * cus)
         for L in item_len:
-            for _ in range(hkv):
+            for _ in range(units):
                 heapq.heapreplace(slots, slots[0] + L)
-        ideal = sum(item_len) * hkv / (2 * cus)
+        ideal = sum(item_len) * units / len(slots)
         assert max(slots) <= ideal + max(item_len)
 
 

@@ -105,8 +105,12 @@ bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int 
 
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
                     int head_fuse, WorkList &out) {
-    if (forced_chunk == 0 && plan_head_fused(lens, n, num_kv_heads, cus, head_fuse, out)) return;
+    if (forced_chunk == 0 && plan_head_fused(lens, n, num_kv_heads, cus, head_fuse, out)) {
+        out.fused_chunked = false;
+        return;
+    }
     out.fused_heads = 0;
+    out.fused_chunked = false;
     out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
     out.part_base.assign((size_t)std::max(n, 0) + 1, 0);
     out.any_multi = false;
@@ -138,6 +142,19 @@ void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int f
                             out.part_base.begin()) - 1;
         out.work[2 * w] = i;
         out.work[2 * w + 1] = row - out.part_base[(size_t)i];
+    }
+    // Head-fused over the chunk items: forced heads per workgroup, or (auto)
+    // two heads per 8-wave workgroup where the per-head plan takes 4-wave
+    // workgroups -- as many waves per head, two heads' pieces of each row
+    // read together.  (Where per-head workgroups have 8 waves, fusing would
+    // halve the workgroups and unbalance ragged lengths.)
+    if ((head_fuse == 2 || head_fuse == 4 || head_fuse == 8) && num_kv_heads % head_fuse == 0) {
+        out.fused_heads = head_fuse;
+        out.fused_chunked = true;
+    } else if (head_fuse == 1 && num_kv_heads % 2 == 0 && out.n_work > 0 &&
+               plan_waves((int64_t)out.n_work * num_kv_heads, cus, 0) == 4) {
+        out.fused_heads = 2;
+        out.fused_chunked = true;
     }
 }
 

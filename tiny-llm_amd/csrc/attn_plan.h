@@ -33,6 +33,7 @@ struct WorkList {
     bool                 any_multi = false;
     bool                 any_empty = false;
     int                  fused_heads = 0;
+    bool                 fused_chunked = false; // head-fused over the chunk plan's items
     std::vector<int32_t> part_base; // n + 1
     std::vector<int32_t> work;      // 2 * n_work
 };
@@ -62,7 +63,10 @@ bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int 
                      WorkList &out);
 
 // The whole ragged plan (chunk, part_base, work list) for lens[0..n): the
-// head-fused plan when it applies and no chunk is forced, else chunks.
+// head-fused plan when it applies and no chunk is forced, else chunks --
+// head-fused over the chunk items (fused_chunked) when head_fuse forces 2, 4
+// or 8 heads per workgroup, or, for head_fuse 1, with 2 heads per 8-wave
+// workgroup where the per-head plan would take 4-wave workgroups.
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
                     int head_fuse, WorkList &out);
 

@@ -538,6 +538,7 @@ int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, 
                                       : d::plan_waves((int64_t)wl.n_work * num_kv_heads, num_cus,
                                                       waves_setting);
         info->head_fused = wl.fused_heads;
+        info->fused_chunked = wl.fused_chunked ? 1 : 0;
         info->any_multi = wl.any_multi ? 1 : 0;
         info->any_empty = wl.any_empty ? 1 : 0;
         info->max_len = wl.max_len;

@@ -650,8 +650,14 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     // the workgroup reads HPW heads' pieces of each token row at once; items
     // fastest, so that an entry's head blocks are dealt to one XCD when
     // n_work is a multiple of the XCD count.
-    const int item = HF ? (int)(blockIdx.x % (unsigned)pl.n_work) : blockIdx.x / a.Hkv;
-    const int hb = HF ? (int)(blockIdx.x / (unsigned)pl.n_work) : 0;
+    // (Head-fused over chunk items: head block fastest, keeping the work
+    // list's longest-first order.)
+    const bool ilv = HF && !pl.fused_chunked; // items interleave an entry's tiles
+    const int  hbn = a.Hkv / H1;              // head blocks per item
+    const int  item = !HF ? blockIdx.x / a.Hkv
+                      : ilv ? (int)(blockIdx.x % (unsigned)pl.n_work)
+                            : (int)(blockIdx.x / (unsigned)hbn);
+    const int  hb = !HF ? 0 : ilv ? (int)(blockIdx.x / (unsigned)pl.n_work) : (int)(blockIdx.x % (unsigned)hbn);
     const int slice = wave / H1;
     const int g = HF ? hb * HPW + wave % H1 : blockIdx.x - item * a.Hkv;
     int       b, c, S, nch, widx, row;
@@ -659,8 +665,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     // HF: the nch items of an entry interleave its tiles in slices: slice s
     // of item c takes tiles u, u + nch * NS, ... with u = c * NS + s, instead
     // of contiguous chunks.
-    const int t0 = HF ? 0 : c * pl.chunk;
-    const int n = HF ? S : min(pl.chunk, S - t0); // >= 1 by construction of the plan
+    const int t0 = ilv ? 0 : c * pl.chunk;
+    const int n = ilv ? S : min(pl.chunk, S - t0); // >= 1 by construction of the plan
     const int ntiles = (n + kTile - 1) / kTile;
     // Tile order: wave w walks tiles tile_of(j), j = w, w + NW, ... (head-fused:
     // j = c * NS + slice, + nch * NS, ...) -- every tile once, rotated by an
@@ -672,7 +678,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     const int rot = ntiles > 1 ? (int)((((uint32_t)b * 2654435761u) >> 8) % (uint32_t)ntiles) : 0;
     auto tile_of = [&](int j_) { const int x = j_ + rot; return x < ntiles ? x : x - ntiles; };
     // HF: the item holding the last tile appends (it reads token S-1).
-    const int app_c = HF ? ((ntiles - 1 - rot + ntiles) % ntiles) % (nch * NS) / NS : nch - 1;
+    const int app_c = ilv ? ((ntiles - 1 - rot + ntiles) % ntiles) % (nch * NS) / NS : nch - 1;
 
     const RowAddr<PAGED> ra(a.kv, row, g);
 
@@ -741,8 +747,8 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
         return ra.tile_blocks(t0 + ti_ * kTile, t0 + min(n, ti_ * kTile + kTile) - 1, lane);
     };
 
-    const int JS = HF ? nch * NS : kNW;        // tile stride of a wave
-    const int j0 = HF ? c * NS + slice : wave; // its first tile
+    const int JS = !HF ? kNW : ilv ? nch * NS : NS;         // tile stride of a wave
+    const int j0 = !HF ? wave : ilv ? c * NS + slice : slice; // its first tile
     int       j = j0;
     int       bt_cur = 0, bt_next = 0;
     if (j < ntiles) {
@@ -1462,10 +1468,11 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         throw std::invalid_argument("attention: a multi-chunk plan needs the partials workspace");
     const int  hpw = plan.fused_heads;
     const bool hf = hpw != 0;
-    if (hf && (D != 128 || (hpw != 2 && hpw != 4 && hpw != 8) || Hkv % hpw != 0 || plan.any_empty))
+    if (hf && (D != 128 || (hpw != 2 && hpw != 4 && hpw != 8) || Hkv % hpw != 0 ||
+               (plan.any_empty && !plan.fused_chunked)))
         throw std::invalid_argument("attention: a head-fused plan needs head_dim 128, 2, 4 or 8 "
-                                    "kv heads per workgroup dividing the kv heads, and no empty "
-                                    "sequence");
+                                    "kv heads per workgroup dividing the kv heads, and (items "
+                                    "interleaving tiles) no empty sequence");
     if (inl && inl->compact && (plan.any_multi || plan.any_empty || plan.n_work != inl->n))
         throw std::invalid_argument("attention: compact metadata needs one chunk per entry");
     AttnArgs args;

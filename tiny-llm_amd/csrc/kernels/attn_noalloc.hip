@@ -114,6 +114,7 @@ std::string attn_decode_view_noalloc(const __half *q, const KvView &kv,
     plan.any_empty = wl.any_empty;
     plan.max_len = wl.max_len;
     plan.fused_heads = wl.fused_heads;
+    plan.fused_chunked = wl.fused_chunked;
     if (!in_args) {
         words.resize(meta_words);
         std::memcpy(words.data(), seq_lens_host, nb * 4);

@@ -55,6 +55,7 @@ struct AttnPlan {
     // Head-fused plan (WorkList::fused_heads): 8-wave workgroups of
     // fused_heads kv heads, an entry's items interleaving its tiles; 0: per head.
     int            fused_heads = 0;
+    bool           fused_chunked = false; // head-fused over chunk items (ragged plans)
 };
 
 // Chunk length for the current device (TL_ATTN_CHUNK overrides), see

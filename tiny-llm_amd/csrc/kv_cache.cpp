@@ -558,6 +558,7 @@ Result<void> DecodeBatch::upload(const int *seq_ids, const int *attended, int n,
     detail::plan_work(lens_.data(), n, cfg.num_heads, cfg.head_dim, wl);
     chunk_ = wl.chunk;
     fused_heads_ = wl.fused_heads;
+    fused_chunked_ = wl.fused_chunked;
     any_multi_ = wl.any_multi;
     any_empty_ = wl.any_empty;
     n_work_ = wl.n_work;
@@ -656,6 +657,7 @@ Result<void> DecodeBatch::run_attention(int layer_idx, const half *q, const half
     plan.any_empty = any_empty_;
     plan.max_len = cfg.max_seq_len;
     plan.fused_heads = fused_heads_;
+    plan.fused_chunked = fused_chunked_;
     float *part = nullptr;
     if (any_multi_)
         part = work_->get(detail::attn_workspace_floats(n_work_, num_q_heads_, cfg.head_dim));

@@ -199,6 +199,7 @@ class DecodeBatch {
     int             chunk_ = 0;
     int             n_work_ = 0;
     int             fused_heads_ = 0;
+    bool            fused_chunked_ = false;
     bool            any_multi_ = false;
     bool            any_empty_ = false;
     std::vector<int32_t> ids_, lens_, wpos_, slot_;

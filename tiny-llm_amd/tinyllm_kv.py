@@ -88,7 +88,7 @@ class KVView(C.Structure):
 class AttnPlanInfo(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("chunk_tokens", "work_items", "waves", "any_multi",
                                        "any_empty", "max_len", "inline_words", "inline_compact",
-                                       "head_fused")]
+                                       "head_fused", "fused_chunked")]
 
 
 def _declare(L: C.CDLL) -> None:
