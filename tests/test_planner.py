@@ -46,8 +46,10 @@ def cases():
 
 
 EXPECTED = {
-    # cfg1: 4 MHA sequences of 129..513 tokens; 513 > 256 spans 3 chunks
-    "cfg1": dict(chunk_tokens=256, work_items=8, waves=8, any_multi=1, inline_words=29),
+    # cfg1: 4 MHA sequences of 129..513 tokens, at most two tiles per wave of
+    # an 8-wave workgroup: no split (a merge launch would cost more than it
+    # saves), one 768-token chunk each
+    "cfg1": dict(chunk_tokens=768, work_items=4, waves=8, any_multi=0, inline_words=21),
     # cfg2: ragged, every length within the per-CU share: one chunk each
     "cfg2": dict(chunk_tokens=4096, work_items=16, waves=8, any_multi=0, inline_words=81),
     # cfg3 (headline): 64 x 8193 tokens, one 8448-token chunk per sequence,

@@ -17,7 +17,11 @@ namespace detail {
 //    workgroups sharing a CU share its bandwidth, and longest-first ordering
 //    balances the CUs without partials or a merge launch);
 //  - longer ragged lengths: chunks of W / (2P), so that longest-first list
-//    scheduling ends within about one small item of the ideal.
+//    scheduling ends within about one small item of the ideal;
+//  - but no split at all when the longest length is at most two tiles per
+//    wave of an 8-wave workgroup (kPlanShortLen): the unsplit launch is then a
+//    couple of tile latencies long, and a split would only add the merge
+//    launch.
 int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, int cus,
                int forced_chunk) {
     int64_t total = 0;
@@ -39,7 +43,8 @@ int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, in
     const int64_t work = total * num_kv_heads;
     const bool    uniform = mn >= mx - mx / 10;
     int64_t       per;
-    if (uniform) per = (work + slots - 1) / slots;
+    if (mx <= kPlanShortLen) per = mx;
+    else if (uniform) per = (work + slots - 1) / slots;
     else if (mx <= (work + c - 1) / c) per = mx;
     else per = (work + slots - 1) / slots / 2;
     const int64_t chunk = (per + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum;

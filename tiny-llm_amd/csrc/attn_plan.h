@@ -14,6 +14,7 @@ namespace detail {
 constexpr int kPlanTile = 64;                  // tokens per wave tile
 constexpr int kPlanQuantum = 4 * kPlanTile;    // chunk lengths are multiples of this
 constexpr int kPlanSlotsPerCU = 2;             // resident 4-wave workgroups per CU
+constexpr int kPlanShortLen = 2 * 8 * kPlanTile; // never split lengths up to this
 constexpr int kPlanFusedWaves = 8;             // waves of a head-fused workgroup
 constexpr int kPlanFusedMaxItems = 8;          // head-fused items per entry, at most
 
