@@ -67,7 +67,6 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
             plan.any_empty = wl.any_empty;
             plan.max_len = wl.max_len;
             plan.fused_heads = wl.fused_heads;
-    plan.fused_chunked = wl.fused_chunked;
             plan.fused_chunked = wl.fused_chunked;
             float *part = wl.any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
             launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, nullptr, nullptr, stream,
