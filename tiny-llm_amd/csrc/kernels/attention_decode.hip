@@ -54,6 +54,10 @@
 //   P.V      v_dot2_f32_f16 on token pairs: a lane holds 8 dims of tokens t
 //            and t+TPI, v_perm_b32 interleaves them into half2
 //            (v[t][d], v[t+TPI][d]); one dot2 per (head, dim) takes two tokens.
+//            At head_dim 128 and groups 2-8 (kMfmaPV) instead on MFMA: the
+//            tile's V rows go to the wave's LDS stage as loaded, and per 16
+//            tokens O^T += V^T P^T by v_mfma_f32_16x16x16f16, V^T by the
+//            transposing ds_read_b64_tr_b16, P^T from p stored [head][token].
 // End: per-wave (m, l, o) combined across the NW waves (head-fused: the NS
 // waves of each head) in LDS; a work item that
 // covers its whole sequence is normalised and written as fp16, otherwise
@@ -338,23 +342,43 @@ __device__ __forceinline__ float h_bits2f(uint16_t x) { return (float)__builtin_
 __device__ __forceinline__ float bcast(float v, int src_lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src_lane));
 }
+typedef _Float16 f16x4m __attribute__((ext_vector_type(4)));
+typedef short    s16x4m __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __attribute__((address_space(3))) s16x4m *mma_lds(const uint16_t *p) {
+    return (__attribute__((address_space(3))) s16x4m *)(p);
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// P.V on MFMA (v_mfma_f32_16x16x16f16, O^T += V^T P^T, G of the 16 columns
+// live) instead of v_dot2 on token pairs: the VALU score path at head_dim 128
+// and groups 2 to 8.  P.V's v_dot2 (64 G per lane and tile) give way to 32
+// MFMAs, 16 transposing LDS reads and 8 LDS stores of the V rows, and the
+// accumulators shrink to 32 VGPRs.  Measured: Llama-3-8B decode (group 4)
+// 322 -> 311 us per step, group 8 and group 2 batches 3-8% faster; group 1,
+// one live column in 16, was 1.5% slower and keeps v_dot2.
+template <int D, int G, bool MFMA>
+constexpr bool kMfmaPV = !MFMA && D == 128 && G >= 2;
+
 // Dynamic shared memory of one workgroup.  Per wave one region that holds,
-// in turn, the K transpose tile of the MFMA path (16 rows of D halves, padded
-// by 8 halves so that column reads of 16 rows fall in distinct bank groups),
-// the tile's fp16 p, and at the end the wave's o[G][D] for the combine.
+// in turn, the K transpose tile of the MFMA score path (16 rows of D halves,
+// padded by 8 halves so that column reads of 16 rows fall in distinct bank
+// groups) or the tile's fp16 p (and, with the MFMA P.V, the tile's V rows
+// after it), and at the end the wave's o[G][D] for the combine.
 template <int D, int G, bool MFMA, int kNW>
 struct Smem {
     static constexpr int kKt = MFMA ? 16 * (D + 8) * 2 : 0; // bytes
     static constexpr int kPp = kTile * G * 2;
     static constexpr int kO = G * D * 4;
-    static constexpr int kA = kKt > kPp ? kKt : kPp;
+    static constexpr int kV = kMfmaPV<D, G, MFMA> ? kTile * D * 2 : 0; // V stage of the MFMA P.V
+    static constexpr int kA = (kKt > kPp ? kKt : kPp) + kV;
     static constexpr int kWave = kA > kO ? kA : kO;
+    __device__ static char  *vstage(char *wave_base) { return wave_base + kPp; }
     static constexpr int kBytes = kNW * kWave + 2 * kNW * G * 4;
     __device__ static char  *wave(char *base, int w) { return base + w * kWave; }
     __device__ static float *m(char *base) { return reinterpret_cast<float *>(base + kNW * kWave); }
@@ -489,8 +513,11 @@ struct ValuScorer {
                     const float    pv = sc[hh][s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[hh][s] - mnew);
                     const uint16_t ph = f2h_bits(pv);
                     l += h_bits2f(ph);
-                    // token s*TPI + r: pair block s/2, half s%2, q = r
-                    pp[(((s >> 1) * TPI + r) * G + h) * 2 + (s & 1)] = ph;
+                    if constexpr (kMfmaPV<D, G, false>) { // [head][token]
+                        pp[h * kTile + s * TPI + r] = ph;
+                    } else { // token s*TPI + r: pair block s/2, half s%2, q = r
+                        pp[(((s >> 1) * TPI + r) * G + h) * 2 + (s & 1)] = ph;
+                    }
                 }
             }
             lrun[hh] = lrun[hh] * alpha[hh] + l;
@@ -711,6 +738,20 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+    // MFMA P.V: O^T (dims x heads) in v_mfma_f32_16x16x16f16 tiles, lane
+    // (hc, kq) holding dims 16 dt + 4 kq .. + 3 of head hc; the tile's V rows
+    // go through the wave's LDS stage (16-byte piece x of row t at slot
+    // t * KP + (x ^ (t % KP))) and come back as V^T fragments by the
+    // transposing read, P^T from the [head][token] p the scorer writes.
+    constexpr bool MPV = kMfmaPV<D, G, MFMA>;
+    constexpr int  DT = D / 16;
+    constexpr int  KPV = D / 8;
+    f32x4          oacc[MPV ? DT : 1];
+#pragma unroll
+    for (int dt = 0; dt < (MPV ? DT : 1); ++dt) oacc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int hc = lane & 15, kq = lane >> 4;
+    uint16_t *vst = reinterpret_cast<uint16_t *>(SM::vstage(wbuf));
+    auto vslot = [](int t, int x) { return t * KPV + (x ^ (t & (KPV - 1))); };
 
     uint4     kb[2][KB];
     uint4     va[2][VB], vb[2][VB];
@@ -784,11 +825,22 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
         }
         // ---- softmax; rescale the running P.V sums
         sco.softmax(pp);
+        if constexpr (MPV) { // the lane's head hc (rows of heads >= G stay zero)
+            float al = 0.0f;
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float al = sco.head_alpha(h);
+            for (int h = 0; h < G; ++h) {
+                const float ah = sco.head_alpha(h);
+                al = hc == h ? ah : al;
+            }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= al;
+            for (int dt = 0; dt < DT; ++dt) oacc[dt] *= al;
+        } else {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float al = sco.head_alpha(h);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] *= al;
+            }
         }
         wave_sync_lds();
         // ---- P.V on token pairs
@@ -802,7 +854,13 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
             }
 #pragma unroll
             for (int u = 0; u < VB; ++u) {
-                const int       blk = bj * VB + u;
+                const int blk = bj * VB + u;
+                if constexpr (MPV) { // the pair block's rows into the V stage
+                    const int t = blk * 2 * TPI + r;
+                    *reinterpret_cast<uint4 *>(vst + vslot(t, p) * 8) = va[bj & 1][u];
+                    *reinterpret_cast<uint4 *>(vst + vslot(t + TPI, p) * 8) = vb[bj & 1][u];
+                    continue;
+                }
                 uint32_t        pw[G];
                 const uint32_t *src = reinterpret_cast<const uint32_t *>(pp) + (blk * TPI + r) * G;
                 if constexpr (G >= 4) {
@@ -837,17 +895,35 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        wave_sync_lds(); // pp / kt are rewritten by the next tile
+        if constexpr (MPV) { // O^T += V^T P^T, 16 tokens a step
+            wave_sync_lds(); // the V stage is complete
+#pragma unroll
+            for (int q = 0; q < kTile / 16; ++q) {
+                f16x4m pb = {0, 0, 0, 0};
+                if (hc < G)
+                    pb = __builtin_bit_cast(f16x4m, *reinterpret_cast<const uint2 *>(pp + hc * kTile + 16 * q + 4 * kq));
+                const int vr = 16 * q + 4 * kq + (hc >> 2), vh = 4 * (hc & 1);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int    vx = 2 * dt + ((hc & 3) >> 1);
+                    const s16x4m vf = __builtin_amdgcn_ds_read_tr16_b64_v4i16(mma_lds(vst + vslot(vr, vx) * 8 + vh));
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4m, vf), pb, oacc[dt], 0, 0, 0);
+                }
+            }
+        }
+        wave_sync_lds(); // pp / kt / the V stage are rewritten by the next tile
         bt_cur = bt_next;
     }
 
     // ---- per-wave results -> LDS
+    if constexpr (!MPV) {
 #pragma unroll
-    for (int off = LPR; off < 64; off <<= 1)
+        for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+            for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+                for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], off);
+    }
     float *sm = SM::m(smem), *sl = SM::l(smem);
     if (j0 < ntiles) {
         sco.finish(sm + wave * G, sl + wave * G);
@@ -856,7 +932,14 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
         sl[wave * G + lane] = 0.0f;
     }
     float *so = reinterpret_cast<float *>(wbuf);
-    if (r == 0) {
+    if constexpr (MPV) {
+        if (hc < G) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                *reinterpret_cast<float4 *>(so + hc * D + 16 * dt + 4 * kq) =
+                    make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
+        }
+    } else if (r == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             float *dst = so + h * D + p * 8;
@@ -923,12 +1006,6 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 // attn_decode_kernel.
 constexpr float kMmaLazy = 8.0f;
 
-typedef _Float16 f16x4m __attribute__((ext_vector_type(4)));
-typedef short    s16x4m __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __attribute__((address_space(3))) s16x4m *mma_lds(const uint16_t *p) {
-    return (__attribute__((address_space(3))) s16x4m *)(p);
-}
 
 template <int D, int G, bool PAGED, int kNW>
 __global__ __launch_bounds__(kNW * 64) void attn_decode_mma_kernel(AttnArgs a) {
