@@ -358,24 +358,32 @@ __device__ __forceinline__ void wave_sync_lds() {
 // P.V on MFMA (v_mfma_f32_16x16x16f16, O^T += V^T P^T, G of the 16 columns
 // live) instead of v_dot2 on token pairs: the VALU score path at head_dim 128
 // and groups 2 to 8.  P.V's v_dot2 (64 G per lane and tile) give way to 32
-// MFMAs, 16 transposing LDS reads and 8 LDS stores of the V rows, and the
+// MFMAs, 32 transposing LDS reads and 8 LDS stores of the V rows, and the
 // accumulators shrink to 32 VGPRs.  Measured: Llama-3-8B decode (group 4)
 // 322 -> 311 us per step, group 8 and group 2 batches 3-8% faster; group 1,
 // one live column in 16, was 1.5% slower and keeps v_dot2.
 template <int D, int G, bool MFMA>
 constexpr bool kMfmaPV = !MFMA && D == 128 && G >= 2;
+// The V stage of the MFMA P.V is a ring of two 16-token quarters per wave
+// (8 KB at head_dim 128, 69 KB an 8-wave workgroup at group 4): a quarter's
+// MFMAs run as soon as its rows are staged, while the next V batch loads.
+// Against a whole-tile stage (16 KB a wave, 132 KB a workgroup, which leaves
+// no room for a second workgroup's LDS on the CU) it measured level on
+// Llama-3-8B decode and 0.3-1.5% faster per step on ragged, churn and
+// group-8 batches.
+constexpr int kVStageQuarters = 2;
 
 // Dynamic shared memory of one workgroup.  Per wave one region that holds,
 // in turn, the K transpose tile of the MFMA score path (16 rows of D halves,
 // padded by 8 halves so that column reads of 16 rows fall in distinct bank
-// groups) or the tile's fp16 p (and, with the MFMA P.V, the tile's V rows
-// after it), and at the end the wave's o[G][D] for the combine.
+// groups) or the tile's fp16 p (and, with the MFMA P.V, the ring of staged
+// V quarters after it), and at the end the wave's o[G][D] for the combine.
 template <int D, int G, bool MFMA, int kNW>
 struct Smem {
     static constexpr int kKt = MFMA ? 16 * (D + 8) * 2 : 0; // bytes
     static constexpr int kPp = kTile * G * 2;
     static constexpr int kO = G * D * 4;
-    static constexpr int kV = kMfmaPV<D, G, MFMA> ? kTile * D * 2 : 0; // V stage of the MFMA P.V
+    static constexpr int kV = kMfmaPV<D, G, MFMA> ? kVStageQuarters * 16 * D * 2 : 0; // V stage of the MFMA P.V
     static constexpr int kA = (kKt > kPp ? kKt : kPp) + kV;
     static constexpr int kWave = kA > kO ? kA : kO;
     __device__ static char  *vstage(char *wave_base) { return wave_base + kPp; }
@@ -740,9 +748,10 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
     // MFMA P.V: O^T (dims x heads) in v_mfma_f32_16x16x16f16 tiles, lane
     // (hc, kq) holding dims 16 dt + 4 kq .. + 3 of head hc; the tile's V rows
-    // go through the wave's LDS stage (16-byte piece x of row t at slot
-    // t * KP + (x ^ (t % KP))) and come back as V^T fragments by the
-    // transposing read, P^T from the [head][token] p the scorer writes.
+    // go, a 16-token quarter at a time, through the wave's LDS stage (16-byte
+    // piece x of the quarter's row t at slot t * KP + (x ^ t)) and come back
+    // as V^T fragments by the transposing read, P^T from the [head][token] p
+    // the scorer writes.
     constexpr bool MPV = kMfmaPV<D, G, MFMA>;
     constexpr int  DT = D / 16;
     constexpr int  KPV = D / 8;
@@ -752,6 +761,14 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     const int hc = lane & 15, kq = lane >> 4;
     uint16_t *vst = reinterpret_cast<uint16_t *>(SM::vstage(wbuf));
     auto vslot = [](int t, int x) { return t * KPV + (x ^ (t & (KPV - 1))); };
+    // V batches per staged quarter, quarters per V batch.  A slot of the ring
+    // is rewritten only after the MFMAs of the quarter staged in between,
+    // which wait for that quarter's reads and so for every older LDS read.
+    constexpr int kVBT = VB * 2 * TPI; // tokens per V batch
+    constexpr int kBPQ = kVBT < 16 ? 16 / kVBT : 1;
+    constexpr int kQPB = kVBT < 16 ? 1 : kVBT / 16;
+    static_assert(!MPV || (kVBT % 16 == 0 || 16 % kVBT == 0), "V batches and quarters");
+    static_assert(!MPV || kVStageQuarters >= 2 * kQPB, "V stage ring");
 
     uint4     kb[2][KB];
     uint4     va[2][VB], vb[2][VB];
@@ -855,10 +872,11 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 #pragma unroll
             for (int u = 0; u < VB; ++u) {
                 const int blk = bj * VB + u;
-                if constexpr (MPV) { // the pair block's rows into the V stage
-                    const int t = blk * 2 * TPI + r;
-                    *reinterpret_cast<uint4 *>(vst + vslot(t, p) * 8) = va[bj & 1][u];
-                    *reinterpret_cast<uint4 *>(vst + vslot(t + TPI, p) * 8) = vb[bj & 1][u];
+                if constexpr (MPV) { // the pair block's rows into their quarter's slot
+                    const int t = blk * 2 * TPI + r; // t and t + TPI: one quarter
+                    uint16_t *vq = vst + ((t >> 4) % kVStageQuarters) * (16 * D);
+                    *reinterpret_cast<uint4 *>(vq + vslot(t & 15, p) * 8) = va[bj & 1][u];
+                    *reinterpret_cast<uint4 *>(vq + vslot((t + TPI) & 15, p) * 8) = vb[bj & 1][u];
                     continue;
                 }
                 uint32_t        pw[G];
@@ -893,23 +911,28 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[h][e] = fdot2(pw[h], vp[e], acc[h][e]);
             }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (MPV) { // O^T += V^T P^T, 16 tokens a step
-            wave_sync_lds(); // the V stage is complete
+            if constexpr (MPV) { // O^T += V^T P^T over each quarter this batch completed
+                if ((bj + 1) % kBPQ == 0) {
+                    wave_sync_lds(); // the quarter's rows are staged
 #pragma unroll
-            for (int q = 0; q < kTile / 16; ++q) {
-                f16x4m pb = {0, 0, 0, 0};
-                if (hc < G)
-                    pb = __builtin_bit_cast(f16x4m, *reinterpret_cast<const uint2 *>(pp + hc * kTile + 16 * q + 4 * kq));
-                const int vr = 16 * q + 4 * kq + (hc >> 2), vh = 4 * (hc & 1);
+                    for (int q = (bj + 1) / kBPQ * kQPB - kQPB; q < (bj + 1) / kBPQ * kQPB; ++q) {
+                        f16x4m pb = {0, 0, 0, 0};
+                        if (hc < G)
+                            pb = __builtin_bit_cast(f16x4m, *reinterpret_cast<const uint2 *>(pp + hc * kTile + 16 * q + 4 * kq));
+                        const uint16_t *vq = vst + (q % kVStageQuarters) * (16 * D);
+                        const int       vr = 4 * kq + (hc >> 2), vh = 4 * (hc & 1);
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const int    vx = 2 * dt + ((hc & 3) >> 1);
-                    const s16x4m vf = __builtin_amdgcn_ds_read_tr16_b64_v4i16(mma_lds(vst + vslot(vr, vx) * 8 + vh));
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4m, vf), pb, oacc[dt], 0, 0, 0);
+                        for (int dt = 0; dt < DT; ++dt) {
+                            const int    vx = 2 * dt + ((hc & 3) >> 1);
+                            const s16x4m vf = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                mma_lds(vq + vslot(vr, vx) * 8 + vh));
+                            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4m, vf), pb,
+                                                                             oacc[dt], 0, 0, 0);
+                        }
+                    }
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
         wave_sync_lds(); // pp / kt / the V stage are rewritten by the next tile
         bt_cur = bt_next;
