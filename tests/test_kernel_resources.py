@@ -58,16 +58,15 @@ def test_decode_kernels_use_no_argument_copy_in_scratch(tmp_path):
 
 def test_default_decode_kernels_spill_little(tmp_path):
     """The VALU score path (the default for every group) at head_dim <= 128,
-    per-head and head-fused, spills at most a few VGPRs, only at group 8 (256
-    VGPRs of 8 heads x 8 dims of accumulators; 5 for the paged 8-heads-per-
-    workgroup form)."""
+    per-head and head-fused, spills no VGPRs.  (At head_dim 128 and group 8
+    the v_dot2 P.V's 8 heads x 8 dims of accumulators spilled up to 5; the
+    MFMA P.V keeps 32 VGPRs of them.)"""
     ks = kernels("attention_decode.o", tmp_path)
     for name, r in ks.items():
         m = re.search(r"attn_decode_kernelILi(\d+)ELi(\d)ELb(\d)ELb0ELi(\d)E", name)
         if not m or int(m.group(1)) > 128:
             continue
-        g = int(m.group(2))
-        assert r["vgpr_spill_count"] <= (5 if g == 8 else 0), (name, r)
+        assert r["vgpr_spill_count"] == 0, (name, r)
 
 
 def test_w8a16_kernels_use_no_scratch(tmp_path):
