@@ -55,9 +55,11 @@
 //            and t+TPI, v_perm_b32 interleaves them into half2
 //            (v[t][d], v[t+TPI][d]); one dot2 per (head, dim) takes two tokens.
 //            At head_dim 128 and groups 2-8 (kMfmaPV) instead on MFMA: the
-//            tile's V rows go to the wave's LDS stage as loaded, and per 16
-//            tokens O^T += V^T P^T by v_mfma_f32_16x16x16f16, V^T by the
-//            transposing ds_read_b64_tr_b16, P^T from p stored [head][token].
+//            V rows go to a two-quarter ring in the wave's LDS as loaded, and
+//            per staged 16-token quarter O^T += V^T P^T by
+//            v_mfma_f32_16x16x16f16, V^T by the transposing ds_read_b64_tr_b16,
+//            P^T from p stored [head][token].  V batches are 8 tokens, 16 for
+//            the head-fused chunk items of ragged plans.
 // End: per-wave (m, l, o) combined across the NW waves (head-fused: the NS
 // waves of each head) in LDS; a work item that
 // covers its whole sequence is normalised and written as fp16, otherwise
