@@ -4,7 +4,8 @@ against the oracle.
 The bench times the decode kernel on plans that small tests do not reach:
 cfg3's head-fused plan (an 8-wave workgroup per sequence and kv head pair,
 each wave a quarter of the sequence's tiles of one head), cfg2's
-4096-token chunks, cfg4's 3328-token chunks over a permuted 16-token block
+4096-token chunks, cfg4's 5120-token chunks (two kv heads per 8-wave
+workgroup; 3/2 of the per-head plan's 3328) over a permuted 16-token block
 map of a pool larger than 4 GiB, cfg5's ~4600-token chunks over a block pool
 with hundreds of group-8 sequences and the compact metadata encoding.  Each
 test builds that state through appendKV, asserts the plan the bench reports
@@ -258,8 +259,9 @@ def test_cfg4_ragged_permuted_blocks_over_4gib(tl, orc):
     batch = tl.DecodeBatch(g, B, Hq)
     batch.prepare(ids, stream())
     info = batch.info()
-    assert info["chunk_tokens"] == 3328 and info["work_items"] == 195
-    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus())
+    assert info["chunk_tokens"] == 5120 and info["work_items"] == 163
+    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus())  # per head
+    assert (plan["chunk_tokens"], plan["work_items"]) == (3328, 195)
     assert (plan["waves"], plan["any_multi"]) == (4, 1) and plan["inline_words"] > 0
     q, nk, nv = randn(gen, (B, Hq, D)), randn(gen, (B, Hkv * D)), randn(gen, (B, Hkv * D))
     out = empty_dev((B, Hq, D))

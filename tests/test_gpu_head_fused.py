@@ -4,7 +4,8 @@ pieces of each token row at once, and a sequence's work items interleave its
 64-token tiles; split sequences are combined by the merge launch.
 
 Ragged lengths keep the chunk plan's items (longest first), with 2 heads per
-workgroup where per-head workgroups would have 4 waves.
+workgroup where per-head workgroups would have 4 waves, split sequences in
+chunks 3/2 as long.
 
 Checked for H = 2, 4 and 8 and the planner's own choice, every group size,
 contiguous and paged caches, one to eight interleaved items per sequence and
@@ -98,7 +99,12 @@ def test_head_fused_chunk_items_decode_step(tl, orc, head_fuse, run):
     assert plan["fused_chunked"] == 1 and plan["head_fused"] == (setting or 2)
     assert plan["waves"] == 8
     per_head = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True)
-    assert plan["work_items"] == per_head["work_items"] and per_head["waves"] == 4
+    assert per_head["waves"] == 4
+    if setting:  # forced heads per workgroup: the per-head plan's items
+        assert plan["work_items"] == per_head["work_items"]
+    else:  # the planner's 2 heads: split sequences in chunks 3/2 as long
+        assert plan["chunk_tokens"] >= per_head["chunk_tokens"]
+        assert plan["work_items"] <= per_head["work_items"]
     decode_step_checks(tl, orc, head_fuse, rng, setting, Hkv, G, paged, ctx, plan)
 
 

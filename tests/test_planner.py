@@ -81,13 +81,30 @@ def test_benchmark_config_plans(tl, name):
 # one per CU, so one item per sequence (4 heads: 2 items, 8 heads: 4) -- 64
 # items, no merge, metadata 64 + 65 + 2 * 64 + 64 words.  The ragged
 # configurations keep their chunk plans; cfg4 and cfg5, whose per-head
-# workgroups would have 4 waves, run them with 2 heads per 8-wave workgroup.
+# workgroups would have 4 waves, run them with 2 heads per 8-wave workgroup,
+# cfg4's split sequences in chunks 3/2 as long (3328 * 3/2 = 4992, rounded
+# up to 5120 tokens: 163 items).
 EXPECTED_FUSED = {
     "cfg3": dict(chunk_tokens=8448, work_items=64, waves=8, any_multi=0, inline_words=321,
                  head_fused=2, fused_chunked=0),
     **{k: dict(EXPECTED[k], head_fused=0, fused_chunked=0) for k in ("cfg1", "cfg2")},
-    **{k: dict(EXPECTED[k], waves=8, head_fused=2, fused_chunked=1) for k in ("cfg4", "cfg5")},
+    "cfg4": dict(EXPECTED["cfg4"], chunk_tokens=5120, work_items=163, inline_words=711, waves=8,
+                 head_fused=2, fused_chunked=1),
+    "cfg5": dict(EXPECTED["cfg5"], waves=8, head_fused=2, fused_chunked=1),
 }
+
+
+def fused_chunk_plan(per_head, lens):
+    """(chunk, items, any_multi) of the automatic 2-heads-per-workgroup
+    chunk plan: where the per-head plan splits a sequence, chunks 3/2 as long,
+    rounded up to 256 tokens and capped at the longest length."""
+    lens = np.asarray(lens, dtype=np.int64)
+    chunk = per_head["chunk_tokens"]
+    if per_head["any_multi"]:
+        cap = -(-int(lens.max()) // 256) * 256
+        chunk = min(-(-(chunk * 3 // 2) // 256) * 256, cap)
+    per_entry = -(-lens // chunk)
+    return chunk, int(per_entry.sum()), int((per_entry > 1).any())
 
 
 @pytest.mark.parametrize("name", sorted(EXPECTED_FUSED))
@@ -177,8 +194,11 @@ def test_random_plans_head_fused(tl, seed):
         else:
             want = 2 if hkv % 2 == 0 and per_head["waves"] == 4 else 0
         assert (p["head_fused"], p["fused_chunked"]) == (want, int(want > 0))
-        assert {k: p[k] for k in ("chunk_tokens", "work_items", "any_multi")} == \
-            {k: per_head[k] for k in ("chunk_tokens", "work_items", "any_multi")}
+        got = tuple(p[k] for k in ("chunk_tokens", "work_items", "any_multi"))
+        if force == 1 and want == 2:
+            assert got == fused_chunk_plan(per_head, lens)
+        else:
+            assert got == tuple(per_head[k] for k in ("chunk_tokens", "work_items", "any_multi"))
         check_invariants(p, lens, hkv, cus)
     # forced 4-wave workgroups keep the per-head plan; a forced chunk the
     # chunk plan, head-fused over its items by the same rule

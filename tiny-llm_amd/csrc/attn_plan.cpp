@@ -108,15 +108,11 @@ bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int 
     return true;
 }
 
-void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
-                    int head_fuse, WorkList &out) {
-    if (forced_chunk == 0 && plan_head_fused(lens, n, num_kv_heads, cus, head_fuse, out)) {
-        out.fused_chunked = false;
-        return;
-    }
-    out.fused_heads = 0;
-    out.fused_chunked = false;
-    out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
+namespace {
+
+// The chunk items of out.chunk over lens: part_base, and the work list
+// sorted by item length descending (then entry, chunk).
+void chunk_items(const int32_t *lens, int n, WorkList &out) {
     out.part_base.assign((size_t)std::max(n, 0) + 1, 0);
     out.any_multi = false;
     out.any_empty = false;
@@ -148,6 +144,20 @@ void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int f
         out.work[2 * w] = i;
         out.work[2 * w + 1] = row - out.part_base[(size_t)i];
     }
+}
+
+} // namespace
+
+void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
+                    int head_fuse, WorkList &out) {
+    if (forced_chunk == 0 && plan_head_fused(lens, n, num_kv_heads, cus, head_fuse, out)) {
+        out.fused_chunked = false;
+        return;
+    }
+    out.fused_heads = 0;
+    out.fused_chunked = false;
+    out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
+    chunk_items(lens, n, out);
     // Head-fused over the chunk items: forced heads per workgroup, or (auto)
     // two heads per 8-wave workgroup where the per-head plan takes 4-wave
     // workgroups -- as many waves per head, two heads' pieces of each row
@@ -160,6 +170,19 @@ void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int f
                plan_waves((int64_t)out.n_work * num_kv_heads, cus, 0) == 4) {
         out.fused_heads = 2;
         out.fused_chunked = true;
+        // These workgroups run one per CU where the per-head ones ran two:
+        // chunks kFusedChunkNum / kFusedChunkDen as long (capped at the
+        // longest length), fewer items and partials.
+        if (forced_chunk == 0 && out.any_multi) {
+            const int64_t c2 = ((int64_t)out.chunk * kFusedChunkNum / kFusedChunkDen + kPlanQuantum - 1) /
+                               kPlanQuantum * kPlanQuantum;
+            const int cap = (out.max_len + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum;
+            const int chunk = (int)std::min<int64_t>(c2, cap);
+            if (chunk != out.chunk) {
+                out.chunk = chunk;
+                chunk_items(lens, n, out);
+            }
+        }
     }
 }
 

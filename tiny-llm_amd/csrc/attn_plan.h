@@ -17,6 +17,7 @@ constexpr int kPlanSlotsPerCU = 2;             // resident 4-wave workgroups per
 constexpr int kPlanShortLen = 2 * 8 * kPlanTile; // never split lengths up to this
 constexpr int kPlanFusedWaves = 8;             // waves of a head-fused workgroup
 constexpr int kPlanFusedMaxItems = 8;          // head-fused items per entry, at most
+constexpr int kFusedChunkNum = 3, kFusedChunkDen = 2; // chunk scale of head-fused chunk items
 
 // Host side of a ragged plan: chunk length, per-entry partial-row bases and
 // the (entry, chunk) work list in longest-first order, so the hardware
