@@ -308,9 +308,7 @@ def fixed_batch(args, tl, torch, workloads, np):
     B, Hq, Hkv, D, L = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, cfg.num_layers
     ctx = cfg.contexts.astype(np.int64)
     bt = cfg.block_tokens
-    M = int((ctx.max() + K + 1 + 63) // 64 * 64)
-    if cfg.cfg == 3:  # the configuration's pool: max_seq_len 8448 (8192 + 256 decode steps)
-        M = max(M, 8448)
+    M = workloads.fixed_pool_len(cfg, K)  # the parity tests build the same pool
     if args.max_seq_len:
         if args.max_seq_len < ctx.max() + K + 1 or (bt and args.max_seq_len % bt):
             raise SystemExit(f"--max-seq-len {args.max_seq_len} cannot hold the context and "
@@ -384,10 +382,8 @@ def fixed_batch(args, tl, torch, workloads, np):
     # kv heads per attention workgroup of the last timed step's plan (1: per
     # head; 2, 4, 8: head-fused), as the library's planner makes it
     att_last = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int32)
-    hf_mode = tl.get_head_fuse()
-    hf_ok = D == 128 and hf_mode != 1 and tl.get_waves() != 4 and tl.get_score_path() in (0, 2)
     plan = tl.attn_plan(att_last, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
-                        head_fuse=(hf_mode or 1) if hf_ok else 0)
+                        head_fuse="current", head_dim=D)
     heads_per_wg = plan["head_fused"] or 1
     fused_items = ("chunks" if plan["fused_chunked"] else "interleaved tiles") if plan["head_fused"] else None
 
@@ -478,32 +474,16 @@ def churn(args, tl, torch, workloads, np):
         mgr = tl.KVCacheManager(1, Hkv, D, M, slots)
     batch = tl.DecodeBatch(mgr, slots, Hq)
     prompts_in = tl.PrefillBatch(mgr, slots, Hq)  # the batched append of a step's prompts
-
-    def append_prompts(new):
-        """The prompt K/V of a step's arrivals, (seq id, prompt) in arrival
-        order, appended with one launch per src_rows tokens: the bytes of
-        appendKV(seq, 0, rows, prompt) per arrival, then advanceSeqLen."""
-        i = 0
-        while i < len(new):
-            group, tok = [], 0
-            while i < len(new) and tok + new[i][1] <= src_rows:
-                group.append(new[i])
-                tok += new[i][1]
-                i += 1
-            prompts_in.prepare([g[0] for g in group], [g[1] for g in group], stream)
-            prompts_in.append(0, src_k.data_ptr(), src_v.data_ptr(), stream)
-            prompts_in.commit()
+    bufs = dict(q=q.data_ptr(), nk=nk.data_ptr(), nv=nv.data_ptr(), out=out.data_ptr(),
+                scale=scale, src_k=src_k.data_ptr(), src_v=src_v.data_ptr())
 
     def run(profile):
         sim = workloads.ChurnSim(hq=Hq, hkv=Hkv, head_dim=D, max_seq_len=M, slots=slots, **sim_args)
         events = list(sim.events())  # drawn before the clock starts
-        # live sequences in admission order: id, remaining decode steps, length
-        ids_a = np.zeros(slots, dtype=np.int32)
-        rem_a = np.zeros(slots, dtype=np.int64)
-        len_a = np.zeros(slots, dtype=np.int64)
-        n = 0
-        nbytes, attn_nbytes, rejected, live_sum, peak = 0, 0, 0, 0, 0
-        preempted, used_sum = 0, 0
+        # the step logic the parity tests replay (workloads.ChurnDriver)
+        drv = workloads.ChurnDriver(mgr, batch, prompts_in, slots=slots, max_seq_len=M, hq=Hq,
+                                    hkv=Hkv, head_dim=D, src_rows=src_rows, blocks=blocks,
+                                    block_tokens=bt)
         if profile:
             tl.profile_reset()
             tl.profile_enable(True)
@@ -517,55 +497,9 @@ def churn(args, tl, torch, workloads, np):
                 e = torch.cuda.Event(enable_timing=True)
                 e.record()
                 step_ev.append(e)
-            new, pending = [], 0  # admitted this step; blocks their prompts will map
-            for prompt, life in zip(ev.arrivals, ev.lifetimes):
-                sid, err = mgr.allocateSequence(M)
-                if err is None and blocks and mgr.freeBlocks() < pending + -(-prompt // bt) + n:
-                    mgr.releaseSequence(sid)  # admit only with a block of headroom per live seq
-                    err = "exhausted"
-                if err is not None:
-                    rejected += 1
-                    continue
-                new.append((sid, prompt))
-                pending += -(-prompt // bt)
-                nbytes += 2 * prompt * Hkv * D * 2 * 2  # read + write of K and V
-                ids_a[n], rem_a[n], len_a[n] = sid, max(1, life), prompt
-                n += 1
-            if new:
-                append_prompts(new)
-            if blocks:
-                # A step opens a block for every sequence at a block boundary;
-                # when the pool cannot back them, the newest sequences are
-                # preempted (released) first.
-                need = int(np.count_nonzero(len_a[:n] % bt == 0))
-                while need > mgr.freeBlocks() and n:
-                    n -= 1
-                    need -= int(len_a[n] % bt == 0)
-                    assert mgr.releaseSequence(int(ids_a[n])) is None
-                    preempted += 1
-            used_sum += mgr.getUsedMemory()
-            if n:
-                batch.prepare(ids_a[:n], stream)
-                batch.decode(0, q.data_ptr(), nk.data_ptr(), nv.data_ptr(), out.data_ptr(), scale,
-                             stream)
-                batch.commit(1)
-                sb = workloads.step_bytes(len_a[:n], Hq, Hkv, D)
-                if args.launch_log:
-                    log_launches(args.launch_log, 1, sb, n)
-                nbytes += sb
-                attn_nbytes += sb
-            live_sum += n
-            peak = max(peak, n)
-            rem_a[:n] -= 1
-            len_a[:n] += 1
-            fin = (rem_a[:n] == 0) | (len_a[:n] >= M)
-            if fin.any():
-                for s in ids_a[:n][fin]:
-                    assert mgr.releaseSequence(int(s)) is None
-                keep = ~fin
-                k = int(np.count_nonzero(keep))
-                ids_a[:k], rem_a[:k], len_a[:k] = ids_a[:n][keep], rem_a[:n][keep], len_a[:n][keep]
-                n = k
+            drv.step(ev, stream, **bufs)
+            if args.launch_log and drv.last_attn_bytes:
+                log_launches(args.launch_log, 1, drv.last_attn_bytes, drv.last_decoded)
         ev1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
@@ -575,18 +509,16 @@ def churn(args, tl, torch, workloads, np):
             step_ev.append(ev1)
             per_step = np.array([step_ev[i].elapsed_time(step_ev[i + 1])
                                  for i in range(len(step_ev) - 1)]) * 1e3
-        for s in ids_a[:n]:
-            mgr.releaseSequence(int(s))
+        drv.release_all()
         ks = None
         if profile:
             tl.profile_enable(False)
             ks = kernel_stats(tl)
             tl.profile_reset()
-        return dict(ms=ms, wall=wall, nbytes=nbytes, attn_nbytes=attn_nbytes, rejected=rejected,
-                    per_step=per_step,
-                    preempted=preempted, used_avg=used_sum / sim.steps,
-                    live_avg=live_sum / sim.steps,
-                    live_peak=peak, ks=ks)
+        return dict(ms=ms, wall=wall, nbytes=drv.nbytes, attn_nbytes=drv.attn_nbytes,
+                    rejected=drv.rejected, per_step=per_step, preempted=drv.preempted,
+                    used_avg=drv.used_sum / sim.steps, live_avg=drv.live_sum / sim.steps,
+                    live_peak=drv.peak, ks=ks)
 
     for _ in range(1 if args.warmup else 0):  # one short untimed pass warms the kernels
         sim_args["steps"] = min(K, 50)

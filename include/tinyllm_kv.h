@@ -364,20 +364,26 @@ int tl_attn_get_waves(void);
 int tl_attn_set_head_fuse(int mode);
 int tl_attn_get_head_fuse(void);
 
-/* The launch plan the decode attention entry points (tl_kv_batch_attention,
- * tl_kv_batch_decode, tl_attn_decode_gqa) make for attended lengths
- * seq_lens[0..n) on a device of num_cus compute units -- host only, no GPU
- * needed.  forced_chunk: 0, or a multiple of 256 tokens as TL_ATTN_CHUNK
- * would force; waves_setting: 0 (auto), 4 or 8 as tl_attn_set_waves;
- * head_fuse: 0 (per-head plans only), 1 (head-fused where it applies, as the
- * entry points do for head_dim 128 on the VALU score path), or 2 / 4 / 8
- * (that many kv heads per workgroup).
+/* The launch plan of the decode attention entry points (tl_kv_batch_attention,
+ * tl_kv_batch_decode, tl_attn_decode_gqa) for attended lengths
+ * seq_lens[0..n) at head_dim (32, 64, 128 or 256) on a device of num_cus
+ * compute units -- host only, no GPU needed.
+ * head_fuse = TL_PLAN_HF_CURRENT: the plan those entry points make now, under
+ * this process's settings (tl_attn_get_head_fuse, tl_attn_get_waves,
+ * tl_attn_get_score_path, TL_ATTN_CHUNK); forced_chunk / waves_setting of 0
+ * then mean "the process setting" too.
+ * head_fuse = 0 (auto), 1 (off), 2 / 4 / 8 (that many kv heads per
+ * workgroup): the codes of tl_attn_set_head_fuse, as if set, with the VALU
+ * score path; forced_chunk: 0 or a multiple of 256 tokens, as TL_ATTN_CHUNK
+ * would force; waves_setting: 0 (auto), 4 or 8, as tl_attn_set_waves.  A
+ * head-fused plan exists only for head_dim 128 with waves not forced to 4.
  * with_rows != 0 counts the slot row per entry that DecodeBatch passes.
  * Optional outputs: part_base[n + 1] (first partial row of each entry) and
  * work[2 * work_items] ((entry, chunk) pairs in launch order, longest
  * first).  No reference counterpart (planner introspection for tests and
  * tuning; the reference launches one workgroup per (sequence, head),
  * kernels/attention.cu:121-125). */
+#define TL_PLAN_HF_CURRENT (-1)
 typedef struct tl_attn_plan_info {
     int chunk_tokens;  /* tokens per work item, a multiple of 256 */
     int work_items;    /* workgroups of the attention launch / Hkv */
@@ -396,9 +402,9 @@ typedef struct tl_attn_plan_info {
                           interleave its tiles, chunk_tokens is the longest
                           length rounded up, work is in chunk-major order */
 } tl_attn_plan_info;
-int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
-                 int waves_setting, int head_fuse, int with_rows, tl_attn_plan_info *info,
-                 int32_t *part_base, int32_t *work);
+int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int head_dim, int num_cus,
+                 int forced_chunk, int waves_setting, int head_fuse, int with_rows,
+                 tl_attn_plan_info *info, int32_t *part_base, int32_t *work);
 
 /* ------------------------------------------------------------------------
  * Kernel timing (the reference has only an unused CudaEvent wrapper,

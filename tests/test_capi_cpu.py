@@ -70,3 +70,20 @@ def test_null_handles_are_rejected(tlc):
     assert lib.tl_kv_batch_prepare(None, None, 0, None) == tlc.TL_ERR_INVALID
     assert lib.tl_profile_query(b"nope", C.byref(C.c_double()), C.byref(C.c_longlong())) \
         == tlc.TL_ERR_INVALID
+
+
+def test_destructors_survive_interpreter_shutdown(tlc, monkeypatch):
+    """At interpreter shutdown module globals (load() among them) may already
+    be None when a manager or batch is collected: the destructors use the
+    handle taken at construction, so they still release the object and raise
+    nothing."""
+    freed = []
+    monkeypatch.setattr(tlc, "load", None)
+    for cls in (tlc.KVCacheManager, tlc.DecodeBatch, tlc.PrefillBatch):
+        obj = object.__new__(cls)
+        obj._h = C.c_void_p(0x1000 + len(freed))
+        obj._destroy = lambda h, name=cls.__name__: freed.append((name, h.value))
+        obj.__del__()
+        obj.__del__()  # a second close is a no-op
+        assert obj._h is None
+    assert [n for n, _ in freed] == ["KVCacheManager", "DecodeBatch", "PrefillBatch"]

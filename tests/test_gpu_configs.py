@@ -3,8 +3,7 @@ against the oracle.
 
 The bench times the decode kernel on plans that small tests do not reach:
 cfg3's head-fused plan (an 8-wave workgroup per sequence and kv head pair,
-each wave a quarter of the sequence's tiles of one head), cfg2's
-4096-token chunks, cfg4's 5120-token chunks (two kv heads per 8-wave
+each wave a quarter of the sequence's tiles of one head), cfg4's 5120-token chunks (two kv heads per 8-wave
 workgroup; 3/2 of the per-head plan's 3328) over a permuted 16-token block
 map of a pool larger than 4 GiB, cfg5's ~4600-token chunks over a block pool
 with hundreds of group-8 sequences and the compact metadata encoding.  Each
@@ -21,7 +20,8 @@ attention, the bench's call), and checks
 
 Inputs are drawn on the device (torch, seeded) and copied to the host for the
 oracle.  Set TL_PARITY_REPORT=<file> to append each test's worst error as a
-JSON line."""
+JSON line.  Config 2 at its 32 layers and config 5's churn on the bench's
+slot pool are in test_gpu_bench_geometry.py."""
 import json
 import os
 
@@ -89,11 +89,13 @@ def compact_view(orc, k_parts, v_parts, hkv, d):
 
 def test_cfg3_full_size(tl, orc):
     """Config 3 (headline): B=64, 32 q / 8 kv heads, D=128, context 8192, the
-    bench's pool (max_seq_len 8320) and two consecutive decode steps."""
+    bench's pool (max_seq_len 8448, the slot stride the bench times) and two
+    consecutive decode steps."""
     cfg = workloads.config(3)
     B, Hq, Hkv, D = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim
     ctx = int(cfg.contexts[0])
-    M = (ctx + 100 + 1 + 63) // 64 * 64
+    M = workloads.fixed_pool_len(cfg, 100)
+    assert M == 8448
     gen = torch.Generator(device="cuda")
     gen.manual_seed(workloads.seed(3, 1))
     g = tl.KVCacheManager(1, Hkv, D, M, B)
@@ -118,7 +120,7 @@ def test_cfg3_full_size(tl, orc):
         # head-fused: one 8-wave workgroup per (sequence, kv head pair), 256
         # in all, one per CU; the whole sequence per workgroup, no merge
         assert info["chunk_tokens"] == 8448 and info["work_items"] == 64
-        plan = tl.attn_plan(np.full(B, S, np.int32), Hkv, num_cus=cus(), head_fuse=True)
+        plan = tl.attn_plan(np.full(B, S, np.int32), Hkv, num_cus=cus(), head_fuse="auto")
         assert (plan["chunk_tokens"], plan["work_items"], plan["waves"], plan["head_fused"],
                 plan["any_multi"]) == (8448, 64, 8, 2, 0)
         q = randn(gen, (B, Hq, D))
@@ -147,67 +149,6 @@ def test_cfg3_full_size(tl, orc):
         vh = np.stack([pool[s, 1, :S] for s in slots])
         ctx = S
         del pool
-
-
-def test_cfg2_two_layers(tl, orc):
-    """Config 2 per layer: B=16, MHA 32/32 heads, D=128, contexts
-    U{512..4096} (the bench's seeded draw), KV ~ 0.5 N(0,1); two layers of
-    the 32 (the plan depends only on the lengths and kv heads)."""
-    cfg = workloads.config(2)
-    B, Hq, Hkv, D, L = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim, 2
-    ctx = cfg.contexts.astype(np.int64)
-    M = int((ctx.max() + 100 + 1 + 63) // 64 * 64)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(workloads.seed(2, 1))
-    g = tl.KVCacheManager(L, Hkv, D, M, B)
-    host = {}
-    ids = []
-    for b in range(B):
-        sid, err = g.allocateSequence(M)
-        assert err is None, err
-        c = int(ctx[b])
-        for layer in range(L):
-            k = randn(gen, (c, Hkv * D), cfg.kv_std)
-            v = randn(gen, (c, Hkv * D), cfg.kv_std)
-            assert g.appendKV(sid, layer, k.data_ptr(), v.data_ptr(), c, stream()) is None
-            host[b, layer] = (host_bits(k), host_bits(v))
-        g.advanceSeqLen(sid, c)
-        ids.append(sid)
-    batch = tl.DecodeBatch(g, B, Hq)
-    batch.prepare(ids, stream())
-    info = batch.info()
-    assert info["chunk_tokens"] == 4096 and info["work_items"] == 16
-    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus())
-    assert (plan["chunk_tokens"], plan["waves"], plan["any_multi"]) == (4096, 8, 0)
-    outs, qs, news = [], [], []
-    for layer in range(L):
-        q = randn(gen, (B, Hq, D), cfg.q_std)
-        nk = randn(gen, (B, Hkv * D), cfg.kv_std)
-        nv = randn(gen, (B, Hkv * D), cfg.kv_std)
-        out = empty_dev((B, Hq, D))
-        batch.decode(layer, q.data_ptr(), nk.data_ptr(), nv.data_ptr(), out.data_ptr(), cfg.scale,
-                     stream())
-        outs.append(out)
-        qs.append(q)
-        news.append((host_bits(nk), host_bits(nv)))
-    batch.commit(1)
-    pool = read_dev(g.pool(), B * g.slot_bytes() // 2).reshape(B, L, 2, M, Hkv * D)
-    slots = [g.slot_of(s) for s in ids]
-    for layer in range(L):
-        for b, s in enumerate(slots):
-            c = int(ctx[b])
-            k, v = host[b, layer]
-            assert np.array_equal(pool[s, layer, 0, :c], k)
-            assert np.array_equal(pool[s, layer, 1, :c], v)
-            assert np.array_equal(pool[s, layer, 0, c], news[layer][0][b])
-            assert np.array_equal(pool[s, layer, 1, c], news[layer][1][b])
-            assert not pool[s, layer, :, c + 1:].any()
-        view = orc.cache_view(pool.reshape(-1), L, Hkv, D, M, layer, slots)
-        ref32, _ = orc.attn_decode_gqa(host_bits(qs[layer]), view, ctx + 1, Hq, Hkv, D, cfg.scale,
-                                       nthreads=16)
-        errs = row_errors(host_bits(outs[layer]), ref32)
-        report(f"cfg2_layer{layer}", errs, {"chunk": info["chunk_tokens"]})
-        assert errs.max() <= 1e-3, (layer, float(errs.max()))
 
 
 def _check_gathered(tl, g, ids, subset, k_parts, v_parts, hkv, d):
@@ -260,7 +201,7 @@ def test_cfg4_ragged_permuted_blocks_over_4gib(tl, orc):
     batch.prepare(ids, stream())
     info = batch.info()
     assert info["chunk_tokens"] == 5120 and info["work_items"] == 163
-    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus())  # per head
+    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus(), head_fuse="off")  # per head
     assert (plan["chunk_tokens"], plan["work_items"]) == (3328, 195)
     assert (plan["waves"], plan["any_multi"]) == (4, 1) and plan["inline_words"] > 0
     q, nk, nv = randn(gen, (B, Hq, D)), randn(gen, (B, Hkv * D)), randn(gen, (B, Hkv * D))
@@ -321,7 +262,7 @@ def test_cfg5_block_pool_500_live_group8(tl, orc):
     batch = tl.DecodeBatch(g, n, Hq)
     batch.prepare(ids, stream())
     info = batch.info()
-    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus())
+    plan = tl.attn_plan((ctx + 1).astype(np.int32), Hkv, num_cus=cus(), head_fuse="off")
     assert info["chunk_tokens"] == plan["chunk_tokens"] and info["work_items"] == plan["work_items"]
     # 520 entries of one chunk each: the compact kernel-argument metadata
     assert plan["waves"] == 4 and plan["inline_compact"] == 1 and plan["inline_words"] == 780

@@ -70,7 +70,7 @@ def test_head_fused_decode_step(tl, orc, head_fuse, run, expect):
     rng = np.random.default_rng(zlib.crc32(repr(run).encode()))
     ctx = rng.integers(lo, hi + 1, B)
     lens = (ctx + 1).astype(np.int32)
-    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or 1)
+    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or "auto")
     nch = plan["work_items"] // B
     if cus() == 256:
         assert (plan["head_fused"], nch) == expect
@@ -95,10 +95,10 @@ def test_head_fused_chunk_items_decode_step(tl, orc, head_fuse, run):
     # ragged: mostly short, a few long enough to split into several chunks
     ctx = np.where(rng.random(B) < 0.1, rng.integers(3000, 4000, B), rng.integers(20, 1500, B))
     lens = (ctx + 1).astype(np.int32)
-    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or 1)
+    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse=setting or "auto")
     assert plan["fused_chunked"] == 1 and plan["head_fused"] == (setting or 2)
     assert plan["waves"] == 8
-    per_head = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True)
+    per_head = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse="off")
     assert per_head["waves"] == 4
     if setting:  # forced heads per workgroup: the per-head plan's items
         assert plan["work_items"] == per_head["work_items"]
@@ -186,14 +186,14 @@ def test_head_fused_stateless_two_plans_in_a_row(tl, orc, head_fuse):
                                    (128, (0, 2000), 3, 0)):
         rng = np.random.default_rng(seed)
         lens = rng.integers(lo, hi + 1, B).astype(np.int32)
-        p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse=True)
+        p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse="auto")
         assert p["head_fused"] in (2, 4, 8)
         if nch:  # items interleaving tiles
             assert p["fused_chunked"] == 0
             assert p["work_items"] == B * nch or cus() != 256
         else:  # ragged, an empty sequence included: chunk items, 2 heads per workgroup
             lens[7] = 0
-            p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse=True)
+            p = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=False, head_fuse="auto")
             assert p["fused_chunked"] == 1 and p["any_empty"] == 1
         M = max(1, int(lens.max()))
         pool = f16bits(rng, 2 * B * M * Hkv * D)

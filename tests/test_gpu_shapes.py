@@ -208,7 +208,7 @@ def test_decode_compact_metadata(tl, orc, score_path, path, D, G, paged):
         g.advanceSeqLen(s, int(S))
         o.advance(s, int(S))
     plan = tl.attn_plan((lens + 1).astype(np.int32), Hkv,
-                        num_cus=__import__("torch").cuda.get_device_properties(0).multi_processor_count)
+                        num_cus=__import__("torch").cuda.get_device_properties(0).multi_processor_count, head_fuse="off")
     assert plan["inline_compact"] == 1 and plan["work_items"] == n
     batch = tl.DecodeBatch(g, n, Hq)
     batch.prepare(ids, stream())

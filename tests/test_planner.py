@@ -68,7 +68,7 @@ EXPECTED = {
 @pytest.mark.parametrize("name", sorted(EXPECTED))
 def test_benchmark_config_plans(tl, name):
     lens, hkv = cases()[name]
-    p = tl.attn_plan(lens, hkv, num_cus=CUS)
+    p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="off")
     got = {k: p[k] for k in EXPECTED[name]}
     assert got == EXPECTED[name]
     assert p["max_len"] == int(lens.max())
@@ -110,7 +110,7 @@ def fused_chunk_plan(per_head, lens):
 @pytest.mark.parametrize("name", sorted(EXPECTED_FUSED))
 def test_benchmark_config_plans_head_fused(tl, name):
     lens, hkv = cases()[name]
-    p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse=True)
+    p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="auto")
     got = {k: p[k] for k in EXPECTED_FUSED[name]}
     assert got == EXPECTED_FUSED[name]
     if p["head_fused"] and not p["fused_chunked"]:
@@ -180,7 +180,8 @@ def test_random_plans_head_fused(tl, seed):
     spread = top // 10 if seed % 3 else top // 4  # within 10%, or ragged
     lens = (top - rng.integers(0, spread + 1, n)).astype(np.int32)
     force = int(rng.choice([1, 1, 2, 4, 8]))
-    p = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force)
+    hf = "auto" if force == 1 else force  # force: 1 = the planner's choice
+    p = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=hf)
     choice = fused_choice(lens, hkv, cus, force)
     if choice:
         check_fused(p, lens, hkv, cus, *choice)
@@ -188,7 +189,7 @@ def test_random_plans_head_fused(tl, seed):
     else:
         # the chunk plan, over 2 (auto, where per-head workgroups would have 4
         # waves) or the forced number of heads per workgroup
-        per_head = tl.attn_plan(lens, hkv, num_cus=cus)
+        per_head = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse="off")
         if force in (2, 4, 8):
             want = force if hkv % force == 0 else 0
         else:
@@ -202,9 +203,9 @@ def test_random_plans_head_fused(tl, seed):
         check_invariants(p, lens, hkv, cus)
     # forced 4-wave workgroups keep the per-head plan; a forced chunk the
     # chunk plan, head-fused over its items by the same rule
-    assert tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, waves=4)["head_fused"] == 0
-    pf = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=force, forced_chunk=512)
-    per_head = tl.attn_plan(lens, hkv, num_cus=cus, forced_chunk=512)
+    assert tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=hf, waves=4)["head_fused"] == 0
+    pf = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse=hf, forced_chunk=512)
+    per_head = tl.attn_plan(lens, hkv, num_cus=cus, forced_chunk=512, head_fuse="off")
     if force in (2, 4, 8):
         want = force if hkv % force == 0 else 0
     else:
@@ -216,7 +217,7 @@ def test_random_plans_head_fused(tl, seed):
 def test_head_fused_choice_examples(tl):
     """Fewest items per sequence, then more heads per workgroup (256 CUs)."""
     def pick(B, hkv, L):
-        p = tl.attn_plan(np.full(B, L, np.int32), hkv, num_cus=CUS, head_fuse=True)
+        p = tl.attn_plan(np.full(B, L, np.int32), hkv, num_cus=CUS, head_fuse="auto")
         return p["head_fused"], p["work_items"] // B
     assert pick(64, 8, 8193) == (2, 1)     # cfg3: 256 head-pair blocks
     assert pick(128, 8, 8193) == (4, 1)    # 256 blocks of 4 heads
@@ -225,7 +226,7 @@ def test_head_fused_choice_examples(tl):
     assert pick(80, 8, 8193) == (8, 3)     # only 8 heads fill 90%: 3 x 80 = 240
     assert pick(64, 4, 8193) == (2, 2)     # 4 kv heads: pairs, 2 items
     assert pick(64, 8, 600) == (2, 1)      # short sequences: one item still fills
-    p = tl.attn_plan(np.full(100, 8193, np.int32), 8, num_cus=CUS, head_fuse=True)
+    p = tl.attn_plan(np.full(100, 8193, np.int32), 8, num_cus=CUS, head_fuse="auto")
     assert (p["head_fused"], p["fused_chunked"]) == (2, 1)  # no h fills 90%: chunk plan, 2 heads
 
 
@@ -286,14 +287,14 @@ def test_random_plans_keep_invariants(tl, seed):
         lens = rng.integers(1, 600, n)
     hkv = int(rng.choice([1, 2, 8, 32]))
     cus = int(rng.choice([8, 80, 256]))
-    p = tl.attn_plan(lens.astype(np.int32), hkv, num_cus=cus)
+    p = tl.attn_plan(lens.astype(np.int32), hkv, num_cus=cus, head_fuse="off")
     check_invariants(p, lens, hkv, cus)
 
 
 @pytest.mark.parametrize("forced", [256, 512, 4096, 1 << 20])
 def test_forced_chunk_is_capped_at_the_longest_length(tl, forced):
     lens = np.array([2101, 4096, 4601, 17], dtype=np.int32)
-    p = tl.attn_plan(lens, 2, num_cus=CUS, forced_chunk=forced)
+    p = tl.attn_plan(lens, 2, num_cus=CUS, forced_chunk=forced, head_fuse="off")
     check_invariants(p, lens, 2, CUS, forced=forced)
 
 
@@ -301,17 +302,17 @@ def test_whole_sequence_chunk_gives_many_tiles_per_wave(tl):
     """A forced chunk at least as long as every sequence puts each sequence in
     one work item, so a wave of an 8-wave workgroup walks len/64/8 tiles."""
     lens = np.array([2101, 4097, 4601], dtype=np.int32)
-    p = tl.attn_plan(lens, 2, num_cus=CUS, forced_chunk=4608)
+    p = tl.attn_plan(lens, 2, num_cus=CUS, forced_chunk=4608, head_fuse="off")
     assert p["chunk_tokens"] == 4608 and p["work_items"] == 3 and p["any_multi"] == 0
     assert min(-(-int(s) // 64) // 8 for s in lens) >= 4
 
 
 def test_waves_setting_and_empty_sequences(tl):
     lens = np.array([0, 5, 0], dtype=np.int32)
-    p = tl.attn_plan(lens, 8, num_cus=CUS)
+    p = tl.attn_plan(lens, 8, num_cus=CUS, head_fuse="off")
     assert p["any_empty"] == 1 and p["work_items"] == 1
-    assert tl.attn_plan(lens, 8, num_cus=CUS, waves=4)["waves"] == 4
-    assert tl.attn_plan(np.zeros(0, np.int32), 8, num_cus=CUS)["work_items"] == 0
+    assert tl.attn_plan(lens, 8, num_cus=CUS, waves=4, head_fuse="off")["waves"] == 4
+    assert tl.attn_plan(np.zeros(0, np.int32), 8, num_cus=CUS, head_fuse="off")["work_items"] == 0
 
 
 def test_inline_metadata_limit(tl):
@@ -320,24 +321,64 @@ def test_inline_metadata_limit(tl):
     work item, the compact encoding: one word per sequence (16-bit length and
     slot) and 16 bits per work item."""
     fits = np.full(223, 100, dtype=np.int32)      # 223 + 224 + 446 + 0 = 893
-    p = tl.attn_plan(fits, 8, num_cus=CUS, with_rows=False)
+    p = tl.attn_plan(fits, 8, num_cus=CUS, with_rows=False, head_fuse="off")
     assert (p["inline_words"], p["inline_compact"]) == (893, 0)
-    p = tl.attn_plan(fits, 8, num_cus=CUS, with_rows=True)  # 1116 full words
+    p = tl.attn_plan(fits, 8, num_cus=CUS, with_rows=True, head_fuse="off")  # 1116 full words
     assert (p["inline_words"], p["inline_compact"]) == (223 + 112, 1)
     big = np.full(597, 100, dtype=np.int32)       # 597 + 299 = 896: the most that fits
-    assert tl.attn_plan(big, 8, num_cus=CUS)["inline_words"] == 896
-    assert tl.attn_plan(np.full(598, 100, np.int32), 8, num_cus=CUS)["inline_words"] == -1
+    assert tl.attn_plan(big, 8, num_cus=CUS, head_fuse="off")["inline_words"] == 896
+    assert tl.attn_plan(np.full(598, 100, np.int32), 8, num_cus=CUS, head_fuse="off")["inline_words"] == -1
     split = np.array([30000] + [100] * 300, dtype=np.int32)  # a split sequence: full only
-    p = tl.attn_plan(split, 8, num_cus=CUS)
+    p = tl.attn_plan(split, 8, num_cus=CUS, head_fuse="off")
     assert p["any_multi"] == 1 and (p["inline_words"], p["inline_compact"]) == (-1, 0)
     long_ = np.full(300, 70000, dtype=np.int32)   # lengths beyond 16 bits: full only
-    assert tl.attn_plan(long_, 1, num_cus=CUS, forced_chunk=70144)["inline_compact"] == 0
+    assert tl.attn_plan(long_, 1, num_cus=CUS, forced_chunk=70144, head_fuse="off")["inline_compact"] == 0
 
 
 def test_plan_rejects_bad_arguments(tl):
     with pytest.raises(tl.TinyLLMError):
-        tl.attn_plan(np.array([-1], np.int32), 8)
+        tl.attn_plan(np.array([-1], np.int32), 8, head_fuse="off")
     with pytest.raises(tl.TinyLLMError):
-        tl.attn_plan(np.array([1], np.int32), 0)
+        tl.attn_plan(np.array([1], np.int32), 0, head_fuse="off")
     with pytest.raises(tl.TinyLLMError):
-        tl.attn_plan(np.array([1], np.int32), 8, waves=3)
+        tl.attn_plan(np.array([1], np.int32), 8, waves=3, head_fuse="off")
+    with pytest.raises(tl.TinyLLMError):
+        tl.attn_plan(np.array([1], np.int32), 8, head_dim=96)
+    with pytest.raises(ValueError):
+        tl.attn_plan(np.array([1], np.int32), 8, head_fuse=True)
+
+
+def test_current_mode_follows_the_process_settings(tl, monkeypatch):
+    """head_fuse="current" is the entry points' plan: the head-fuse setter's
+    mode, the waves setting and TL_ATTN_CHUNK, at the given head_dim; the
+    explicit codes are the setter's (0 auto, 1 off, 2 / 4 / 8 forced)."""
+    lens = np.full(64, 8193, np.int32)  # config 3: head-fused, 2 kv heads per workgroup
+    keys = ("chunk_tokens", "work_items", "waves", "head_fused", "fused_chunked")
+
+    def plan(**kw):
+        p = tl.attn_plan(lens, 8, num_cus=CUS, **kw)
+        return tuple(p[k] for k in keys)
+    hf0, w0 = tl.get_head_fuse(), tl.get_waves()
+    monkeypatch.delenv("TL_ATTN_CHUNK", raising=False)
+    try:
+        tl.set_head_fuse(0)
+        tl.set_waves(0)
+        assert plan(head_fuse="current") == plan(head_fuse="auto")
+        assert plan(head_fuse="current")[3] == 2
+        assert plan(head_fuse="current", head_dim=64) == plan(head_fuse="off", head_dim=64)
+        assert plan(head_fuse="auto", head_dim=64)[3] == 0  # no head-fused form at 64
+        tl.set_head_fuse(1)
+        assert plan(head_fuse="current") == plan(head_fuse="off")
+        assert plan(head_fuse="current")[3] == 0
+        tl.set_head_fuse(4)
+        assert plan(head_fuse="current") == plan(head_fuse=4)
+        tl.set_head_fuse(0)
+        tl.set_waves(4)
+        assert plan(head_fuse="current") == plan(head_fuse="off", waves=4)
+        tl.set_waves(0)
+        monkeypatch.setenv("TL_ATTN_CHUNK", "1024")
+        assert plan(head_fuse="current") == plan(head_fuse="auto", forced_chunk=1024)
+        assert plan(head_fuse="current")[0] == 1024
+    finally:
+        tl.set_head_fuse(hf0)
+        tl.set_waves(w0)

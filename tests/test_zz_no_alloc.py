@@ -63,17 +63,20 @@ def test_noalloc_matches_decode_gqa_twice_then_smaller(tl, orc):
     # call 1: 300 sequences, one of 30000 tokens split into many chunks
     # (partials in the scratch), metadata beyond the kernel arguments (filled
     # into the scratch by the metadata kernel), empty sequences included
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
     lens1 = np.concatenate([[30000, 0], rng.integers(1, 1000, 298)]).astype(np.int32)
-    p1 = tl.attn_plan(lens1, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
-                      with_rows=False)
-    assert p1["any_multi"] == 1 and p1["inline_words"] == -1
+    # the plan the entry point runs: ragged lengths, the chunk plan's items
+    # with 2 kv heads per 8-wave workgroup
+    p1 = tl.attn_plan(lens1, Hkv, num_cus=ncu, with_rows=False, head_fuse="current")
+    assert p1["any_multi"] == 1 and p1["any_empty"] == 1 and p1["inline_words"] == -1
+    assert (p1["head_fused"], p1["fused_chunked"]) == (2, 1) or ncu != 256
     run_pair(tl, orc, rng, lens1, Hq, Hkv, D)
     # call 2: five sequences, metadata in the kernel arguments, partials in
     # the scratch the first call left behind
     lens2 = np.array([5000, 100, 0, 3000, 1], dtype=np.int32)
-    p2 = tl.attn_plan(lens2, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
-                      with_rows=False)
+    p2 = tl.attn_plan(lens2, Hkv, num_cus=ncu, with_rows=False, head_fuse="current")
     assert p2["any_multi"] == 1 and p2["inline_words"] > 0
+    assert p2["head_fused"] == 0 or ncu != 256  # 8-wave per-head workgroups
     run_pair(tl, orc, rng, lens2, Hq, Hkv, D)
 
 
@@ -86,7 +89,7 @@ def test_noalloc_head_fused_twice_then_smaller(tl, orc):
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     for B, lo, hi, nch in ((32, 4200, 4400, 2), (64, 2048, 2100, 1)):
         lens = rng.integers(lo, hi + 1, B).astype(np.int32)
-        p = tl.attn_plan(lens, Hkv, num_cus=ncu, with_rows=False, head_fuse=True)
+        p = tl.attn_plan(lens, Hkv, num_cus=ncu, with_rows=False, head_fuse="current")
         assert p["head_fused"] == 2 or ncu != 256
         assert p["work_items"] == B * nch or ncu != 256
         run_pair(tl, orc, rng, lens, Hq, Hkv, D)
@@ -108,3 +111,68 @@ def test_noalloc_rejects_calls_beyond_the_scratch(tl, monkeypatch):
                                    stream())
     torch.cuda.synchronize()
     assert not out.any().item()
+
+
+def test_noalloc_allocates_nothing_on_a_first_large_call(tl, orc):
+    """After one small call (code objects loaded, the scratch address looked
+    up), a first call with a much larger split plan leaves the device's free
+    memory unchanged to the byte."""
+    rng = np.random.default_rng(20261204)
+    Hq, Hkv, D = 32, 8, 128
+    keep = run_pair(tl, orc, rng, np.array([300, 17], dtype=np.int32), Hq, Hkv, D)
+    lens = np.concatenate([[24000, 0], rng.integers(1, 3000, 250)]).astype(np.int32)
+    keep2, view, _, _, _ = paged_cache(tl, rng, lens, Hkv, D)
+    q = torch.randn((len(lens), Hq, D), dtype=torch.float16, device="cuda")
+    out = torch.empty((len(lens), Hq, D), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    tl.attn_decode_gqa_noalloc(q.data_ptr(), view, lens, Hq, Hkv, D, 0.0884, out.data_ptr(),
+                               stream())
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.isfinite(out.float()).all().item()
+    del keep, keep2
+
+
+def test_noalloc_replays_under_hip_graph_capture(tl, orc):
+    """A call captured in a HIP graph (torch.cuda.CUDAGraph; the split-K
+    partials and the plan metadata in the static scratch, the metadata
+    written by a kernel) and replayed on new cache and query values, with
+    eager calls between the replays: every replay equals tl_attn_decode_gqa
+    on the same inputs, bit for bit."""
+    rng = np.random.default_rng(20261205)
+    Hq, Hkv, D = 32, 8, 128
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    lens = np.concatenate([[20000, 0], rng.integers(1, 2000, 298)]).astype(np.int32)
+    p = tl.attn_plan(lens, Hkv, num_cus=ncu, with_rows=False, head_fuse="current")
+    assert p["any_multi"] == 1 and p["inline_words"] == -1  # partials and metadata in scratch
+    (dpool, dbt), view, _, _, _ = paged_cache(tl, rng, lens, Hkv, D)
+    B = len(lens)
+    dq = torch.randn((B, Hq, D), dtype=torch.float16, device="cuda")
+    got = torch.empty((B, Hq, D), dtype=torch.float16, device="cuda")
+    ref = torch.empty((B, Hq, D), dtype=torch.float16, device="cuda")
+    scale = 1.0 / np.sqrt(D)
+    # warm-up outside the capture: per-device set-up happens on a first call
+    tl.attn_decode_gqa_noalloc(dq.data_ptr(), view, lens, Hq, Hkv, D, scale, got.data_ptr(),
+                               stream())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        tl.attn_decode_gqa_noalloc(dq.data_ptr(), view, lens, Hq, Hkv, D, scale, got.data_ptr(),
+                                   stream())
+    torch.cuda.synchronize()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(20261205)
+    for rep in range(3):
+        dq.copy_(torch.randn(dq.shape, generator=gen, device="cuda", dtype=torch.float16))
+        dpool.copy_(torch.randn(dpool.shape, generator=gen, device="cuda",
+                                dtype=torch.float16).view(torch.int16))
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        tl.attn_decode_gqa(dq.data_ptr(), view, lens, Hq, Hkv, D, scale, ref.data_ptr(), stream())
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(got), to_host(ref)), f"replay {rep} differs"
+        assert torch.isfinite(got.float()).all().item()
+    del graph

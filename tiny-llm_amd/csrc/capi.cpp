@@ -513,23 +513,40 @@ int tl_attn_set_head_fuse(int mode) {
 
 int tl_attn_get_head_fuse(void) { return tiny_llm::detail::head_fuse(); }
 
-int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int num_cus, int forced_chunk,
-                 int waves_setting, int head_fuse, int with_rows, tl_attn_plan_info *info,
-                 int32_t *part_base, int32_t *work) {
+int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int head_dim, int num_cus,
+                 int forced_chunk, int waves_setting, int head_fuse, int with_rows,
+                 tl_attn_plan_info *info, int32_t *part_base, int32_t *work) {
     if (!info) return fail(TL_ERR_INVALID, "tl_attn_plan: info is null");
     if (n < 0 || (n > 0 && !seq_lens)) return fail(TL_ERR_INVALID, "tl_attn_plan: invalid lengths");
     if (num_kv_heads <= 0 || num_cus <= 0)
         return fail(TL_ERR_INVALID, "tl_attn_plan: num_kv_heads and num_cus must be positive");
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail(TL_ERR_INVALID, "tl_attn_plan: head_dim must be 32, 64, 128 or 256");
     if (waves_setting != 0 && waves_setting != 4 && waves_setting != 8)
         return fail(TL_ERR_INVALID, "tl_attn_plan: waves_setting must be 0 (auto), 4 or 8");
+    if (head_fuse != TL_PLAN_HF_CURRENT && head_fuse != 0 && head_fuse != 1 && head_fuse != 2 &&
+        head_fuse != 4 && head_fuse != 8)
+        return fail(TL_ERR_INVALID, "tl_attn_plan: head_fuse must be TL_PLAN_HF_CURRENT (-1), "
+                                    "0 (auto), 1 (off), 2, 4 or 8");
+    if (forced_chunk < 0) return fail(TL_ERR_INVALID, "tl_attn_plan: forced_chunk must be >= 0");
     for (int i = 0; i < n; ++i)
         if (seq_lens[i] < 0) return fail(TL_ERR_INVALID, "tl_attn_plan: negative sequence length");
     return guarded([&] {
         namespace d = tiny_llm::detail;
         d::WorkList wl;
-        const int fuse = waves_setting == 4 || head_fuse == 0 ? 0
-                         : head_fuse == 2 || head_fuse == 4 || head_fuse == 8 ? head_fuse
-                                                                              : 1;
+        int fuse; // planner argument: 0 = per head, 1 = auto, 2 / 4 / 8 = forced
+        if (head_fuse == TL_PLAN_HF_CURRENT) {
+            // exactly the entry points' plan: the process settings
+            if (forced_chunk == 0) forced_chunk = d::chunk_override_from_env();
+            if (waves_setting == 0) waves_setting = d::waves();
+            fuse = d::planner_head_fuse(head_dim);
+        } else {
+            // the setter's codes; a head-fused form exists for head_dim 128
+            // when waves are not forced to 4
+            fuse = head_dim != 128 || waves_setting == 4 || head_fuse == 1 ? 0
+                   : head_fuse == 0                                        ? 1
+                                                                           : head_fuse;
+        }
         d::plan_work_list(seq_lens, n, num_kv_heads, num_cus, forced_chunk, fuse, wl);
         info->chunk_tokens = wl.chunk;
         info->work_items = wl.n_work;

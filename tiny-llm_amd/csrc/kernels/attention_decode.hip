@@ -1552,11 +1552,14 @@ bool head_fused_kernel(int head_dim) {
            !use_mfma_scores(head_dim, 0) && !use_mma_path(head_dim, 0);
 }
 
-void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out) {
-    // planner argument: 0 = per head, 1 = auto, 2 / 4 / 8 = forced heads per workgroup
+int planner_head_fuse(int head_dim) {
     const int mode = head_fuse_setting();
-    const int fuse = !head_fused_kernel(head_dim) ? 0 : mode == 0 ? 1 : mode;
-    plan_work_list(lens, n, num_kv_heads, device_cus(), chunk_override_from_env(), fuse, out);
+    return !head_fused_kernel(head_dim) ? 0 : mode == 0 ? 1 : mode;
+}
+
+void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkList &out) {
+    plan_work_list(lens, n, num_kv_heads, device_cus(), chunk_override_from_env(),
+                   planner_head_fuse(head_dim), out);
 }
 
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,

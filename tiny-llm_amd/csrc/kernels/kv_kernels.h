@@ -147,6 +147,10 @@ int  waves();
 // heads per workgroup where a plan with it applies.
 void set_head_fuse(int mode);
 int  head_fuse();
+// The head_fuse argument plan_work passes to plan_work_list for this
+// head_dim under the current settings (head-fuse mode, waves, score path):
+// 0 = per-head plans only, 1 = auto, 2 / 4 / 8 = forced heads per workgroup.
+int planner_head_fuse(int head_dim);
 
 // Compute units of the current device (cached per device).
 int device_cus();

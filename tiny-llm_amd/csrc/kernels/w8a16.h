@@ -42,8 +42,11 @@ struct CacheRows {
 // segment's n % 16 == 0); other shapes take the reference-order kernel.
 bool w8a16_mfma_ok(int K, int gs, const W8A16Seg *segs, int nseg);
 
-// fp32 workspace (elements) that launch_w8a16 needs for split-K partials
-// (none for M <= 64: that kernel runs over the whole of K).
+// fp32 workspace (elements) that launch_w8a16 needs for split-K partials,
+// the only source of that size.  It is 0 where w8a16_dec_kernel takes the
+// shape -- M <= 64, K a multiple of 128 and at most 4096, every segment's
+// n * K below 2^31 -- because that kernel runs over the whole of K; other
+// MFMA shapes (e.g. M <= 64 with K = 14336) take the split-K pair and need it.
 size_t w8a16_workspace_floats(int M, int K, int gs, const W8A16Seg *segs, int nseg);
 
 // out = x @ dequant(W_i, s_i) for each segment i, with its epilogue.  x [M][K]

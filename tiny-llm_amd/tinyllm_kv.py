@@ -156,7 +156,7 @@ def _declare(L: C.CDLL) -> None:
         "tl_attn_get_waves": (i, []),
         "tl_attn_set_head_fuse": (i, [i]),
         "tl_attn_get_head_fuse": (i, []),
-        "tl_attn_plan": (i, [vp, i, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
+        "tl_attn_plan": (i, [vp, i, i, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
         "tl_profile_enable": (None, [i]),
         "tl_profile_reset": (None, []),
         "tl_profile_query": (i, [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
@@ -200,6 +200,9 @@ class KVCacheManager:
         """block_tokens > 0: a block-granular pool of num_blocks blocks
         (tl_kv_create_paged); otherwise the reference's slot pool."""
         L = load()
+        # the destructor's handle: module globals may already be None when a
+        # manager is collected at interpreter shutdown
+        self._destroy = L.tl_kv_destroy
         self.config = KVConfig(num_layers, num_heads, head_dim, max_seq_len, max_batch_size)
         self._h = C.c_void_p()
         if block_tokens:
@@ -218,7 +221,7 @@ class KVCacheManager:
 
     def close(self):
         if getattr(self, "_h", None):
-            load().tl_kv_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -320,11 +323,12 @@ class DecodeBatch:
     def __init__(self, mgr: KVCacheManager, max_seqs: int, num_q_heads: int):
         self._mgr = mgr
         self._h = C.c_void_p()
+        self._destroy = load().tl_kv_batch_destroy  # usable at interpreter shutdown
         _check(load().tl_kv_batch_create(mgr._h, max_seqs, num_q_heads, C.byref(self._h)))
 
     def close(self):
         if getattr(self, "_h", None):
-            load().tl_kv_batch_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -375,11 +379,12 @@ class PrefillBatch:
     def __init__(self, mgr: KVCacheManager, max_seqs: int, num_q_heads: int):
         self.mgr = mgr
         self._h = C.c_void_p()
+        self._destroy = load().tl_kv_prefill_destroy  # usable at interpreter shutdown
         _check(load().tl_kv_prefill_create(mgr._h, max_seqs, num_q_heads, C.byref(self._h)))
 
     def close(self):
         if getattr(self, "_h", None):
-            load().tl_kv_prefill_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -486,26 +491,31 @@ def get_head_fuse() -> int:
     return load().tl_attn_get_head_fuse()
 
 
+_HEAD_FUSE_CODES = {"current": -1, "auto": 0, "off": 1, 2: 2, 4: 4, 8: 8}
+
+
 def attn_plan(seq_lens, num_kv_heads, num_cus=256, forced_chunk=0, waves=0, with_rows=True,
-              head_fuse=False):
+              head_fuse="current", head_dim=128):
     """The decode attention launch plan for these attended lengths (host
     only): a dict of tl_attn_plan_info plus part_base and the work list as
-    (entry, chunk) pairs in launch order.  head_fuse: False / 0 = per-head
-    plans only; True / 1 = head-fused where it applies, as the entry points do
-    for head_dim 128 on the VALU score path; 2 / 4 / 8 = that many kv heads
-    per workgroup."""
+    (entry, chunk) pairs in launch order.  head_fuse: "current" = the plan the
+    decode entry points make now, under this process's settings (head-fuse
+    mode, waves, score path, TL_ATTN_CHUNK; forced_chunk / waves of 0 mean
+    the process setting); "auto" / "off" / 2 / 4 / 8 = the codes of
+    set_head_fuse, as if set."""
     import numpy as np
+    if isinstance(head_fuse, bool) or head_fuse not in _HEAD_FUSE_CODES:
+        raise ValueError(f"head_fuse must be one of {list(_HEAD_FUSE_CODES)}, not {head_fuse!r}")
+    code = _HEAD_FUSE_CODES[head_fuse]
     lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
     n = lens.size
     info = AttnPlanInfo()
-    _check(load().tl_attn_plan(lens.ctypes.data if n else None, n, num_kv_heads, num_cus,
-                               forced_chunk, waves, int(head_fuse), int(with_rows), C.byref(info),
-                               None, None))
+    args = (lens.ctypes.data if n else None, n, num_kv_heads, head_dim, num_cus, forced_chunk, waves,
+            code, int(with_rows), C.byref(info))
+    _check(load().tl_attn_plan(*args, None, None))
     part = np.zeros(n + 1, dtype=np.int32)
     work = np.zeros(max(1, 2 * info.work_items), dtype=np.int32)
-    _check(load().tl_attn_plan(lens.ctypes.data if n else None, n, num_kv_heads, num_cus,
-                               forced_chunk, waves, int(head_fuse), int(with_rows), C.byref(info),
-                               part.ctypes.data, work.ctypes.data))
+    _check(load().tl_attn_plan(*args, part.ctypes.data, work.ctypes.data))
     out = {name: getattr(info, name) for name, _ in AttnPlanInfo._fields_}
     out["part_base"] = part
     out["work"] = work[:2 * info.work_items].reshape(-1, 2)
