@@ -35,6 +35,11 @@ sys.path.insert(0, os.path.join(REPO, "tiny-llm_amd"))
 METRIC = ("decode attn+KV append µs/step and achieved HBM GB/s (% of peak), "
           "8B GQA b64 ctx8k")
 HBM_PEAK_GBPS = 8000.0
+CPU_FORM = ("orc_attn_decode_gqa_fast: AVX2/F16C, eight tokens per register for the scores, "
+            "eight d for P.V, each K/V row read once per GQA group; the checker's bits")
+GEN_NOTE = ("seeded splitmix64 -> Box-Muller -> fp16 streams drawn on the device by "
+            "tl_fill_normal_f16, seed 20261201 + 1000*set + stream; the oracle's generator "
+            "element for element")
 
 
 def parse():
@@ -45,8 +50,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5),
                     help="1: latency of the small MHA case; 2-4: fixed batches; 5: churn")
-    ap.add_argument("--path", default="decode", choices=("decode", "project", "oproj", "prefill"),
-                    help="decode: append + attention (the headline); project: the decode step's "
+    ap.add_argument("--path", default="decode",
+                    choices=("decode", "project", "oproj", "prefill", "legacy"),
+                    help="decode: append + attention (the headline); legacy: the reference's "
+                         "attention_decode entry point at the shape of its own performance table "
+                         "(B=1, H=32, D=128, S = 128 / 512 / 2048 / 8192); project: the decode step's "
                          "fused QKV W8A16 projection writing K/V into the cache; oproj: the W8A16 "
                          "o_proj + residual (Llama-3-8B layer shapes, batch 64); prefill: prompt "
                          "tokens appended and attended causally over the cache")
@@ -135,6 +143,7 @@ def cpu_baseline_fixed(st, target_s: float):
     import oracle as orc
     import workloads
 
+    build = orc.use_native_build()
     mgr, ids, L, Hq, Hkv, D, M = st["mgr"], st["ids"], st["L"], st["Hq"], st["Hkv"], st["D"], st["M"]
     B = len(ids)
     o = orc.KVCacheOracle(L, Hkv, D, M, B)
@@ -173,7 +182,7 @@ def cpu_baseline_fixed(st, target_s: float):
                 else:
                     o.append(x, layer, nkh[layer][i], nvh[layer][i], 1)
             orc.attn_decode_gqa(qh[layer], views[layer], lens + 1, Hq, Hkv, D, st["scale"],
-                                nthreads=threads)
+                                nthreads=threads, fast=True)
         for x in oids:
             o.advance(x, 1)
         t_used += time.perf_counter() - t0
@@ -182,10 +191,11 @@ def cpu_baseline_fixed(st, target_s: float):
         steps += 1
     return {"value": round(total_bytes / t_used / 1e9, 3), "unit": "GB/s",
             "us_per_step": round(t_used / steps * 1e6, 1), "cores": threads, "kind": "port",
-            "sample": f"oracle C restatement on the GPU run's final cache (copied byte for byte), "
-                      f"full batch of {B} sequences x {L} layer(s), {steps} decode steps "
-                      f"(append + attention + advance), {t_used:.1f} s, {threads} OpenMP threads "
-                      f"of {nproc} CPUs in the affinity mask, cpu={_cpu_model()}"}
+            "sample": f"oracle C restatement ({CPU_FORM}; {build}) on the GPU run's final cache "
+                      f"(copied byte for byte), full batch of {B} sequences x {L} layer(s), "
+                      f"{steps} decode steps (append + attention + advance), {t_used:.1f} s, "
+                      f"{threads} OpenMP threads of {nproc} CPUs in the affinity mask, "
+                      f"cpu={_cpu_model()}"}
 
 
 def cpu_baseline_churn(st, target_s: float):
@@ -202,6 +212,7 @@ def cpu_baseline_churn(st, target_s: float):
     import oracle as orc
     import workloads
 
+    build = orc.use_native_build()
     K, M, slots, Hq, Hkv, D = st["K"], st["M"], st["slots"], st["Hq"], st["Hkv"], st["D"]
     o = orc.KVCacheOracle(1, Hkv, D, M, slots)
     sim = workloads.ChurnSim(steps=K, hq=Hq, hkv=Hkv, head_dim=D, max_seq_len=M, slots=slots)
@@ -233,7 +244,7 @@ def cpu_baseline_churn(st, target_s: float):
             lens = np.fromiter((length[x] + 1 for x in ids), dtype=np.int64, count=len(ids))
             view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(x) for x in ids])
             orc.attn_decode_gqa(st["q"][:len(ids)], view, lens, Hq, Hkv, D, st["scale"],
-                                nthreads=threads)
+                                nthreads=threads, fast=True)
         for sid in ids:
             o.advance(sid, 1)
             live[sid] -= 1
@@ -253,7 +264,8 @@ def cpu_baseline_churn(st, target_s: float):
     return {"value": round(dec_bytes / t_dec / 1e9, 3) if t_dec else None, "unit": "GB/s",
             "us_per_step": round(t_dec / max(1, dec_steps) * 1e6, 1), "cores": threads,
             "kind": "port",
-            "sample": f"oracle C restatement replaying the same {K}-step event sequence on the "
+            "sample": f"oracle C restatement ({CPU_FORM}; {build}) replaying the same {K}-step "
+                      f"event sequence on the "
                       f"reference's slot allocator: {dec_steps} full decode steps (every {every}th "
                       f"step, {live_sampled / max(1, dec_steps):.0f} live sequences on average) "
                       f"timed, {t_dec:.1f} s; bookkeeping, prompt and token appends of all steps "
@@ -327,22 +339,22 @@ def fixed_batch(args, tl, torch, workloads, np):
     if bt:  # config 4: 16-token blocks behind a seeded random permutation
         perm = workloads.block_permutation(B * M // bt, workloads.seed(cfg.cfg, 4))
         assert mgr.setBlockMap(bt, perm) is None
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(workloads.seed(cfg.cfg, 1))
+    ns = tl.NormalStreams(stream)  # seeded device streams: Q 0, K 1, V 2 (workloads.seed)
+    s_q, s_k, s_v = (workloads.seed(cfg.cfg, i) for i in range(3))
     ids = []
     for b in range(B):  # prefill through appendKV, as InferenceEngine::prefill does
         sid, err = mgr.allocateSequence(M)
         assert err is None, err
         c = int(ctx[b])
         for layer in range(L):
-            k = torch.randn((c, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
-            v = torch.randn((c, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
+            k = ns.draw(s_k, (c, Hkv * D), cfg.kv_std)
+            v = ns.draw(s_v, (c, Hkv * D), cfg.kv_std)
             assert mgr.appendKV(sid, layer, k.data_ptr(), v.data_ptr(), c, stream) is None
         mgr.advanceSeqLen(sid, c)
         ids.append(sid)
-    q = torch.randn((L, B, Hq, D), generator=gen, device=dev, dtype=torch.float16) * cfg.q_std
-    nk = torch.randn((L, B, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
-    nv = torch.randn((L, B, Hkv * D), generator=gen, device=dev, dtype=torch.float16) * cfg.kv_std
+    q = ns.draw(s_q, (L, B, Hq, D), cfg.q_std)
+    nk = ns.draw(s_k, (L, B, Hkv * D), cfg.kv_std)  # the K / V streams continue
+    nv = ns.draw(s_v, (L, B, Hkv * D), cfg.kv_std)
     out = torch.empty((B, Hq, D), device=dev, dtype=torch.float16)
     batch = tl.DecodeBatch(mgr, B, Hq)
     torch.cuda.synchronize()
@@ -426,7 +438,7 @@ def fixed_batch(args, tl, torch, workloads, np):
             "chunk_tokens": info["chunk_tokens"], "work_items": info["work_items"],
             "kv_heads_per_workgroup": heads_per_wg, "head_fused_items": fused_items,
             "parallelism": "single GPU"}
-    data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) (torch.randn, seeded), prefilled "
+    data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) ({GEN_NOTE}), prefilled "
             f"via appendKV" + (", 16-token blocks behind a seeded random permutation" if bt else ""))
     cpu = None
     if args.cpu_baseline and not blocks:
@@ -457,15 +469,15 @@ def churn(args, tl, torch, workloads, np):
         slots = min(slots, budget // slot_bytes)
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream().cuda_stream
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(workloads.seed(5, 1))
+    ns = tl.NormalStreams(stream)  # seeded device streams: Q 0, K 1, V 2 (workloads.seed)
+    s_q, s_k, s_v = (workloads.seed(5, i) for i in range(3))
     # prompt K/V: a step's arrivals take consecutive rows of these, from row 0
     src_rows = 32768
-    src_k = torch.randn((src_rows, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    src_v = torch.randn((src_rows, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    q = torch.randn((slots, Hq, D), generator=gen, device=dev, dtype=torch.float16)
-    nk = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    nv = torch.randn((slots, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    src_k = ns.draw(s_k, (src_rows, Hkv * D))
+    src_v = ns.draw(s_v, (src_rows, Hkv * D))
+    q = ns.draw(s_q, (slots, Hq, D))
+    nk = ns.draw(s_k, (slots, Hkv * D))
+    nv = ns.draw(s_v, (slots, Hkv * D))
     out = torch.empty((slots, Hq, D), device=dev, dtype=torch.float16)
     scale = 1.0 / float(np.sqrt(D))
     if blocks:
@@ -549,7 +561,7 @@ def churn(args, tl, torch, workloads, np):
     return dict(cfg=None, K=K, elapsed_ms=timed["ms"], t_wall=timed["wall"],
                 total_bytes=timed["nbytes"], attn_bytes=prof["attn_nbytes"] / launches, ks=ks,
                 kpass=K, conf=conf, per_step_us=prof["per_step"], cpu=cpu,
-                data="synthetic: KV/Q ~ N(0,1) (torch.randn, seeded); Poisson/uniform/geometric "
+                data=f"synthetic: KV/Q ~ N(0,1) ({GEN_NOTE}); Poisson/uniform/geometric "
                      "events from the seeded simulator",
                 kpass_desc=f"second run of the same {K}-step event sequence")
 
@@ -564,25 +576,26 @@ def prefill_bench(args, tl, torch, np):
     append).  The cache is
     rewound after each step (lengths are not committed), so every step
     repeats the same work."""
+    import workloads
     Hq, Hkv, D = 32, 8, 128
     nseq, n, p0 = args.prefill_seqs, args.prefill_tokens, args.prefill_prefix
     K = args.steps or 20
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream().cuda_stream
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(20261201 + 11)
+    ns = tl.NormalStreams(stream)
+    s_q, s_k, s_v = (workloads.seed(7, i) for i in range(3))  # prefill: stream set 7
     M = ((p0 + n + 63) // 64) * 64
     mgr = tl.KVCacheManager(1, Hkv, D, M, nseq)
     ids = [mgr.allocateSequence(M)[0] for _ in range(nseq)]
     if p0:
-        pk = torch.randn((p0, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+        pk = ns.draw(s_k, (p0, Hkv * D))
         for sid in ids:
             assert mgr.appendKV(sid, 0, pk.data_ptr(), pk.data_ptr(), p0, stream) is None
             mgr.advanceSeqLen(sid, p0)
     T = nseq * n
-    q = torch.randn((T, Hq, D), generator=gen, device=dev, dtype=torch.float16)
-    nk = torch.randn((T, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
-    nv = torch.randn((T, Hkv * D), generator=gen, device=dev, dtype=torch.float16)
+    q = ns.draw(s_q, (T, Hq, D))
+    nk = ns.draw(s_k, (T, Hkv * D))
+    nv = ns.draw(s_v, (T, Hkv * D))
     out = torch.empty((T, Hq, D), device=dev, dtype=torch.float16)
     pb = tl.PrefillBatch(mgr, nseq, Hq)
     scale = 1.0 / float(np.sqrt(D))
@@ -623,7 +636,7 @@ def prefill_bench(args, tl, torch, np):
         "value": round(flops / (ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
-        "data": "synthetic: Q/K/V ~ N(0,1) (torch.randn, seeded)",
+        "data": f"synthetic: Q/K/V ~ N(0,1) ({GEN_NOTE})",
         "config": {"workload": f"llama3_8b_prefill_{nseq}x{n}" + (f"_prefix{p0}" if p0 else ""),
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "prompts": nseq,
                    "new_tokens": n, "cached_prefix": p0, "attended_keys": keys},
@@ -634,6 +647,126 @@ def prefill_bench(args, tl, torch, np):
                      "frac": round(tflops / peak, 4), "traffic": None},
         "cpu_baseline": None,
     }
+
+
+def legacy_bench(args, tl, torch, np):
+    """attention_decode (kernels/attention.cuh:15-18), the call an unchanged
+    TransformerLayer::attention makes (src/transformer.cpp:236-237), at the
+    shape the reference's own performance table quotes: B=1, H=32, D=128,
+    S in {128, 512, 2048, 8192} (docs/en/performance/benchmarks.md:60-69),
+    compact [B][H][S][D] K/V.  Two timings per S, K calls each, back to back:
+    `cold` rotates over copies of Q/K/V whose total exceeds 1 GiB, so every
+    call streams its K/V from HBM (the headline form); `hot` repeats one
+    copy, whose K/V (at most 134 MB) then stays in the 256 MB MALL.  `value`
+    is the cold µs per call at S = 8192."""
+    import workloads
+    B, H, D = 1, 32, 128
+    seq_lens = (128, 512, 2048, 8192)
+    published_us = {128: 24.0, 512: 52.0, 2048: 180.0, 8192: 680.0}  # RTX A6000, reference docs
+    K = args.steps or 200
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream().cuda_stream
+    ns = tl.NormalStreams(stream)
+    s_q, s_k, s_v = (workloads.seed(6, i) for i in range(3))  # legacy: stream set 6
+    scale = 1.0 / float(np.sqrt(D))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    rows, cpu_rows = [], []
+    for S in seq_lens:
+        kv_bytes = 2 * B * H * S * D * 2
+        nbytes = kv_bytes + 2 * B * H * D * 2  # K + V read, Q read, O write
+        R = max(2, min(256, -(-(1 << 30) // kv_bytes)))
+        kc = ns.draw(s_k, (R, B, H, S, D))
+        vc = ns.draw(s_v, (R, B, H, S, D))
+        qc = ns.draw(s_q, (R, B, H, D))
+        out = torch.empty((B, H, D), device=dev, dtype=torch.float16)
+
+        def call(i):
+            tl.attention_decode(qc[i].data_ptr(), kc[i].data_ptr(), vc[i].data_ptr(), out.data_ptr(),
+                                scale, B, H, S, D, stream)
+
+        def timed(rotate):
+            for i in range(args.warmup):
+                call(i % R if rotate else 0)
+            torch.cuda.synchronize()
+            torch.cuda._sleep(50_000_000)  # the host queues every call meanwhile
+            ev0.record()
+            for i in range(K):
+                call(i % R if rotate else 0)
+            ev1.record()
+            torch.cuda.synchronize()
+            return ev0.elapsed_time(ev1) / K * 1e3
+        cold_us, hot_us = timed(True), timed(False)
+        tl.profile_reset()
+        tl.profile_enable(True)
+        for i in range(min(K, 50)):
+            call(i % R)
+        torch.cuda.synchronize()
+        tl.profile_enable(False)
+        c_ms, c_n = tl.profile_query("attn_chunk")
+        m_ms, m_n = tl.profile_query("attn_merge")
+        tl.profile_reset()
+        k_us = c_ms / max(1, c_n) * 1e3
+        rows.append({"seq_len": S, "cold_us": round(cold_us, 2), "hot_us": round(hot_us, 2),
+                     "cold_gbps": round(nbytes / (cold_us * 1e-6) / 1e9, 1),
+                     "cold_frac": round(nbytes / (cold_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "kernel_us": round(k_us, 2),
+                     "merge_us": round(m_ms / max(1, m_n) * 1e3, 2), "merge_launches": m_n,
+                     "bytes": nbytes, "reference_published_us": published_us[S]})
+        if args.cpu_baseline:
+            cpu_rows.append(cpu_baseline_legacy(qc[0], kc[0], vc[0], B, H, S, D, scale, torch))
+        del kc, vc, qc
+    last = rows[-1]
+    k_gbps = last["bytes"] / (last["kernel_us"] * 1e-6) / 1e9
+    cpu = None
+    if cpu_rows:
+        c = cpu_rows[-1]
+        cpu = {"value": c["gbps"], "unit": "GB/s", "cores": c["threads"], "kind": "port",
+               "us_per_call": c["us"], "per_seq_len": cpu_rows,
+               "sample": f"oracle C restatement of attention_decode ({CPU_FORM}, built with gcc "
+                         f"-O3 -march=native on this host) on copy 0 of each S, "
+                         f"cpu={_cpu_model()}"}
+    return {
+        "metric": "attention_decode µs/call (reference entry point, compact K/V), B=1 H=32 "
+                  "D=128 S=8192",
+        "value": last["cold_us"], "unit": "us", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": round(last["cold_us"] / 1e3, 5), "us_per_step": last["cold_us"],
+        "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": round(last["cold_us"] / published_us[8192], 4),
+        "vs_baseline_note": "µs ratio to the reference's own published figure (680 µs on an RTX "
+                            "A6000, docs/en/performance/benchmarks.md:69): below 1 is faster",
+        "dtype": "fp16", "data": f"synthetic: Q/K/V ~ N(0,1) ({GEN_NOTE})",
+        "config": {"workload": "legacy_attention_decode_b1_h32_d128", "batch": B, "heads": H,
+                   "head_dim": D, "seq_lens": list(seq_lens), "timing": "cold (rotating copies)"},
+        "per_seq_len": rows,
+        "roofline": {"kernel": "attn_decode_kernel<D=128,G=1> (+ attn_merge_kernel)", "bound": "hbm",
+                     "achieved": round(k_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_baseline_legacy(q, k, v, B, H, S, D, scale, torch):
+    """The oracle's restatement of attention_decode (compact view, its
+    vectorised timing form, the native build) on the same Q/K/V, one OpenMP
+    thread per (b, h) row up to the box's 16, timed over at least 0.2 s."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as orc
+    orc.use_native_build()
+    qh, kh, vh = host_bits(q), host_bits(k), host_bits(v)
+    view = orc.compact_view(kh, vh, B, H, S, D)
+    _, threads = cpu_counts()
+    lens = np.full(B, S, dtype=np.int32)
+    n, t = 0, 0.0
+    while n == 0 or t < 0.2:
+        t0 = time.perf_counter()
+        orc.attn_decode_gqa(qh, view, lens, H, H, D, scale, nthreads=threads, fast=True)
+        t += time.perf_counter() - t0
+        n += 1
+    us = t / n * 1e6
+    nbytes = 2 * B * H * S * D * 2 + 2 * B * H * D * 2
+    return {"seq_len": S, "us": round(us, 1), "gbps": round(nbytes / (us * 1e-6) / 1e9, 3),
+            "threads": threads}
 
 
 def gemm_bench(args, tl, torch, np):
@@ -650,6 +783,7 @@ def gemm_bench(args, tl, torch, np):
     each call (project: with its prepare and commit) from the host and waits
     several microseconds of host work between kernels, so each starts cold.
     `value`, `kernels_us` and the roofline are the back-to-back ones."""
+    import workloads
     B, hidden, Hq, Hkv, D, gs, sets = 64, 4096, 32, 8, 128, 128, 16
     K = args.steps or 100
     dev = torch.device("cuda", 0)
@@ -669,7 +803,8 @@ def gemm_bench(args, tl, torch, np):
             tl.w8a16_pack(w.data_ptr(), hidden, n, wp.data_ptr(), stream)
         sc = (torch.rand(((hidden + gs - 1) // gs, n), generator=gen, device=dev) * 0.02 + 1e-3).half()
         return wp, sc
-    x = torch.randn((B, hidden), generator=gen, device=dev, dtype=torch.float16)
+    ns = tl.NormalStreams(stream)
+    x = ns.draw(workloads.seed(8, 0), (B, hidden))
     if args.path == "project":
         nq, nkv = Hq * D, Hkv * D
         W = [(weights(nq), weights(nkv), weights(nkv)) for _ in range(sets)]
@@ -695,7 +830,7 @@ def gemm_bench(args, tl, torch, np):
         desc = "fused QKV projection: q -> buffer, K/V rows -> cache at the write position"
     else:
         W = [weights(hidden) for _ in range(sets)]
-        h = torch.randn((B, hidden), generator=gen, device=dev, dtype=torch.float16)
+        h = ns.draw(workloads.seed(8, 1), (B, hidden))
         n_out = hidden
 
         def kernel(i):
@@ -761,8 +896,8 @@ def gemm_bench(args, tl, torch, np):
         "value": round(nbytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "us_per_step": round(ms * 1e3, 2),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16 x int8",
-        "data": f"synthetic: x ~ N(0,1), int8 weights uniform ({args.weights} layout), scales "
-                "U(0.001, 0.021) (torch, seeded)",
+        "data": f"synthetic: x ~ N(0,1) ({GEN_NOTE}); int8 weights uniform ({args.weights} "
+                "layout) and scales U(0.001, 0.021) (torch, seeded)",
         "config": {"workload": f"llama3_8b_{args.path}_b64", "batch": B, "hidden": hidden,
                    "out_columns": n_out, "group_size": gs, "weight_sets": sets,
                    "weights": args.weights, "what": desc, "timing": "back_to_back"},
@@ -801,6 +936,9 @@ def main():
     torch.cuda.set_device(0)
     if args.path == "prefill":
         print(json.dumps(prefill_bench(args, tl, torch, np)), flush=True)
+        return
+    if args.path == "legacy":
+        print(json.dumps(legacy_bench(args, tl, torch, np)), flush=True)
         return
     if args.path != "decode":
         print(json.dumps(gemm_bench(args, tl, torch, np)), flush=True)
@@ -860,6 +998,7 @@ def main():
                                         "profile, not this run" if traffic_src else None)},
         "cpu_baseline": r.get("cpu"),
         "library": tl.loaded_path(),
+        "library_version": tl.version(),
         "device": {"name": torch.cuda.get_device_properties(0).name,
                    "cus": torch.cuda.get_device_properties(0).multi_processor_count,
                    "host": os.uname().nodename},

@@ -406,6 +406,16 @@ int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int head_dim,
                  int forced_chunk, int waves_setting, int head_fuse, int with_rows,
                  tl_attn_plan_info *info, int32_t *part_base, int32_t *work);
 
+/* Seeded normal fp16 values for synthetic inputs: out[j] (device, j < n) =
+ * element first + j of the stream splitmix64(seed) -> Box-Muller (double)
+ * -> x stddev -> fp32 -> fp16 round-to-nearest-even, where element pair P
+ * takes splitmix64 calls 2P + 1 and 2P + 2 (cosine, then sine).  Element for
+ * element the oracle's generator (oracle/kv_oracle.c, orc_fill_normal_f16),
+ * so any range of a stream can be drawn on its own, on any host.  No
+ * reference counterpart: the input generator of the benchmarks and tests. */
+int tl_fill_normal_f16(uint64_t seed, uint64_t first, float stddev, void *out, size_t n,
+                       void *stream);
+
 /* ------------------------------------------------------------------------
  * Kernel timing (the reference has only an unused CudaEvent wrapper,
  * include/tiny_llm/cuda_streams.h:67-99).  When enabled, every launch of the

@@ -22,6 +22,10 @@
  *                          order; round trips of test_transformer.cu:141-194,
  *                          :302-381 (KVCachePreservesData) and :383-446
  *                          (SequentialAppendEquivalence).
+ *   orc_attn_decode_gqa_fast  (the CPU baseline's timing form) bit-identical
+ *                          to orc_attn_decode_gqa on every shape, layout and
+ *                          length tested, which pins it to the checks below
+ *                          (tests/test_oracle_attention.py).
  *   orc_attn_decode_gqa    float64 matrix-form softmax(q K^T s) V computed by
  *                          numpy on small cases; closed forms S=1, q=0,
  *                          identical keys, dominant score; permutation
@@ -58,6 +62,7 @@
 #include "kv_oracle.h"
 
 #include <float.h>
+#include <immintrin.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -506,6 +511,141 @@ void orc_attn_decode_gqa(const uint16_t *q, const orc_kv_view *kv, const int32_t
         free(scores);
         free(acc);
         free(qf);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* timing restatement of the decode attention (the CPU baseline)             */
+/* ------------------------------------------------------------------------ */
+
+/* The timing form's vector code, whatever -march the file is built with
+ * (the x86-64-v3 hosts this runs on all have AVX2, FMA and F16C). */
+#define ORC_AVX2 __attribute__((target("avx2,fma,f16c")))
+
+/* Eight fp32 rows r[0..7] of 8 values -> their transpose (AVX2 shuffles). */
+ORC_AVX2 static inline void transpose8(__m256 r[8]) {
+    __m256 t0 = _mm256_unpacklo_ps(r[0], r[1]), t1 = _mm256_unpackhi_ps(r[0], r[1]);
+    __m256 t2 = _mm256_unpacklo_ps(r[2], r[3]), t3 = _mm256_unpackhi_ps(r[2], r[3]);
+    __m256 t4 = _mm256_unpacklo_ps(r[4], r[5]), t5 = _mm256_unpackhi_ps(r[4], r[5]);
+    __m256 t6 = _mm256_unpacklo_ps(r[6], r[7]), t7 = _mm256_unpackhi_ps(r[6], r[7]);
+    __m256 u0 = _mm256_shuffle_ps(t0, t2, 0x44), u1 = _mm256_shuffle_ps(t0, t2, 0xEE);
+    __m256 u2 = _mm256_shuffle_ps(t1, t3, 0x44), u3 = _mm256_shuffle_ps(t1, t3, 0xEE);
+    __m256 u4 = _mm256_shuffle_ps(t4, t6, 0x44), u5 = _mm256_shuffle_ps(t4, t6, 0xEE);
+    __m256 u6 = _mm256_shuffle_ps(t5, t7, 0x44), u7 = _mm256_shuffle_ps(t5, t7, 0xEE);
+    r[0] = _mm256_permute2f128_ps(u0, u4, 0x20);
+    r[1] = _mm256_permute2f128_ps(u1, u5, 0x20);
+    r[2] = _mm256_permute2f128_ps(u2, u6, 0x20);
+    r[3] = _mm256_permute2f128_ps(u3, u7, 0x20);
+    r[4] = _mm256_permute2f128_ps(u0, u4, 0x31);
+    r[5] = _mm256_permute2f128_ps(u1, u5, 0x31);
+    r[6] = _mm256_permute2f128_ps(u2, u6, 0x31);
+    r[7] = _mm256_permute2f128_ps(u3, u7, 0x31);
+}
+
+/* The G query heads of kv head g of entry b, with decode_row's arithmetic
+ * per (b, h) row, operation for operation, so the results are the same bits:
+ *   scores: eight tokens per AVX2 register, one lane per token; each lane
+ *           runs the row's sequential FMA chain over d (the K rows of eight
+ *           tokens are widened with F16C and transposed to [d][token]);
+ *   max, expf, the sum and the scaling: scalar, in token order;
+ *   P.V:    eight d per register, p in order, one FMA per (p, d).
+ * Each K and V row is read once for the G heads instead of once per head. */
+ORC_AVX2 static void decode_group_fast(const uint16_t *q, const orc_kv_view *kv, int b, int g, int S,
+                              int D, int G, float scale, float *qf, float *scores, float *acc,
+                              float *kt, float *out_f32, uint16_t *out_f16) {
+    for (int i = 0; i < G * D; ++i) qf[i] = g_h2f_table[q[i]];
+    for (int p0 = 0; p0 < S; p0 += 8) {
+        const int nb = S - p0 < 8 ? S - p0 : 8;
+        for (int d0 = 0; d0 < D; d0 += 8) {
+            __m256 r[8];
+            for (int j = 0; j < 8; ++j) {
+                if (j < nb) {
+                    const uint16_t *krow = kv->k_base + view_elem(kv, b, g, p0 + j) + d0;
+                    r[j] = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)krow));
+                } else {
+                    r[j] = _mm256_setzero_ps();
+                }
+            }
+            transpose8(r);
+            for (int k = 0; k < 8; ++k) _mm256_storeu_ps(kt + (size_t)(d0 + k) * 8, r[k]);
+        }
+        const __m256 vs = _mm256_set1_ps(scale);
+        for (int i = 0; i < G; ++i) {
+            const float *qi = qf + (size_t)i * D;
+            __m256       a = _mm256_setzero_ps();
+            for (int d = 0; d < D; ++d)
+                a = _mm256_fmadd_ps(_mm256_set1_ps(qi[d]), _mm256_loadu_ps(kt + (size_t)d * 8), a);
+            float tmp[8];
+            _mm256_storeu_ps(tmp, _mm256_mul_ps(a, vs));
+            memcpy(scores + (size_t)i * S + p0, tmp, sizeof(float) * (size_t)nb);
+        }
+    }
+    for (int i = 0; i < G; ++i) {
+        float *sc = scores + (size_t)i * S;
+        float  max_score = -FLT_MAX;
+        for (int p = 0; p < S; ++p) max_score = fmaxf(max_score, sc[p]);
+        float sum_exp = 0.0f;
+        for (int p = 0; p < S; ++p) {
+            float e = expf(sc[p] - max_score);
+            sc[p] = e;
+            sum_exp += e;
+        }
+        float inv_sum = 1.0f / (sum_exp + 1e-6f);
+        for (int p = 0; p < S; ++p) sc[p] *= inv_sum;
+    }
+    for (int i = 0; i < G * D; ++i) acc[i] = 0.0f;
+    for (int p = 0; p < S; ++p) {
+        const uint16_t *vrow = kv->v_base + view_elem(kv, b, g, p);
+        for (int d0 = 0; d0 < D; d0 += 8) {
+            const __m256 v = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(vrow + d0)));
+            for (int i = 0; i < G; ++i) {
+                float *ai = acc + (size_t)i * D + d0;
+                _mm256_storeu_ps(ai, _mm256_fmadd_ps(_mm256_set1_ps(scores[(size_t)i * S + p]), v,
+                                                     _mm256_loadu_ps(ai)));
+            }
+        }
+    }
+    for (int i = 0; i < G * D; ++i) {
+        if (out_f32) out_f32[i] = S > 0 ? acc[i] : 0.0f;
+        if (out_f16) out_f16[i] = orc_f2h(S > 0 ? acc[i] : 0.0f);
+    }
+}
+
+void orc_attn_decode_gqa_fast(const uint16_t *q, const orc_kv_view *kv, const int32_t *seq_lens,
+                              int B, int Hq, int Hkv, int D, float scale, float *out_f32,
+                              uint16_t *out_f16, int nthreads) {
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0) return;
+    if (D % 8 != 0) { /* the vector form needs whole registers of d */
+        orc_attn_decode_gqa(q, kv, seq_lens, B, Hq, Hkv, D, scale, out_f32, out_f16, nthreads);
+        return;
+    }
+    h2f_table_init();
+    const int G = Hq / Hkv;
+    int       smax = 0;
+    for (int b = 0; b < B; ++b) smax = seq_lens[b] > smax ? seq_lens[b] : smax;
+    const long tasks = (long)B * Hkv;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = 1;
+#pragma omp parallel num_threads(nthreads)
+#endif
+    {
+        float *scores = (float *)malloc(sizeof(float) * (size_t)G * (size_t)(smax > 0 ? smax : 1));
+        float *acc = (float *)malloc(sizeof(float) * (size_t)G * (size_t)D);
+        float *qf = (float *)malloc(sizeof(float) * (size_t)G * (size_t)D);
+        float *kt = (float *)malloc(sizeof(float) * 8u * (size_t)D);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (long t = 0; t < tasks; ++t) {
+            const int  b = (int)(t / Hkv), g = (int)(t % Hkv);
+            const long r0 = (long)b * Hq + (long)g * G; /* first (b, h) row of the group */
+            decode_group_fast(q + r0 * D, kv, b, g, seq_lens[b], D, G, scale, qf, scores, acc, kt,
+                              out_f32 ? out_f32 + r0 * D : NULL, out_f16 ? out_f16 + r0 * D : NULL);
+        }
+        free(scores);
+        free(acc);
+        free(qf);
+        free(kt);
     }
 }
 

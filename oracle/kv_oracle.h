@@ -106,6 +106,14 @@ typedef struct {
 void orc_attn_decode_gqa(const uint16_t *q, const orc_kv_view *kv, const int32_t *seq_lens,
                          int B, int Hq, int Hkv, int D, float scale, float *out_f32,
                          uint16_t *out_f16, int nthreads);
+/* The same function with the same arithmetic per (b, h) row (the same bits),
+ * vectorised (AVX2 + F16C: eight tokens per register for the scores, eight d
+ * for P.V) and reading each K/V row once per GQA group: the timing form of
+ * the CPU baseline.  head_dim not a multiple of 8 falls back to
+ * orc_attn_decode_gqa. */
+void orc_attn_decode_gqa_fast(const uint16_t *q, const orc_kv_view *kv, const int32_t *seq_lens,
+                              int B, int Hq, int Hkv, int D, float scale, float *out_f32,
+                              uint16_t *out_f16, int nthreads);
 
 /* Literal attention_decode contract: compact [B][H][S][D] K/V, MHA. */
 void orc_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out_f32,

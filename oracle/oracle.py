@@ -38,6 +38,27 @@ def lib() -> C.CDLL:
     return _lib
 
 
+def use_native_build() -> str:
+    """The CPU baseline's timing build: compile kv_oracle.c with -O3
+    -march=native on this machine (make native) and route every later call of
+    this module through it.  Returns a description of the build used; falls
+    back to the portable build when the compile fails."""
+    global _lib
+    path = os.path.join(_HERE, "_build", "libkv_oracle_native.so")
+    if os.path.exists(path):
+        os.remove(path)  # -march=native belongs to the machine it runs on
+    try:
+        subprocess.run(["make", "-s", "-C", _HERE, "native"], check=True, capture_output=True,
+                       timeout=300)
+        native = C.CDLL(path)
+    except (subprocess.SubprocessError, OSError) as e:
+        lib()
+        return f"portable build (-O3 -march=x86-64-v3; native build failed: {e})"
+    _declare(native)
+    _lib = native
+    return "gcc -O3 -march=native -fopenmp, built on this host"
+
+
 class _Config(C.Structure):
     _fields_ = [("num_layers", C.c_int), ("num_heads", C.c_int), ("head_dim", C.c_int),
                 ("max_seq_len", C.c_int), ("max_batch_size", C.c_int)]
@@ -72,6 +93,7 @@ def _declare(L: C.CDLL) -> None:
     L.orc_kv_active.restype, L.orc_kv_active.argtypes = i, [vp]
     L.orc_kv_pool.restype, L.orc_kv_pool.argtypes = vp, [vp]
     L.orc_attn_decode_gqa.argtypes = [vp, C.POINTER(_View), vp, i, i, i, i, C.c_float, vp, vp, i]
+    L.orc_attn_decode_gqa_fast.argtypes = L.orc_attn_decode_gqa.argtypes
     L.orc_attention_decode.argtypes = [vp, vp, vp, vp, vp, C.c_float, i, i, i, i]
     L.orc_kv_gather.argtypes = [C.POINTER(_View), i, vp, i, i, i, i, vp]
     L.orc_attention_prefill.argtypes = [vp, vp, vp, vp, vp, C.c_float, i, i, i, i, i]
@@ -255,16 +277,17 @@ def compact_view(k, v, B, H, S, D):
     return View(pool, 0, k.size, None, 30, H * S * D, D, S * D)
 
 
-def attn_decode_gqa(q, view: View, seq_lens, Hq, Hkv, D, scale, nthreads=1):
-    """Returns (out_f32, out_f16_bits), each [B][Hq][D]."""
+def attn_decode_gqa(q, view: View, seq_lens, Hq, Hkv, D, scale, nthreads=1, fast=False):
+    """Returns (out_f32, out_f16_bits), each [B][Hq][D].  fast: the
+    vectorised timing form (orc_attn_decode_gqa_fast, the same bits)."""
     q = np.ascontiguousarray(q, dtype=np.uint16)
     lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
     B = lens.shape[0]
     o32 = np.zeros((B, Hq, D), dtype=np.float32)
     o16 = np.zeros((B, Hq, D), dtype=np.uint16)
     cv = view.c_view()
-    lib().orc_attn_decode_gqa(_ptr(q), C.byref(cv), _ptr(lens), B, Hq, Hkv, D, scale, _ptr(o32),
-                              _ptr(o16), nthreads)
+    fn = lib().orc_attn_decode_gqa_fast if fast else lib().orc_attn_decode_gqa
+    fn(_ptr(q), C.byref(cv), _ptr(lens), B, Hq, Hkv, D, scale, _ptr(o32), _ptr(o16), nthreads)
     return o32, o16
 
 

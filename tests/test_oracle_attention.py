@@ -234,3 +234,33 @@ def test_gather_matches_dense(orc):
     for b, S in enumerate(ctx):
         assert np.array_equal(gk[b, :, :S], bits(Ks[b])) and not gk[b, :, S:].any()
         assert np.array_equal(gv[b, :, :S], bits(Vs[b])) and not gv[b, :, S:].any()
+
+
+@pytest.mark.parametrize("G,D,lens,paged", [
+    (1, 32, [8, 1, 0, 13], False), (4, 128, [257, 64, 9, 1000], False),
+    (8, 128, [1, 7, 300, 4100], True), (2, 64, [95, 0, 33], True), (1, 256, [40, 41], False),
+    (4, 40, [21, 9], False)])
+def test_fast_timing_form_is_bit_identical(orc, G, D, lens, paged):
+    """orc_attn_decode_gqa_fast (the CPU baseline's vectorised form) gives the
+    checker's bits on slot and paged views, ragged and empty lengths,
+    lengths that are not multiples of its 8-token blocks, and a head_dim it
+    does not vectorise (40: the fallback)."""
+    rng = np.random.default_rng(G * 1000 + D + len(lens))
+    Hkv, B = 2, len(lens)
+    Hq = Hkv * G
+    M = max(16, -(-max(lens) // 16) * 16)
+    row = Hkv * D
+    pool = bits(f16(rng.standard_normal(2 * B * M * row)))
+    if paged:
+        nblk = M // 16
+        table = rng.permutation(B * nblk).astype(np.int32).reshape(B, nblk)
+        view = orc.View(pool, 0, B * M * row, table, 4, 16 * row, row, D)
+    else:
+        view = orc.View(pool, 0, B * M * row, np.arange(B, dtype=np.int32).reshape(B, 1), 30,
+                        M * row, row, D)
+    q = bits(f16(rng.standard_normal((B, Hq, D)) * 2))
+    a32, a16 = orc.attn_decode_gqa(q, view, np.array(lens), Hq, Hkv, D, D ** -0.5, nthreads=3)
+    b32, b16 = orc.attn_decode_gqa(q, view, np.array(lens), Hq, Hkv, D, D ** -0.5, nthreads=3,
+                                   fast=True)
+    assert np.array_equal(a32.view(np.uint32), b32.view(np.uint32))
+    assert np.array_equal(a16, b16)

@@ -84,7 +84,13 @@ extern "C" {
 
 const char *tl_last_error(void) { return g_last_error.c_str(); }
 
-const char *tl_version(void) { return "tinyllm_kv 0.1.0 gfx950"; }
+const char *tl_version(void) {
+#ifdef TL_ATTN_PV_DOT2
+    return "tinyllm_kv 0.1.0 gfx950 (comparison build: decode P.V on v_dot2)";
+#else
+    return "tinyllm_kv 0.1.0 gfx950";
+#endif
+}
 
 int tl_kv_create(const tl_kv_config *cfg, tl_kv_manager **out) {
     if (!out) return fail(TL_ERR_INVALID, "tl_kv_create: out is null");
@@ -571,6 +577,18 @@ int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int head_dim,
         }
         if (part_base) std::memcpy(part_base, wl.part_base.data(), wl.part_base.size() * 4);
         if (work && wl.n_work) std::memcpy(work, wl.work.data(), wl.work.size() * 4);
+        g_last_error.clear();
+        return TL_OK;
+    });
+}
+
+int tl_fill_normal_f16(uint64_t seed, uint64_t first, float stddev, void *out, size_t n,
+                       void *stream) {
+    if (n == 0) return TL_OK;
+    if (!out) return fail(TL_ERR_INVALID, "tl_fill_normal_f16: out is null");
+    return guarded([&] {
+        tiny_llm::detail::launch_fill_normal(seed, first, stddev, static_cast<__half *>(out), n,
+                                             static_cast<hipStream_t>(stream));
         g_last_error.clear();
         return TL_OK;
     });

@@ -364,8 +364,15 @@ __device__ __forceinline__ void wave_sync_lds() {
 // accumulators shrink to 32 VGPRs.  Measured: Llama-3-8B decode (group 4)
 // 322 -> 311 us per step, group 8 and group 2 batches 3-8% faster; group 1,
 // one live column in 16, was 1.5% slower and keeps v_dot2.
+// Building with -DTL_ATTN_PV_DOT2 (make EXTRA=-DTL_ATTN_PV_DOT2) keeps P.V on
+// v_dot2 token pairs everywhere: the comparison build behind that choice.
+#ifdef TL_ATTN_PV_DOT2
+template <int D, int G, bool MFMA>
+constexpr bool kMfmaPV = false;
+#else
 template <int D, int G, bool MFMA>
 constexpr bool kMfmaPV = !MFMA && D == 128 && G >= 2;
+#endif
 // The V stage of the MFMA P.V is a ring of two 16-token quarters per wave
 // (8 KB at head_dim 128, 69 KB an 8-wave workgroup at group 4): a quarter's
 // MFMAs run as soon as its rows are staged, while the next V batch loads.

@@ -152,6 +152,11 @@ int  head_fuse();
 // 0 = per-head plans only, 1 = auto, 2 / 4 / 8 = forced heads per workgroup.
 int planner_head_fuse(int head_dim);
 
+// out[j] = element first + j of the seeded normal fp16 stream (splitmix64 ->
+// Box-Muller -> fp16 RNE, times stddev before rounding), j < n.
+void launch_fill_normal(uint64_t seed, uint64_t first, float stddev, __half *out, uint64_t n,
+                        hipStream_t stream);
+
 // Compute units of the current device (cached per device).
 int device_cus();
 

@@ -61,6 +61,11 @@ def load() -> C.CDLL:
     return _lib
 
 
+def version() -> str:
+    """tl_version(): names the build (and a comparison build's switch)."""
+    return load().tl_version().decode()
+
+
 def loaded_path() -> str | None:
     """Path of the libtinyllm_kv.so this process has mapped (from
     /proc/self/maps), or None when none is mapped."""
@@ -156,6 +161,7 @@ def _declare(L: C.CDLL) -> None:
         "tl_attn_get_waves": (i, []),
         "tl_attn_set_head_fuse": (i, [i]),
         "tl_attn_get_head_fuse": (i, []),
+        "tl_fill_normal_f16": (i, [C.c_uint64, C.c_uint64, C.c_float, vp, sz, vp]),
         "tl_attn_plan": (i, [vp, i, i, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
         "tl_profile_enable": (None, [i]),
         "tl_profile_reset": (None, []),
@@ -520,6 +526,34 @@ def attn_plan(seq_lens, num_kv_heads, num_cus=256, forced_chunk=0, waves=0, with
     out["part_base"] = part
     out["work"] = work[:2 * info.work_items].reshape(-1, 2)
     return out
+
+
+def fill_normal(seed, first, stddev, out, n, stream=0):
+    """out[j] = element first + j of the seeded normal fp16 stream
+    (tl_fill_normal_f16; the oracle's orc_fill_normal_f16 element for
+    element)."""
+    _check(load().tl_fill_normal_f16(seed, first, stddev, out, n, stream))
+
+
+class NormalStreams:
+    """Seeded fp16 normal streams drawn on the device in call order: each seed
+    is one stream, and every draw continues it where the last draw of that
+    seed ended (tl_fill_normal_f16), so a sequence of draws defines the same
+    values on any host and torch build.  Draws return torch tensors."""
+
+    def __init__(self, stream=0):
+        self.stream = stream
+        self.offset = {}
+
+    def draw(self, seed, shape, stddev=1.0):
+        import math
+        import torch
+        t = torch.empty(shape, dtype=torch.float16, device="cuda")
+        n = math.prod(shape) if isinstance(shape, (tuple, list)) else int(shape)
+        first = self.offset.get(seed, 0)
+        fill_normal(seed, first, stddev, t.data_ptr(), n, self.stream)
+        self.offset[seed] = first + n
+        return t
 
 
 def profile_enable(on: bool = True):
