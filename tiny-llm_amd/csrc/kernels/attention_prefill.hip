@@ -218,6 +218,19 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
         row = b;
     }
     const int c = lane & 15, qg = lane >> 4;
+    // Transposing V^T reads: lane (c, qg) names, for dim tile dt and a
+    // 16-key row group at key offset r0 (a multiple of 16), the 4 dims
+    // 16dt + 4(c%4) .. +3 of key row r0 + 4qg + c/4.  The swizzle depends on
+    // a row's low four bits only, and the piece 2dt + (c%4)/2 has bit 0 from
+    // c alone, so the address is a lane constant, (2dt ^ vxor) pieces and an
+    // immediate r0 * KP * 8: eight lane offsets instead of one register per
+    // (key group, dim tile).
+    const int vrow = 4 * qg + (c >> 2);
+    const int vxor = ((c & 3) >> 1) ^ swz(vrow);
+    const int vlane = vrow * KP * 8 + 4 * (c & 1);
+    auto vt_read = [&](const uint16_t *vd, int r0, int dt) __attribute__((always_inline)) {
+        return __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(&vd[vlane + ((2 * dt) ^ vxor) * 8 + r0 * KP * 8]));
+    };
     const int kend = p0 + min(n, (qt + 1) * BQ);
     const int ntile = (kend + kKeyTile - 1) / kKeyTile;
     int       pos[NQG];  // keys 0 .. pos are attended by the lane's query column
@@ -291,12 +304,18 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
     for (int j = 0; j < NQG; ++j)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[j][dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run[NQG], l_run[NQG];
+    // Running row sums on the MFMA: l^T += 1^T P^T (A = a 16 x 32 block of
+    // ones, B = the P^T fragment), so every lane of a query column holds the
+    // column's whole sum of the fp16 weights the P.V uses, with no VALU add
+    // chain and no cross-lane sum at the end.
+    float m_run[NQG];
+    f32x4 l_run[NQG];
 #pragma unroll
     for (int j = 0; j < NQG; ++j) {
         m_run[j] = -INFINITY;
-        l_run[j] = 0.0f;
+        l_run[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    const f16x8 ones = __builtin_bit_cast(f16x8, make_uint4(0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u));
 
     // One tile: issue the next tile's DMA into the other buffers, compute on
     // kd/vd, wait for the DMA, barrier.
@@ -382,15 +401,12 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
                 m_run[j] = m_new;
             }
             const float m_new = m_run[j];
-            float psum = 0.0f;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
                 float p[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 4; ++i)
                     p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][tt][i], a.scale_log2, -m_new));
-                    psum += p[i];
-                }
                 const uint32_t lo = __builtin_bit_cast(uint32_t, __floats2half2_rn(p[0], p[1]));
                 const uint32_t hi = __builtin_bit_cast(uint32_t, __floats2half2_rn(p[2], p[3]));
                 uint4 w = __builtin_bit_cast(uint4, pf[j][tt >> 1]);
@@ -403,26 +419,30 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
                 }
                 pf[j][tt >> 1] = __builtin_bit_cast(f16x8, w);
             }
-            l_run[j] += psum;
         }
         // ---- O^T += V^T P^T on v_mfma_f32_16x16x32_f16 over 32 keys per
         // step.  Lane group qg's k index 8qg+j stands for key 32tp + 4qg + j
         // (j < 4) or 32tp + 16 + 4qg + j - 4 (j >= 4): the keys its S^T
         // fragments of tiles 2tp and 2tp+1 hold, so P^T needs no data
         // movement; the V^T fragment is read with the same key order.
+        // Key step outermost: the first step's MFMAs need only the first
+        // half's weights, so they can issue while the second half's are
+        // still in the exponentials (each accumulator still sees step 0,
+        // then step 1).
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int tp = 0; tp < 2; ++tp) {
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp) {
+            for (int j = 0; j < NQG; ++j)
+                l_run[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[j][tp], l_run[j], 0, 0, 0);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
                 // Transposing LDS reads: lane s of each 16-lane group names
                 // the 4 dims 16dt + 4(s%4) .. +3 of key row 32tp + 4qg + s/4
                 // (+16 for the second read); lane i then holds dim 16dt + i
                 // of keys 32tp + 4qg + j (j = 0..3), the A fragment in the key
                 // order above.
-                const int       vr0 = 32 * tp + 4 * qg + (c >> 2), vx = 2 * dt + ((c & 3) >> 1);
-                const int       vh = 4 * (c & 1); // half offset within the 16-byte piece
-                const s16x4     v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(&vd[slot(vr0, vx) * 8 + vh]));
-                const s16x4     v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr(&vd[slot(vr0 + 16, vx) * 8 + vh]));
+                const s16x4     v0 = vt_read(vd, 32 * tp, dt);
+                const s16x4     v1 = vt_read(vd, 32 * tp + 16, dt);
                 const f16x8     vf = __builtin_bit_cast(
                     f16x8, make_uint4(__builtin_bit_cast(uint2, v0).x, __builtin_bit_cast(uint2, v0).y,
                                       __builtin_bit_cast(uint2, v1).x, __builtin_bit_cast(uint2, v1).y));
@@ -430,6 +450,7 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
                 for (int j = 0; j < NQG; ++j)
                     acc[j][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[j][tp], acc[j][dt], 0, 0, 0);
             }
+        }
         __builtin_amdgcn_s_waitcnt(kVmcnt0); // this wave's part of the next tile has landed
         __syncthreads();                      // ... every wave's, and this tile's buffer is free
     };
@@ -465,9 +486,7 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
     }
 #pragma unroll
     for (int j = 0; j < NQG; ++j) {
-        float l = l_run[j] + __shfl_xor(l_run[j], 16);
-        l += __shfl_xor(l, 32);
-        const float inv = 1.0f / (l + 1e-6f);
+        const float inv = 1.0f / (l_run[j][0] + 1e-6f);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             const __half2 lo = __floats2half2_rn(acc[j][dt][0] * inv, acc[j][dt][1] * inv);
