@@ -8,8 +8,11 @@
  *   orc_h2f / orc_f2h      exhaustive over all 65536 binary16 patterns and
  *                          every midpoint between neighbours, against numpy's
  *                          float16 conversion (tests/test_oracle_fp16.py).
- *   orc_fill_normal_f16    moments / determinism only (input generator; its
- *                          exact values are not a parity claim).
+ *   orc_fill_normal_f16    input generator (its values are no parity claim
+ *                          about the reference): splitmix64's published
+ *                          known answers for seed 1234567, a pure-Python
+ *                          Box-Muller restatement equal bit for bit, moments
+ *                          and determinism (tests/test_oracle_fp16.py).
  *   orc_kv_* bookkeeping   the reference's own live tests
  *                          (tests/test_kv_cache.cpp:43-287) and its disabled
  *                          invariants (:298-443), ported one for one

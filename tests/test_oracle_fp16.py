@@ -1,5 +1,8 @@
 """Pins the oracle's binary16 conversions against numpy's independent
-float16 implementation (round-to-nearest-even), exhaustively."""
+float16 implementation (round-to-nearest-even), exhaustively, and the input
+generator against splitmix64's published values and a Box-Muller restatement."""
+import math
+
 import numpy as np
 
 
@@ -43,6 +46,44 @@ def test_f2h_nan_stays_nan(orc):
     x = np.array([np.nan, -np.nan], dtype=np.float32)
     h = orc.f2h(x)
     assert np.all(np.isnan(h.view(np.float16)))
+
+
+_M64 = (1 << 64) - 1
+
+
+def _splitmix64(state):
+    """splitmix64 as published with java.util.SplittableRandom and Vigna's
+    splitmix64.c: (new state, output)."""
+    state = (state + 0x9E3779B97F4A7C15) & _M64
+    z = state
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return state, z ^ (z >> 31)
+
+
+def test_normal_generator_values_follow_splitmix64_and_box_muller(orc):
+    """The generator that bench.py's device inputs reproduce bit for bit:
+    element 2i / 2i+1 is r cos(2 pi u2) / r sin(2 pi u2) with r = sqrt(-2 ln u1),
+    u1 = 1 - (x1 >> 11) 2^-53, u2 = (x2 >> 11) 2^-53 from the next two splitmix64
+    outputs, each scaled by stddev, rounded to fp32 and then to fp16 (RNE)."""
+    # splitmix64's published known answers for seed 1234567
+    s, got = 1234567, []
+    for _ in range(5):
+        s, x = _splitmix64(s)
+        got.append(x)
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                   4593380528125082431, 16408922859458223821]
+    seed, n, std = 0xDEADBEEF12345678, 513, 0.75
+    s, vals = seed, []
+    while len(vals) < n:
+        s, x1 = _splitmix64(s)
+        s, x2 = _splitmix64(s)
+        u1 = 1.0 - (x1 >> 11) * 2.0**-53
+        u2 = (x2 >> 11) * 2.0**-53
+        r = math.sqrt(-2.0 * math.log(u1))
+        vals += [r * math.cos(2 * math.pi * u2) * std, r * math.sin(2 * math.pi * u2) * std]
+    want = np.array(vals[:n], dtype=np.float64).astype(np.float32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(orc.normal_f16(seed, (n,), std), want)
 
 
 def test_normal_generator_moments_and_determinism(orc):
