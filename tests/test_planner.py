@@ -307,6 +307,19 @@ def test_whole_sequence_chunk_gives_many_tiles_per_wave(tl):
     assert min(-(-int(s) // 64) // 8 for s in lens) >= 4
 
 
+@pytest.mark.parametrize("S,chunk", [(8192, 1024), (2048, 256), (4096, 512), (512, 512)])
+def test_uniform_split_is_one_round_of_workgroups(tl, S, chunk):
+    """The reference's published attention_decode shape (B = 1, 32 heads,
+    compact K/V): uniform lengths that must split take chunks of W / C, so
+    the items x heads fill each CU once with an 8-wave workgroup (one round);
+    512 tokens stay whole (at most two tiles per wave)."""
+    p = tl.attn_plan(np.full(1, S, np.int32), 32, num_cus=CUS, head_fuse="off")
+    assert p["chunk_tokens"] == chunk and p["waves"] == 8
+    assert p["work_items"] * 32 == (CUS if S > 1024 else 32)
+    assert p["any_multi"] == int(S > 1024)
+    check_invariants(p, np.full(1, S), 32, CUS)
+
+
 def test_waves_setting_and_empty_sequences(tl):
     lens = np.array([0, 5, 0], dtype=np.int32)
     p = tl.attn_plan(lens, 8, num_cus=CUS, head_fuse="off")
