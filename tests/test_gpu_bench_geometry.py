@@ -24,7 +24,7 @@ import torch
 
 import workloads
 from devutil import empty_dev, read_dev, stream, to_dev, to_host
-from test_gpu_configs import cus, host_bits, randn, report, row_errors
+from test_gpu_configs import cus, elem_err, host_bits, randn, report, row_errors
 
 pytestmark = pytest.mark.gpu
 
@@ -103,9 +103,11 @@ def test_cfg2_32_layers_slot_pool_over_4gib(tl, orc):
         view = orc.cache_view(lp.reshape(-1), 1, Hkv, D, M, 0, list(range(B)))
         ref32, _ = orc.attn_decode_gqa(host_bits(q[layer]), view, ctx + 1, Hq, Hkv, D, cfg.scale,
                                        nthreads=16)
-        errs = row_errors(host_bits(outs[layer]), ref32)
+        bits = host_bits(outs[layer])
+        errs = row_errors(bits, ref32)
         report(f"cfg2_32L_layer{layer}", errs, {"chunk": info["chunk_tokens"],
-                                                "pool_gib": round(g.slot_bytes() * B / (1 << 30), 1)})
+                                                "pool_gib": round(g.slot_bytes() * B / (1 << 30), 1),
+                                                "worst_elem_err": elem_err(bits, ref32)})
         assert errs.max() <= 1e-3, (layer, float(errs.max()))
     del g, batch, q, nk, nv, outs
     torch.cuda.empty_cache()
@@ -139,7 +141,7 @@ def test_cfg5_churn_bench_events_on_the_slot_pool(tl, orc):
     scale = 1.0 / np.sqrt(D)
     bufs = dict(q=q.data_ptr(), nk=nk.data_ptr(), nv=nv.data_ptr(), out=out.data_ptr(),
                 scale=scale, src_k=src_k.data_ptr(), src_v=src_v.data_ptr())
-    freed, reused, top_slot, checks, worst = set(), 0, 0, 0, 0.0
+    freed, reused, top_slot, checks, worst, worst_elem = set(), 0, 0, 0, 0.0, 0.0
     for ev in sim.events():
         nk.copy_(randn(gen, nk.shape))
         nv.copy_(randn(gen, nv.shape))
@@ -169,8 +171,10 @@ def test_cfg5_churn_bench_events_on_the_slot_pool(tl, orc):
             view = orc.cache_view(o.pool(), 1, Hkv, D, M, 0, [o.slot_of(int(s)) for s in ids])
             ref32, _ = orc.attn_decode_gqa(host_bits(q[:n]), view, lens + 1, Hq, Hkv, D, scale,
                                            nthreads=16)
-            errs = row_errors(host_bits(out[:n]), ref32)
+            bits = host_bits(out[:n])
+            errs = row_errors(bits, ref32)
             worst = max(worst, float(errs.max()))
+            worst_elem = max(worst_elem, elem_err(bits, ref32))
             checks += 1
             assert errs.max() <= 1e-3, (ev.step, float(errs.max()))
         for sid in ids:
@@ -182,7 +186,8 @@ def test_cfg5_churn_bench_events_on_the_slot_pool(tl, orc):
     info = batch.info()
     report("cfg5_churn_slot_pool_120_steps", np.array([worst]),
            {"checks": checks, "live": int(len(live)), "reused_slots": reused,
-            "chunk": info["chunk_tokens"], "work_items": info["work_items"]})
+            "chunk": info["chunk_tokens"], "work_items": info["work_items"],
+            "worst_elem_err": worst_elem})
     assert checks >= steps // 10 - 1 and len(live) > 100 and reused > 0
     # the plan of the last steps: one chunk per sequence in the compact
     # kernel-argument encoding (head-fused chunk items on 256 CUs)
