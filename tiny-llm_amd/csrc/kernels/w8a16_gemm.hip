@@ -535,21 +535,32 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
         }
     const bool eact = wave < 2 * CB && tile * CB + ecb < a.blocks; // (a block past the last segment: none)
     const int  ekind = TL_DEC_SEG(a, esi, kind);
-    int        erow[4] = {0, 0, 0, 0}, epos[4] = {0, 0, 0, 0};
-    __half     eres[4];
+    // These loads go out before the weight stream, so nothing may wait for
+    // them here.  Rows and write positions are never negative: held
+    // unsigned, their widening to 64 bits is a zero high word (a
+    // sign-extending load is lowered to the load and a shift right after
+    // it, a wait per row).  The kind test is outside the row loop, so each
+    // path is a straight run of loads (a test per row let one path's zero
+    // overwrite a register another path still had a load in flight for,
+    // which needs a wait).
+    uint32_t erow[4] = {0, 0, 0, 0}, epos[4] = {0, 0, 0, 0};
+    __half   eres[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) eres[i] = __float2half(0.0f);
-    if (eact) {
+    int em[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) em[i] = min(kDecHalf * half + 16 * erb + 4 * (lane >> 4) + i, a.M - 1);
+    if (eact && ekind == kEpiCache) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int m = min(kDecHalf * half + 16 * erb + 4 * (lane >> 4) + i, a.M - 1);
-            if (ekind == kEpiCache) {
-                erow[i] = a.cache.seq_row[m];
-                epos[i] = a.cache.wpos[m];
-            } else if (ekind == kEpiResidual) {
-                eres[i] = TL_DEC_SEG(a, esi, res)[(int64_t)m * TL_DEC_SEG(a, esi, ld) + en];
-            }
+            erow[i] = (uint32_t)a.cache.seq_row[em[i]];
+            epos[i] = (uint32_t)a.cache.wpos[em[i]];
         }
+    } else if (eact && ekind == kEpiResidual) {
+        const __half *res = TL_DEC_SEG(a, esi, res);
+        const int64_t ld = TL_DEC_SEG(a, esi, ld);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) eres[i] = res[(int64_t)em[i] * ld + en];
     }
     // x is loaded in whole 128-byte lines -- 4 rows x 256 bytes (one chunk)
     // per load -- and rearranged into MFMA A fragments through the wave's LDS
@@ -757,8 +768,8 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
             const CacheRows &c = a.cache;
             int64_t          off;
             if (c.block_table) {
-                const int blk = c.block_table[(int64_t)erow[i] * c.bt_stride + (epos[i] >> c.log2_blk)];
-                off = (int64_t)blk * c.blk_stride + (int64_t)(epos[i] & ((1 << c.log2_blk) - 1)) * c.tok_stride;
+                const int blk = c.block_table[(int64_t)erow[i] * c.bt_stride + (int64_t)(epos[i] >> c.log2_blk)];
+                off = (int64_t)blk * c.blk_stride + (int64_t)(epos[i] & ((1u << c.log2_blk) - 1)) * c.tok_stride;
             } else {
                 off = (int64_t)erow[i] * c.blk_stride + (int64_t)epos[i] * c.tok_stride;
             }
