@@ -21,8 +21,13 @@ def f16bits(rng, shape, std=1.0):
 
 
 # ------------------------------------------------------ legacy attention_decode
+# B = 1, H = 32, D = 128 at S = 128 / 512 / 2048 / 8192 is the shape of the
+# reference's published attention_decode table (docs/en/performance/
+# benchmarks.md:60-69); at 4096 and 8192 the plan splits every head into
+# 512- and 1024-token chunks (one round of 8-wave workgroups) plus the merge.
 @pytest.mark.parametrize("B,H,S,D", [(1, 2, 8, 32), (1, 4, 8, 32), (2, 8, 129, 64),
                                      (1, 32, 128, 128), (1, 32, 512, 128), (1, 32, 2048, 128),
+                                     (1, 32, 4096, 128), (1, 32, 8192, 128), (2, 16, 8192, 64),
                                      (3, 4, 13000, 128), (2, 2, 700, 256), (1, 1, 1, 64)])
 def test_attention_decode_legacy_vs_oracle(tl, orc, B, H, S, D):
     rng = np.random.default_rng(B * 7 + S)
@@ -37,7 +42,8 @@ def test_attention_decode_legacy_vs_oracle(tl, orc, B, H, S, D):
     got = to_host(out).view(np.float16).astype(np.float32)
     ref32, _ = orc.attn_decode_gqa(q, orc.compact_view(k, v, B, H, S, D), np.full(B, S), H, H, D,
                                    scale, nthreads=8)
-    assert rel_err(got, ref32) <= TOL, rel_err(got, ref32)
+    worst = max(rel_err(got[b, h], ref32[b, h]) for b in range(B) for h in range(H))
+    assert worst <= TOL, worst
 
 
 def test_attention_decode_nonpositive_dims_is_noop(tl):
