@@ -66,8 +66,8 @@ def parse():
     ap.add_argument("--prefill-prefix", type=int, default=0,
                     help="prefill: tokens already cached per prompt (chunked continuation)")
     ap.add_argument("--settle-ms", type=float, default=100.0,
-                    help="prefill: after the warm-up steps, untimed back-to-back steps for at "
-                         "least this long, so the MFMA-bound kernel is timed at the clock the "
+                    help="prefill, project, oproj: untimed back-to-back calls for about this "
+                         "long before the timed ones, so the kernels are timed at the clock the "
                          "GPU settles at under sustained load (0: off)")
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
@@ -880,14 +880,34 @@ def gemm_bench(args, tl, torch, np):
     t_wall = time.perf_counter() - t_wall
     iso_ms = ev0.elapsed_time(ev1) / K
 
+    # Host cost of queueing one call, to size the GPU sleep that lets the
+    # host queue a whole burst before the first call runs.
+    begin()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(200_000_000)
+    t_q = time.perf_counter()
+    for i in range(64):
+        kernel(i)
+    enqueue_us = (time.perf_counter() - t_q) / 64 * 1e6
+    torch.cuda.synchronize()
+    end()
+    # Settle: untimed back-to-back calls for about --settle-ms ahead of the
+    # timed ones in the same queue, so the timed calls run at the clock the
+    # GPU reaches under sustained load (the sleep ahead of a burst idles it).
+    settle = int(args.settle_ms * 1e3 / max(iso_ms * 1e3, 1.0)) if args.settle_ms > 0 else 0
+    sleep_cycles = int(max(200_000_000, 2.0 * (settle + K) * enqueue_us * 2.0e3))
+
     def burst(profile):
-        """K calls queued behind a GPU sleep: the kernels run back to back."""
+        """K calls queued behind a GPU sleep (and the settle calls): the
+        kernels run back to back."""
         begin()
         torch.cuda.synchronize()
+        torch.cuda._sleep(sleep_cycles)  # the host queues every call meanwhile
+        for i in range(settle):
+            kernel(i)
         if profile:
             tl.profile_reset()
             tl.profile_enable(True)
-        torch.cuda._sleep(200_000_000)  # ~0.1 s of GPU cycles: the host queues every call meanwhile
         ev0.record()
         for i in range(K):
             kernel(i)
@@ -919,6 +939,9 @@ def gemm_bench(args, tl, torch, np):
                    "out_columns": n_out, "group_size": gs, "weight_sets": sets,
                    "weights": args.weights, "what": desc, "timing": "back_to_back"},
         "kernels_us": {"w8a16": round(g_avg * 1e3, 2), "w8a16_reduce": round(r_avg * 1e3, 2)},
+        "settle": {"ms": args.settle_ms, "calls": settle, "enqueue_us_per_call": round(enqueue_us, 2),
+                   "why": "untimed back-to-back calls queued ahead of each timed burst: the "
+                          "shader clock ramps under sustained load"},
         "isolated_us_per_call": round(iso_ms * 1e3, 2),
         "host_wall_us_per_call_isolated": round(t_wall / K * 1e6, 2),
         "roofline": {"kernel": kname, "bound": "hbm",
