@@ -707,17 +707,29 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
     auto chunk_of = [&](int j) __attribute__((always_inline)) {
         return mine > 0 ? wave + kDecWaves * min(j, mine - 1) : nchunks - 1;
     };
+    // The loads are issued in the order the multiplies consume them:
+    // vector loads complete in issue order, so a chunk's multiply can start
+    // once that chunk and the loads issued before it have landed.  The
+    // scheduling barriers keep the compiler from hoisting later chunks'
+    // weights above an earlier chunk's x, which made the first multiply wait
+    // for three chunks of weights; the last chunk's weights follow the third
+    // chunk's x, so only the last multiply waits for the end of the stream.
     if constexpr (CB <= 3) {
         WSlot ws[4];
         XSlot xs[2];
         load_w(ws[0], chunk_of(0));
         load_x(xs[0], chunk_of(0));
+        __builtin_amdgcn_sched_barrier(0);
         load_w(ws[1], chunk_of(1));
         load_x(xs[1], chunk_of(1));
+        __builtin_amdgcn_sched_barrier(0);
         load_w(ws[2], chunk_of(2));
-        load_w(ws[3], chunk_of(3));
+        __builtin_amdgcn_sched_barrier(0);
         if (mine > 0) compute(xs[0], ws[0], chunk_of(0));
         load_x(xs[0], chunk_of(2));
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(ws[3], chunk_of(3));
+        __builtin_amdgcn_sched_barrier(0);
         if (mine > 1) compute(xs[1], ws[1], chunk_of(1));
         load_x(xs[1], chunk_of(3));
         if (mine > 2) compute(xs[0], ws[2], chunk_of(2));
@@ -727,8 +739,10 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
         XSlot xs[2];
         load_w(ws[0], chunk_of(0));
         load_x(xs[0], chunk_of(0));
+        __builtin_amdgcn_sched_barrier(0);
         load_w(ws[1], chunk_of(1));
         load_x(xs[1], chunk_of(1));
+        __builtin_amdgcn_sched_barrier(0);
         if (mine > 0) compute(xs[0], ws[0], chunk_of(0));
         load_w(ws[0], chunk_of(2));
         load_x(xs[0], chunk_of(2));
