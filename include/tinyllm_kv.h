@@ -317,7 +317,8 @@ int tl_w8a16_matmul_residual(const void *input, const int8_t *weight, const void
  * bytes at ((nb*K/32 + ks)*64) * 8 hold, for lane l = 0..63, rows
  * 32ks + 8(l/16) .. +7 of column 16nb + l%16 -- the B fragment of
  * v_mfma_f32_16x16x32_f16, so the kernel streams weights straight into MFMA
- * operands.  No reference counterpart (weights are static; an engine packs
+ * operands -- as offset-binary bytes (w + 128, the bits of w ^ 0x80), which
+ * convert to fp16 without a sign fix-up.  No reference counterpart (weights are static; an engine packs
  * them once at load, like model_loader.cpp's quantised tensors). */
 int tl_w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, void *stream);
 /* W8A16 kernel selection, process-wide: 0 = normal (MFMA where the shape

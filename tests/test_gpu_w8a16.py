@@ -83,7 +83,8 @@ def test_w8a16_reference_order_kernel_is_bit_exact(tl, orc, generic, M, N, K, gs
 
 def pack_np(w):
     """The packed layout, restated in numpy: fragment (nb, ks) = 64 lanes x 8
-    bytes, lane l holding rows 32ks + 8(l/16) .. +7 of column 16nb + l%16."""
+    bytes, lane l holding rows 32ks + 8(l/16) .. +7 of column 16nb + l%16, as
+    offset-binary bytes (w + 128, i.e. the bits of w ^ 0x80)."""
     K, N = w.shape
     out = np.empty((N // 16, K // 32, 64, 8), np.int8)
     lanes = np.arange(64)
@@ -91,7 +92,7 @@ def pack_np(w):
         for ks in range(K // 32):
             rows = 32 * ks + 8 * (lanes // 16)[:, None] + np.arange(8)[None, :]
             out[nb, ks] = w[rows, 16 * nb + (lanes % 16)[:, None]]
-    return out.reshape(-1)
+    return (out.view(np.uint8) ^ 0x80).view(np.int8).reshape(-1)
 
 
 def test_w8a16_pack_layout(tl, orc):

@@ -112,16 +112,21 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, int si, int m, int n
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// Four signed bytes -> four fp16 (exact), as two dwords of an MFMA operand.
-// u = b + 128 (b ^ 0x80) placed in the mantissa of 0x6400 (1024.0) is the
-// fp16 value 1024 + u; subtracting 1152 leaves b exactly.
-__device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t v) {
-    const uint32_t u = v ^ 0x80808080u;
+// Four offset-binary bytes u = b + 128 -> four fp16 b (exact), as two dwords
+// of an MFMA operand: u placed in the mantissa of 0x6400 (1024.0) is the fp16
+// value 1024 + u; subtracting 1152 leaves b exactly.
+__device__ __forceinline__ uint2 u8x4_to_f16x4(uint32_t u) {
     const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u); // [u0 64 u1 64]
     const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x05030402u); // [u2 64 u3 64]
     const f16x2    bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     return make_uint2(__builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) + bias),
                       __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) + bias));
+}
+
+// Four bytes of W -> four fp16.  The packed layout holds offset-binary bytes
+// (b ^ 0x80, written by w8a16_pack_kernel); the reference layout holds b.
+template <bool PACKED> __device__ __forceinline__ uint2 w8x4_to_f16x4(uint32_t v) {
+    return u8x4_to_f16x4(PACKED ? v : v ^ 0x80808080u);
 }
 
 // Split-K inside the workgroup: one workgroup (4 waves) per unit (64-row
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
             }
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) {
-                const uint2 lo = i8x4_to_f16x4(wv[j][cb].x), hi = i8x4_to_f16x4(wv[j][cb].y);
+                const uint2 lo = w8x4_to_f16x4<PACKED>(wv[j][cb].x), hi = w8x4_to_f16x4<PACKED>(wv[j][cb].y);
                 const f16x8 bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb)
@@ -443,6 +448,7 @@ struct DecArgs {
     const __half *x; // [M][K]
     int64_t       ldx;
     int           M, K, gs;
+    int           log2_gs; // gs is a power of two
     int           nseg;
     int           tiles;  // column tiles of CB blocks
     int           tpx;    // tiles per XCD: ceil(tiles / 8)
@@ -483,7 +489,8 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
     static_assert(CB >= 1 && CB <= 4, "column blocks");
     constexpr int NF = 4 / FS;                                  // folds per chunk
     constexpr int RED = kDecWaves * 2 * CB * 64 * 4;            // floats: every wave's tile
-    constexpr int XST = kDecHalf * 256;                         // bytes: a wave's x stage (one chunk)
+    constexpr int XPITCH = 256 + 16;                            // bytes: an x stage row (padded)
+    constexpr int XST = kDecHalf * XPITCH;                      // bytes: a wave's x stage (one chunk)
     constexpr int WST = PACKED ? 0 : 128 * CB * 16;             // bytes: its W stage (reference layout)
     constexpr int STAGE = kDecWaves * (XST + WST) / 4;          // floats
     __shared__ __align__(16) float lds[RED > STAGE ? RED : STAGE];
@@ -500,7 +507,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
     if (tile >= a.tiles) return; // uniform for the workgroup
     const int ksteps = a.K >> 5;
     const int nchunks = (ksteps + 3) >> 2;
-    const int ngroups = (a.K + a.gs - 1) / a.gs;
+    const int ngroups = (a.K + a.gs - 1) >> a.log2_gs;
     const int mine = wave < nchunks ? (nchunks - wave + kDecWaves - 1) / kDecWaves : 0; // this wave's chunks
 
     // The tile's column blocks: segment, local block, and the buffer
@@ -594,7 +601,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
                     sl.w[s * CB + cb] = __builtin_bit_cast(
-                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[cb], 8 * lane, (nb[cb] * ksteps + 4 * c + s) * 512, 0));
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[cb], 8 * lane + 512 * s, (nb[cb] * ksteps + 4 * c) * 512, 0));
         } else {
             // stage slot q = t * 64 + lane (16 bytes): row q / CB, slot q % CB
             // of the row, which holds piece (q % CB - dec_rot(row)) mod CB
@@ -618,7 +625,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
         for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) {
-                const int g = (128 * c + 32 * FS * f) / a.gs;
+                const int g = (128 * c + 32 * FS * f) >> a.log2_gs;
                 sl.s[f][cb] = __builtin_bit_cast(
                     __half, __builtin_amdgcn_raw_buffer_load_b16(rs[cb], sv + 32u * nb[cb], 2 * g * sn[cb], 0));
             }
@@ -634,30 +641,30 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
         }
     // The wave's stages (one chunk each; LDS operations of a wave run in
     // order, so the next chunk's writes follow this chunk's reads).  x stage:
-    // 32 rows of 256 bytes, 16-byte piece p of row r in slot p ^ (r & 15), so
-    // that the stores (8 lanes = 8 pieces of a row) and the A-fragment reads
-    // (8 lanes = 8 rows, one piece) touch distinct banks.
+    // 32 rows of 256 bytes, 16 bytes of padding after each, so that the
+    // stores (8 lanes = 8 pieces of a row) and the A-fragment reads (8 lanes =
+    // 8 rows, one piece: 272 bytes apart, 16 bytes apart in the banks) touch
+    // distinct banks, and every address is a lane base plus an immediate.
     uint8_t *const xst = reinterpret_cast<uint8_t *>(lds) + (size_t)wave * (XST + WST);
     uint8_t *const wst = xst + XST;
     auto compute = [&](const XSlot &xs, const WSlot &sl, int c) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int r = 4 * i + (lane >> 4);
-            *reinterpret_cast<u32x4 *>(xst + r * 256 + 16 * ((lane & 15) ^ (r & 15))) = xs.x[i];
+            *reinterpret_cast<u32x4 *>(xst + r * XPITCH + 16 * (lane & 15)) = xs.x[i];
         }
         if constexpr (!PACKED) {
 #pragma unroll
             for (int t = 0; t < 2 * CB; ++t) *reinterpret_cast<u32x4 *>(wst + (t * 64 + lane) * 16) = sl.r[t];
         }
-        const int steps = min(4, ksteps - 4 * c);
+        // (K is a multiple of 128: every chunk has 4 k steps.)
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            if (s >= steps) break; // uniform
             f16x8 xa[2]; // A fragments: row 16 rb + lane % 16, piece 4 s + lane / 16
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 const int r = 16 * rb + (lane & 15);
-                xa[rb] = *reinterpret_cast<const f16x8 *>(xst + r * 256 + 16 * ((4 * s + (lane >> 4)) ^ (r & 15)));
+                xa[rb] = *reinterpret_cast<const f16x8 *>(xst + r * XPITCH + 16 * (4 * s + (lane >> 4)));
             }
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) {
@@ -672,22 +679,23 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
                         (__attribute__((address_space(3))) v2i32 *)(wst + (r * CB + pos) * 16 + 8 * (i & 1)));
                     raw = make_uint2((uint32_t)t[0], (uint32_t)t[1]);
                 }
-                const uint2 lo = i8x4_to_f16x4(raw.x), hi = i8x4_to_f16x4(raw.y);
+                const uint2 lo = w8x4_to_f16x4<PACKED>(raw.x), hi = w8x4_to_f16x4<PACKED>(raw.y);
                 const f16x8 bop = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+// A fold group's first step starts from a zero accumulator (an
+                // inline constant of the MFMA, no register clearing).
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
-                    P[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[rb], bop, P[rb][cb], 0, 0, 0);
+                    P[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        xa[rb], bop, s % FS == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : P[rb][cb], 0, 0, 0);
             }
-            if ((s + 1) % FS == 0 || s + 1 == steps) { // end of a fold group
+            if ((s + 1) % FS == 0) { // end of a fold group
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
+                    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
                             acc[rb][cb][i] = fmaf(P[rb][cb][i], h2f(sl.s[s / FS][cb]), acc[rb][cb][i]);
-                        P[rb][cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
             }
         }
     };
@@ -799,7 +807,9 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
 // Repacks W [K][N] int8 (K % 32 == 0, N % 16 == 0) so that the B fragment of
 // v_mfma_f32_16x16x32_f16 for column block nb and k step ks is 512
 // contiguous bytes: packed[((nb * K/32 + ks) * 64 + l) * 8 + j] =
-// W[32 ks + 8 (l / 16) + j][16 nb + l % 16].  One thread per (nb, ks, l).
+// W[32 ks + 8 (l / 16) + j][16 nb + l % 16] ^ 0x80 -- offset binary (W + 128
+// as an unsigned byte), which the kernels turn into fp16 without the XOR a
+// signed byte needs.  One thread per (nb, ks, l).
 __global__ __launch_bounds__(256) void w8a16_pack_kernel(const int8_t *w, int K, int N, int8_t *out) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t total = (int64_t)(N / 16) * (K / 32) * 64;
@@ -816,7 +826,7 @@ __global__ __launch_bounds__(256) void w8a16_pack_kernel(const int8_t *w, int K,
         lo |= (uint32_t)(uint8_t)w[(int64_t)(k0 + j) * N + col] << (8 * j);
         hi |= (uint32_t)(uint8_t)w[(int64_t)(k0 + 4 + j) * N + col] << (8 * j);
     }
-    *reinterpret_cast<uint2 *>(out + idx * 8) = make_uint2(lo, hi);
+    *reinterpret_cast<uint2 *>(out + idx * 8) = make_uint2(lo ^ 0x80808080u, hi ^ 0x80808080u);
 }
 
 // The epilogue of four consecutive columns n..n+3 of one segment (n % 4 ==
@@ -976,6 +986,7 @@ void launch_dec(const GemmArgs &g, int gs, hipStream_t stream, bool packed) {
     a.M = g.M;
     a.K = g.K;
     a.gs = gs;
+    a.log2_gs = __builtin_ctz((unsigned)gs); // a power of two (w8a16_mfma_ok)
     a.nseg = g.nseg;
     for (int i = 0; i < g.nseg; ++i) a.seg[i] = g.seg[i];
     for (int i = 0; i <= g.nseg; ++i) a.col0[i] = g.col0[i];
