@@ -313,12 +313,14 @@ int tl_w8a16_matmul_residual(const void *input, const int8_t *weight, const void
                              void *stream);
 /* One-time repack of a W8A16 weight [K][N] int8 (K % 32 == 0, N % 16 == 0)
  * into the layout the packed entry points read (K*N bytes, device to device,
- * stream-ordered): for column block nb = n/16 and k step ks = k/32, the 512
- * bytes at ((nb*K/32 + ks)*64) * 8 hold, for lane l = 0..63, rows
- * 32ks + 8(l/16) .. +7 of column 16nb + l%16 -- the B fragment of
- * v_mfma_f32_16x16x32_f16, so the kernel streams weights straight into MFMA
- * operands -- as offset-binary bytes (w + 128, the bits of w ^ 0x80), which
- * convert to fp16 without a sign fix-up.  No reference counterpart (weights are static; an engine packs
+ * stream-ordered): the B fragments of v_mfma_f32_16x16x32_f16, so the kernel
+ * streams weights straight into MFMA operands.  Lane l = 0..63 of the
+ * fragment of column block nb = n/16 and k step ks = k/32 holds rows
+ * 32ks + 8(l/16) .. +7 of column 16nb + l%16 as offset-binary bytes (w + 128,
+ * the bits of w ^ 0x80, which convert to fp16 without a sign fix-up).  Column
+ * block nb takes the K*16 bytes from nb*K*16; in them steps 2p and 2p+1 share
+ * the 1024 bytes from 1024p, lane l's 16 bytes at 16l (step 2p first), and a
+ * last unpaired step (K % 64 == 32) takes 8 bytes per lane.  No reference counterpart (weights are static; an engine packs
  * them once at load, like model_loader.cpp's quantised tensors). */
 int tl_w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, void *stream);
 /* W8A16 kernel selection, process-wide: 0 = normal (MFMA where the shape

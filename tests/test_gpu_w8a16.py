@@ -82,29 +82,41 @@ def test_w8a16_reference_order_kernel_is_bit_exact(tl, orc, generic, M, N, K, gs
 
 
 def pack_np(w):
-    """The packed layout, restated in numpy: fragment (nb, ks) = 64 lanes x 8
-    bytes, lane l holding rows 32ks + 8(l/16) .. +7 of column 16nb + l%16, as
-    offset-binary bytes (w + 128, i.e. the bits of w ^ 0x80)."""
+    """The packed layout, restated in numpy.  The B fragment of column block
+    nb and k step ks is 64 lanes x 8 bytes, lane l holding rows 32ks +
+    8(l/16) .. +7 of column 16nb + l%16 as offset-binary bytes (w + 128, the
+    bits of w ^ 0x80).  Column block nb takes K*16 bytes from nb*K*16; in it
+    steps 2p and 2p+1 share 1024 bytes, lane l's 16 bytes at 16l (step 2p
+    first); a last unpaired step takes 8 bytes per lane."""
     K, N = w.shape
-    out = np.empty((N // 16, K // 32, 64, 8), np.int8)
+    ks_n = K // 32
+    frag = np.empty((N // 16, ks_n, 64, 8), np.uint8)
     lanes = np.arange(64)
+    wu = w.view(np.uint8) ^ 0x80
     for nb in range(N // 16):
-        for ks in range(K // 32):
+        for ks in range(ks_n):
             rows = 32 * ks + 8 * (lanes // 16)[:, None] + np.arange(8)[None, :]
-            out[nb, ks] = w[rows, 16 * nb + (lanes % 16)[:, None]]
-    return (out.view(np.uint8) ^ 0x80).view(np.int8).reshape(-1)
+            frag[nb, ks] = wu[rows, 16 * nb + (lanes % 16)[:, None]]
+    out = np.empty((N // 16, K * 16), np.uint8)
+    pairs = ks_n // 2
+    for nb in range(N // 16):
+        paired = frag[nb, :2 * pairs].reshape(pairs, 2, 64, 8).transpose(0, 2, 1, 3)
+        out[nb, :pairs * 1024] = paired.reshape(-1)
+        if ks_n % 2:
+            out[nb, pairs * 1024:] = frag[nb, ks_n - 1].reshape(-1)
+    return out.view(np.int8).reshape(-1)
 
 
 def test_w8a16_pack_layout(tl, orc):
     rng = np.random.default_rng(3)
-    K, N = 128, 48
-    w = rng.integers(-128, 128, size=(K, N), dtype=np.int64).astype(np.int8)
-    dw = to_dev_raw(w)
-    out = to_dev_raw(np.zeros(K * N, np.int8))
-    tl.w8a16_pack(dw.data_ptr(), K, N, out.data_ptr(), stream())
     import torch
-    torch.cuda.synchronize()
-    assert np.array_equal(out.cpu().numpy(), pack_np(w))
+    for K, N in ((128, 48), (96, 32)):  # paired steps only; a last unpaired step
+        w = rng.integers(-128, 128, size=(K, N), dtype=np.int64).astype(np.int8)
+        dw = to_dev_raw(w)
+        out = to_dev_raw(np.zeros(K * N, np.int8))
+        tl.w8a16_pack(dw.data_ptr(), K, N, out.data_ptr(), stream())
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), pack_np(w))
     with pytest.raises(tl.TinyLLMError, match="multiple"):
         tl.w8a16_pack(dw.data_ptr(), 100, N, out.data_ptr(), stream())
 

@@ -129,6 +129,15 @@ template <bool PACKED> __device__ __forceinline__ uint2 w8x4_to_f16x4(uint32_t v
     return u8x4_to_f16x4(PACKED ? v : v ^ 0x80808080u);
 }
 
+// Byte offset, within its column block, of lane `lane`'s 8 bytes of k step st
+// in the packed layout (see w8a16_pack_kernel): steps are stored in pairs,
+// 16 bytes per lane (step 2p in the low 8), a last unpaired step (K % 64 ==
+// 32) at 8 bytes per lane.
+__device__ __forceinline__ uint32_t packed_step_offset(int st, int ksteps, int lane) {
+    const uint32_t base = (uint32_t)(st >> 1) * 1024u;
+    return st < (ksteps & ~1) ? base + 16u * lane + 8u * (st & 1) : base + 8u * lane;
+}
+
 // Split-K inside the workgroup: one workgroup (4 waves) per unit (64-row
 // tile, 64-column tile, K split); wave w takes k steps 4w..4w+3 of every
 // 16-step (512-row) batch of the split for the whole 64x64 tile, x through
@@ -170,7 +179,7 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
     const int       ngroups = (a.K + GS - 1) / GS;
     const int       m0 = mt * kBM;
 
-    const int8_t *wp[4]; // packed: uniform column-block bases; lanes add 8 * lane (+ 512 per step)
+    const int8_t *wp[4]; // packed: uniform column-block bases (+ packed_step_offset)
     const __half *sp[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
@@ -261,7 +270,7 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
                 const int st = min(first + j, ksteps - 1);
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb)
-                    wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + (uint32_t)(st * 512 + 8 * lane));
+                    wv[j][cb] = *reinterpret_cast<const uint2 *>(wp[cb] + packed_step_offset(st, ksteps, lane));
             }
         } else {
             issue_w(first);
@@ -585,7 +594,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
         u32x4 x[8]; // 4 rows x 256 bytes of x per load
     };
     struct WSlot {
-        uint2  w[PACKED ? 4 * CB : 1]; // [k step][cb]
+        u32x4  w[PACKED ? 2 * CB : 1]; // [k step pair][cb]: steps 2p (.xy) and 2p + 1 (.zw)
         u32x4  r[PACKED ? 1 : 2 * CB]; // row pieces (reference layout)
         __half s[NF][CB];              // converted at the fold: a conversion here would wait for the load
     };
@@ -597,11 +606,11 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
     auto load_w = [&](WSlot &sl, int c) __attribute__((always_inline)) {
         if constexpr (PACKED) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int p = 0; p < 2; ++p)
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
-                    sl.w[s * CB + cb] = __builtin_bit_cast(
-                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[cb], 8 * lane + 512 * s, (nb[cb] * ksteps + 4 * c) * 512, 0));
+                    sl.w[p * CB + cb] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[cb], 16 * lane + 1024 * p, (nb[cb] * ksteps + 4 * c) * 512, 0));
         } else {
             // stage slot q = t * 64 + lane (16 bytes): row q / CB, slot q % CB
             // of the row, which holds piece (q % CB - dec_rot(row)) mod CB
@@ -670,7 +679,8 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
             for (int cb = 0; cb < CB; ++cb) {
                 uint2 raw;
                 if constexpr (PACKED) {
-                    raw = sl.w[s * CB + cb];
+                    const u32x4 &q = sl.w[(s >> 1) * CB + cb];
+                    raw = (s & 1) ? make_uint2(q[2], q[3]) : make_uint2(q[0], q[1]);
                 } else {
                     const int   i = lane & 15;
                     const int   r = 32 * s + 8 * (lane >> 4) + (i >> 1);
@@ -804,12 +814,15 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
     }
 }
 
-// Repacks W [K][N] int8 (K % 32 == 0, N % 16 == 0) so that the B fragment of
-// v_mfma_f32_16x16x32_f16 for column block nb and k step ks is 512
-// contiguous bytes: packed[((nb * K/32 + ks) * 64 + l) * 8 + j] =
-// W[32 ks + 8 (l / 16) + j][16 nb + l % 16] ^ 0x80 -- offset binary (W + 128
-// as an unsigned byte), which the kernels turn into fp16 without the XOR a
-// signed byte needs.  One thread per (nb, ks, l).
+// Repacks W [K][N] int8 (K % 32 == 0, N % 16 == 0) into the B fragments of
+// v_mfma_f32_16x16x32_f16: lane l of the fragment of column block nb and k
+// step ks holds W[32 ks + 8 (l / 16) + j][16 nb + l % 16] ^ 0x80, j = 0..7 --
+// offset binary (W + 128 as an unsigned byte), which the kernels turn into
+// fp16 without the XOR a signed byte needs.  Column block nb takes the K * 16
+// bytes from nb * K * 16; within it the steps come in pairs, 1024 bytes per
+// pair p with lane l's 16 bytes at 16 l (step 2p, then step 2p + 1), so that
+// one 16-byte load per lane brings two steps; a last unpaired step (K % 64 ==
+// 32) takes 8 bytes per lane.  One thread per (nb, ks, l).
 __global__ __launch_bounds__(256) void w8a16_pack_kernel(const int8_t *w, int K, int N, int8_t *out) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t total = (int64_t)(N / 16) * (K / 32) * 64;
@@ -826,7 +839,8 @@ __global__ __launch_bounds__(256) void w8a16_pack_kernel(const int8_t *w, int K,
         lo |= (uint32_t)(uint8_t)w[(int64_t)(k0 + j) * N + col] << (8 * j);
         hi |= (uint32_t)(uint8_t)w[(int64_t)(k0 + 4 + j) * N + col] << (8 * j);
     }
-    *reinterpret_cast<uint2 *>(out + idx * 8) = make_uint2(lo ^ 0x80808080u, hi ^ 0x80808080u);
+    int8_t *const dst = out + (int64_t)nb * K * 16 + packed_step_offset(ks, K / 32, l);
+    *reinterpret_cast<uint2 *>(dst) = make_uint2(lo ^ 0x80808080u, hi ^ 0x80808080u);
 }
 
 // The epilogue of four consecutive columns n..n+3 of one segment (n % 4 ==
