@@ -498,7 +498,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
     static_assert(CB >= 1 && CB <= 4, "column blocks");
     constexpr int NF = 4 / FS;                                  // folds per chunk
     constexpr int RED = kDecWaves * 2 * CB * 64 * 4;            // floats: every wave's tile
-    constexpr int XPITCH = 256 + 16;                            // bytes: an x stage row (padded)
+    constexpr int XPITCH = 256 + 32;                            // bytes: an x stage row (padded)
     constexpr int XST = kDecHalf * XPITCH;                      // bytes: a wave's x stage (one chunk)
     constexpr int WST = PACKED ? 0 : 128 * CB * 16;             // bytes: its W stage (reference layout)
     constexpr int STAGE = kDecWaves * (XST + WST) / 4;          // floats
@@ -650,10 +650,13 @@ __global__ __launch_bounds__(512, 1) void w8a16_dec_kernel(DecArgs a) {
         }
     // The wave's stages (one chunk each; LDS operations of a wave run in
     // order, so the next chunk's writes follow this chunk's reads).  x stage:
-    // 32 rows of 256 bytes, 16 bytes of padding after each, so that the
-    // stores (8 lanes = 8 pieces of a row) and the A-fragment reads (8 lanes =
-    // 8 rows, one piece: 272 bytes apart, 16 bytes apart in the banks) touch
-    // distinct banks, and every address is a lane base plus an immediate.
+    // 32 rows of 256 bytes, 32 bytes of padding after each, so that every
+    // address is a lane base plus an immediate and neither the stores (16
+    // lanes = a row's 16 pieces) nor the A-fragment reads (16 lanes = 16 rows,
+    // one piece, 288 bytes apart) conflict in the banks.  (With 16 bytes of
+    // padding the reads conflicted: an LDS probe counted one conflict cycle
+    // per active cycle; the XOR swizzle this replaces needed ~130 more VALU
+    // per wave for its addresses.)
     uint8_t *const xst = reinterpret_cast<uint8_t *>(lds) + (size_t)wave * (XST + WST);
     uint8_t *const wst = xst + XST;
     auto compute = [&](const XSlot &xs, const WSlot &sl, int c) __attribute__((always_inline)) {
