@@ -597,6 +597,8 @@ def prefill_bench(args, tl, torch, np):
             assert mgr.appendKV(sid, 0, pk.data_ptr(), pk.data_ptr(), p0, stream) is None
             mgr.advanceSeqLen(sid, p0)
     T = nseq * n
+    # the workgroup size the planner takes for this launch (prefill_waves)
+    waves = tl.prefill_plan_waves([p0] * nseq, [n] * nseq, Hq, Hkv, D)
     q = ns.draw(s_q, (T, Hq, D))
     nk = ns.draw(s_k, (T, Hkv * D))
     nv = ns.draw(s_v, (T, Hkv * D))
@@ -656,10 +658,11 @@ def prefill_bench(args, tl, torch, np):
         "data": f"synthetic: Q/K/V ~ N(0,1) ({GEN_NOTE})",
         "config": {"workload": f"llama3_8b_prefill_{nseq}x{n}" + (f"_prefix{p0}" if p0 else ""),
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "prompts": nseq,
-                   "new_tokens": n, "cached_prefix": p0, "attended_keys": keys},
+                   "new_tokens": n, "cached_prefix": p0, "attended_keys": keys,
+                   "workgroup_waves": waves},
         "kernels_us": {"attn_prefill": round(a_avg * 1e3, 2), "kv_append": round(c_avg * 1e3, 2)},
         "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
-        "roofline": {"kernel": "attn_prefill_kernel<128,4,contiguous>", "bound": "mfma",
+        "roofline": {"kernel": f"attn_prefill_kernel<128,4,contiguous,{waves} waves>", "bound": "mfma",
                      "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": None},
         "cpu_baseline": None,

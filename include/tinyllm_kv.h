@@ -296,6 +296,25 @@ int  tl_kv_prefill_run(tl_kv_prefill *p, int layer, const void *q, const void *n
                        const void *new_v, void *out, float scale, void *stream);
 int  tl_kv_prefill_commit(tl_kv_prefill *p);
 
+/* Waves per prefill-attention workgroup, process-wide: 0 = auto, 4 or 8
+ * (8: one 256-row workgroup per CU; 4: two 128-row workgroups per CU, one's
+ * start-up under the other's tiles).  Auto takes 4 at head_dim 128 when the
+ * 8-wave tiling gives every CU at least 3 work items ((entry, query tile) x
+ * kv heads) that attend at most 800 keys on average, else 8; head_dim 256 is
+ * always 4.  Initial value from the environment variable TL_PREFILL_WAVES
+ * ("4" / "8"), else 0.  A prefill batch keeps the waves of its prepare; the
+ * compact tl_attention_prefill chooses per call.  Every setting gives the
+ * same outputs within the 1e-3 gate.  No reference counterpart (tuning
+ * knob). */
+int tl_prefill_set_waves(int waves);
+int tl_prefill_get_waves(void);
+/* The waves per workgroup the prefill entry points choose under the current
+ * setting for n sequences with prefix_lens[i] cached and num_tokens[i] new
+ * tokens (num_tokens[i] >= 1), num_q_heads / num_kv_heads in {1,2,4,8},
+ * head_dim in {32,64,128,256}, on num_cus CUs (0: the current device's). */
+int tl_prefill_plan_waves(const int32_t *prefix_lens, const int32_t *num_tokens, int n,
+                          int num_q_heads, int num_kv_heads, int head_dim, int num_cus, int *waves);
+
 /* w8a16_matmul (kernels/w8a16_matmul.cuh:22-26, w8a16_matmul.cu:219-236):
  * output[M][N] = fp16(input[M][K] @ dequant(weight[K][N] int8,
  * scales[ceil(K/group_size)][N] fp16)), fp32 accumulation.  Returns TL_OK

@@ -21,6 +21,17 @@ from devutil import empty_dev, rel_err, stream, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=[8, 4], ids=["8waves", "4waves"])
+def pwaves(request, tl):
+    """Forces the prefill workgroup size (tl_prefill_set_waves) for one test:
+    both forms of the kernel run every parity case (head_dim 256 has the
+    4-wave form only)."""
+    old = tl.get_prefill_waves()
+    tl.set_prefill_waves(request.param)
+    yield request.param
+    tl.set_prefill_waves(old)
+
+
 def f16bits(rng, shape, std=1.0):
     return (rng.standard_normal(shape) * std).astype(np.float32).astype(np.float16).view(np.uint16)
 
@@ -31,7 +42,7 @@ def f32(bits):
 
 @pytest.mark.parametrize("B,H,S,D", [(1, 2, 8, 32), (2, 4, 100, 64), (1, 8, 300, 128),
                                      (1, 2, 70, 256), (3, 1, 1, 64), (1, 3, 129, 128)])
-def test_attention_prefill_matches_oracle(tl, orc, B, H, S, D):
+def test_attention_prefill_matches_oracle(tl, orc, pwaves, B, H, S, D):
     rng = np.random.default_rng(B * 1000 + S + D)
     q, k, v = (f16bits(rng, (B, H, S, D)) for _ in range(3))
     scale = 1.0 / np.sqrt(D)
@@ -71,7 +82,7 @@ def make_pool(tl, kind, L, H, D, M, B, rng):
 
 @pytest.mark.parametrize("kind", ["slots", "perm", "blocks"])
 @pytest.mark.parametrize("D,G", [(128, 4), (64, 1), (128, 8), (32, 2), (256, 1)])
-def test_prefill_batch_matches_oracle(tl, orc, kind, D, G):
+def test_prefill_batch_matches_oracle(tl, orc, pwaves, kind, D, G):
     rng = np.random.default_rng(D * 7 + G + len(kind))
     L, H, M, B = 2, 2, 512, 5
     Hq = H * G
@@ -132,7 +143,7 @@ def test_prefill_batch_matches_oracle(tl, orc, kind, D, G):
 
 
 @pytest.mark.parametrize("D,G", [(128, 4), (64, 8)])
-def test_chunked_prefill_equals_one_shot(tl, D, G):
+def test_chunked_prefill_equals_one_shot(tl, pwaves, D, G):
     """A prompt prefilled in one call and the same prompt in three chunks
     (each chunk attending to the cached earlier ones) give identical bits."""
     rng = np.random.default_rng(5 + D + G)
@@ -161,7 +172,7 @@ def test_chunked_prefill_equals_one_shot(tl, D, G):
 
 @pytest.mark.parametrize("kind", ["slots", "blocks"])
 @pytest.mark.parametrize("D,G", [(128, 4), (64, 8), (32, 1), (256, 2)])
-def test_fused_prefill_equals_append_then_attention(tl, kind, D, G):
+def test_fused_prefill_equals_append_then_attention(tl, pwaves, kind, D, G):
     """PrefillBatch.run (one launch: keys at or past the write position read
     from new_k/new_v, the rows written into the cache by the attention
     kernel) == append() followed by attention(): identical cache bytes and
@@ -207,6 +218,61 @@ def test_fused_prefill_equals_append_then_attention(tl, kind, D, G):
         pools.append((to_host(gk), to_host(gv)))
         keep.append(g)
     assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(pools[0][0], pools[1][0]) and np.array_equal(pools[0][1], pools[1][1])
+
+
+@pytest.mark.parametrize("D,G", [(128, 4), (64, 8), (32, 1), (128, 1)])
+def test_prefill_waves_give_identical_bits(tl, D, G):
+    """The 4- and 8-wave workgroups compute every query row with the same
+    per-wave code and tile order (tiles past a row's last key, which only the
+    longer query tile visits, add exact zeros), so both give the same output
+    and cache bits: PrefillBatch.run over prompts with and without a cached
+    prefix, and the compact attention_prefill."""
+    rng = np.random.default_rng(31 + D + G)
+    H, M, B = 2, 1024, 4
+    Hq = H * G
+    prefix, new = [0, 130, 0, 64], [333, 200, 64, 7]
+    q = f16bits(rng, (sum(new), Hq, D))
+    nk, nv = f16bits(rng, (sum(new), H * D)), f16bits(rng, (sum(new), H * D))
+    pre = [(f16bits(rng, p0 * H * D), f16bits(rng, p0 * H * D)) for p0 in prefix]
+    old = tl.get_prefill_waves()
+    outs, pools, keep = [], [], []
+    try:
+        for waves in (8, 4):
+            tl.set_prefill_waves(waves)
+            g = tl.KVCacheManager(1, H, D, M, B)
+            ids = []
+            for p0, (k, v) in zip(prefix, pre):
+                sid, _ = g.allocateSequence(M)
+                ids.append(sid)
+                if p0:
+                    dk, dv = to_dev(k), to_dev(v)
+                    keep += [dk, dv]
+                    assert g.appendKV(sid, 0, dk.data_ptr(), dv.data_ptr(), p0, stream()) is None
+                    g.advanceSeqLen(sid, p0)
+            pb = tl.PrefillBatch(g, B, Hq)
+            pb.prepare(ids, new, stream())
+            dq, dk, dv = to_dev(q), to_dev(nk), to_dev(nv)
+            out = empty_dev((sum(new), Hq, D))
+            keep += [dq, dk, dv]
+            pb.run(0, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), out.data_ptr(), D ** -0.5, stream())
+            outs.append(to_host(out))
+            lens = [p + n for p, n in zip(prefix, new)]
+            db = tl.DecodeBatch(g, B, Hq)
+            db.prepare_lengths(ids, lens, stream())
+            gk, gv = empty_dev((B, H, max(lens), D)), empty_dev((B, H, max(lens), D))
+            db.gather(0, gk.data_ptr(), gv.data_ptr(), max(lens), stream())
+            pools.append((to_host(gk), to_host(gv)))
+            keep.append(g)
+            cq, ck, cv = (to_dev(f16bits(np.random.default_rng(9), (2, Hq, 300, D))) for _ in range(3))
+            co = empty_dev((2, Hq, 300, D))
+            tl.attention_prefill(cq.data_ptr(), ck.data_ptr(), cv.data_ptr(), co.data_ptr(), D ** -0.5, 2, Hq,
+                                 300, D, stream())
+            outs.append(to_host(co))
+            keep += [cq, ck, cv, co]
+    finally:
+        tl.set_prefill_waves(old)
+    assert np.array_equal(outs[0], outs[2]) and np.array_equal(outs[1], outs[3])
     assert np.array_equal(pools[0][0], pools[1][0]) and np.array_equal(pools[0][1], pools[1][1])
 
 

@@ -80,3 +80,14 @@ def test_w8a16_kernels_use_no_scratch(tmp_path):
     for name, r in ks.items():
         assert r["private_segment_fixed_size"] == 0, (name, r)
         assert r["vgpr_spill_count"] == 0, (name, r)
+
+
+def test_prefill_kernels_spill_nothing(tmp_path):
+    """Both prefill workgroup forms (8 and 4 waves up to head_dim 128, 4 at
+    256) keep their registers: no spills, no private memory."""
+    ks = kernels("attention_prefill.o", tmp_path)
+    pf = {n: r for n, r in ks.items() if "attn_prefill_kernel" in n}
+    # 4 head_dims x 4 groups x 2 layouts, two wave forms below head_dim 256
+    assert len(pf) == 3 * 4 * 2 * 2 + 4 * 2, sorted(pf)
+    bad = {n: r for n, r in pf.items() if r["vgpr_spill_count"] or r["private_segment_fixed_size"]}
+    assert not bad, bad

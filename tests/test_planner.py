@@ -395,3 +395,66 @@ def test_current_mode_follows_the_process_settings(tl, monkeypatch):
     finally:
         tl.set_head_fuse(hf0)
         tl.set_waves(w0)
+
+
+# Prefill workgroup size (prefill_waves, attention_prefill.hip): the shapes
+# timed on one box at Llama-3-8B heads (32 q / 8 kv, head_dim 128), 8- against
+# 4-wave workgroups, us per launch: (prompts, new tokens, cached prefix) ->
+# the faster form.  4 waves won 2-8.5% where it is expected, 8 waves 3-10%
+# elsewhere.
+PREFILL_MEASURED = {
+    (64, 128, 0): 4,     # 51.4 / 49.8
+    (32, 256, 0): 4,     # 66.1 / 60.9
+    (16, 512, 0): 4,     # 81.1 / 74.2
+    (16, 768, 0): 4,     # 127.4 / 121.7
+    (8, 1024, 0): 4,     # 96.6 / 94.5
+    (16, 1024, 0): 4,    # 207.5 / 202.6
+    (4, 1536, 0): 4,     # 99.5 / 96.0
+    (8, 512, 0): 8,      # 38.4 / 41.6: two items per CU
+    (4, 2048, 0): 8,     # 152 / 157
+    (2, 4096, 0): 8,     # 278.6 / 287.2
+    (1, 8192, 0): 8,     # 518 / 551
+    (16, 512, 1024): 8,  # 192.8 / 205.8: long items (cached prefix)
+    (8, 512, 4096): 8,   # 276.4 / 304.8
+}
+
+
+@pytest.mark.parametrize("shape", sorted(PREFILL_MEASURED))
+def test_prefill_waves_follow_the_measured_shapes(tl, shape):
+    b, n, p0 = shape
+    old = tl.get_prefill_waves()
+    tl.set_prefill_waves(0)
+    try:
+        assert tl.prefill_plan_waves([p0] * b, [n] * b, 32, 8, 128, CUS) == PREFILL_MEASURED[shape]
+    finally:
+        tl.set_prefill_waves(old)
+
+
+def test_prefill_waves_rule_boundaries_and_settings(tl):
+    old = tl.get_prefill_waves()
+    try:
+        tl.set_prefill_waves(0)
+        # items = 4 x 8 kv heads x 24 query tiles = 768 = 3 per CU, mean keys
+        # exactly 800: both limits inclusive
+        assert tl.prefill_plan_waves([0] * 4, [1536] * 4, 32, 8, 128, CUS) == 4
+        # one item per CU fewer than 3 per CU: 8 waves
+        assert tl.prefill_plan_waves([0] * 4, [1536] * 4, 32, 8, 128, CUS + 1) == 8
+        # a cached prefix long enough to lift the mean past 800 keys
+        assert tl.prefill_plan_waves([64] * 4, [1536] * 4, 32, 8, 128, CUS) == 8
+        # auto is measured at head_dim 128 only; 256 has the 4-wave form only
+        assert tl.prefill_plan_waves([0] * 16, [512] * 16, 32, 8, 64, CUS) == 8
+        assert tl.prefill_plan_waves([0] * 16, [512] * 16, 32, 8, 256, CUS) == 4
+        for forced in (4, 8):
+            tl.set_prefill_waves(forced)
+            assert tl.get_prefill_waves() == forced
+            for d in (32, 64, 128):
+                assert tl.prefill_plan_waves([0], [8192], 32, 8, d, CUS) == forced
+            assert tl.prefill_plan_waves([0], [8192], 32, 8, 256, CUS) == 4
+        with pytest.raises(tl.TinyLLMError, match="waves must be"):
+            tl.set_prefill_waves(2)
+        with pytest.raises(tl.TinyLLMError, match="invalid lengths"):
+            tl.prefill_plan_waves([0], [0], 32, 8, 128, CUS)
+        with pytest.raises(tl.TinyLLMError, match="unsupported"):
+            tl.prefill_plan_waves([0], [16], 32, 8, 96, CUS)
+    finally:
+        tl.set_prefill_waves(old)

@@ -3,6 +3,7 @@
 #include "tinyllm_kv.h"
 
 #include "kernels/kv_kernels.h"
+#include "kernels/prefill.h"
 #include "runtime.h"
 #include "tiny_llm/kernels/attention.h"
 #include "tiny_llm/kv_cache.h"
@@ -12,6 +13,7 @@
 #include <cstring>
 #include <memory>
 #include <string>
+#include <vector>
 
 namespace tiny_llm {
 namespace detail {
@@ -460,6 +462,37 @@ int tl_kv_prefill_run(tl_kv_prefill *p, int layer, const void *q, const void *ne
 int tl_kv_prefill_commit(tl_kv_prefill *p) {
     if (!p) return fail(TL_ERR_INVALID, "tl_kv_prefill_commit: null batch");
     return guarded([&] { return status(p->b->commit()); });
+}
+
+int tl_prefill_set_waves(int waves) {
+    if (waves != 0 && waves != 4 && waves != 8)
+        return fail(TL_ERR_INVALID, "tl_prefill_set_waves: waves must be 0 (auto), 4 or 8");
+    tiny_llm::detail::set_prefill_waves(waves);
+    return TL_OK;
+}
+
+int tl_prefill_get_waves(void) { return tiny_llm::detail::prefill_waves_setting(); }
+
+int tl_prefill_plan_waves(const int32_t *prefix_lens, const int32_t *num_tokens, int n,
+                          int num_q_heads, int num_kv_heads, int head_dim, int num_cus, int *waves) {
+    namespace d = tiny_llm::detail;
+    if (!waves) return fail(TL_ERR_INVALID, "tl_prefill_plan_waves: waves is null");
+    if (n < 0 || (n > 0 && (!prefix_lens || !num_tokens)))
+        return fail(TL_ERR_INVALID, "tl_prefill_plan_waves: invalid lengths");
+    if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 || num_cus < 0 ||
+        !d::prefill_shape_supported(head_dim, num_q_heads / num_kv_heads))
+        return fail(TL_ERR_INVALID, "tl_prefill_plan_waves: unsupported heads, head_dim or num_cus");
+    std::vector<d::PrefillEntry> e(static_cast<size_t>(n));
+    for (int i = 0; i < n; ++i) {
+        if (prefix_lens[i] < 0 || num_tokens[i] < 1)
+            return fail(TL_ERR_INVALID, "tl_prefill_plan_waves: invalid lengths");
+        e[static_cast<size_t>(i)] = {0, prefix_lens[i], num_tokens[i], i, 0};
+    }
+    return guarded([&] {
+        *waves = d::prefill_waves(e.data(), n, head_dim, num_q_heads / num_kv_heads, num_kv_heads,
+                                  num_cus > 0 ? num_cus : d::device_cus());
+        return TL_OK;
+    });
 }
 
 void tl_attention_prefill(const void *q, const void *k, const void *v, void *out, float scale,

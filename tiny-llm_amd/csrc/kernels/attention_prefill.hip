@@ -43,8 +43,11 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <climits>
+#include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 
 namespace tiny_llm {
@@ -80,14 +83,15 @@ __device__ __forceinline__ float xor_lane_max(float x) {
     }
 }
 
-// Threads per workgroup: 8 waves (two per SIMD, one workgroup per CU) up to
-// head_dim 128, so each K/V tile in LDS serves 256 query rows; 4 waves for
-// head_dim 256, whose register file allows one wave per SIMD.  (Head_dim 128
-// with 4 waves of three 16-row groups each -- a third less LDS read traffic
-// per flop, one wave per SIMD -- was 1.5x slower: the second wave on each
-// SIMD hides the LDS and MFMA latencies.)
-template <int D>
-constexpr int kPThreads = D <= 128 ? 512 : 256;
+// Waves per workgroup (template argument NW): up to head_dim 128, 8 (two per
+// SIMD, one workgroup per CU), so each K/V tile in LDS serves 256 query rows,
+// or 4 (two workgroups per CU, 128 rows each: one's start-up -- work record,
+// q, first tile -- runs under the other's tiles, which pays for launches of
+// many short items; the planner's rule is prefill_waves); 4 for head_dim 256,
+// whose register file allows one wave per SIMD.  (Head_dim 128 with 4 waves
+// of three 16-row groups each -- a third less LDS read traffic per flop, one
+// wave per SIMD -- was 1.5x slower: the second wave on each SIMD hides the LDS
+// and MFMA latencies.)
 // Lazy rescaling threshold of the online softmax, in log2 units.
 constexpr float kLazyMax = 8.0f;
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt == 0 only.
@@ -159,15 +163,15 @@ __device__ __forceinline__ float materialize(float x) {
     return x;
 }
 
-template <int D, int G, bool PAGED>
-__global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(PrefillArgs a) {
+template <int D, int G, bool PAGED, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(PrefillArgs a) {
     static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head_dim");
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group size");
+    static_assert(NW == 4 || (NW == 8 && D <= 128), "waves");
     constexpr int NQG = kQueryGroups<D>;    // 16-query column groups per wave
-    constexpr int NT = kPThreads<D>;        // threads
-    constexpr int NW = NT / 64;             // waves
+    constexpr int NT = NW * 64;             // threads
     constexpr int ROWS = NW * 16 * NQG;     // query rows per workgroup
-    static_assert(ROWS == prefill_rows(D), "the planner's query tile");
+    static_assert(ROWS == prefill_rows(D, NW), "the planner's query tile");
     constexpr int BQ = ROWS / G;            // query tokens per workgroup
     constexpr int KS = D / 32;              // k steps of S^T
     constexpr int DT = D / 16;              // dim tiles of O^T
@@ -471,10 +475,10 @@ __global__ __launch_bounds__(kPThreads<D>) __attribute__((amdgpu_waves_per_eu(D 
     constexpr int R = 16 * NQG;      // rows of the wave
     constexpr int PPR = D / 8;       // 16-byte pieces per row
     constexpr int NCH = R * PPR / 64; // pieces per lane
-    // Staging: up to head_dim 128 a region of its own (the workgroup has the
-    // CU's LDS to itself); head_dim 256 reuses the K/V buffers, two waves per
-    // buffer.
-    constexpr bool OWN = D <= 128;
+    // Staging: 8-wave workgroups up to head_dim 128 a region of its own (the
+    // workgroup has the CU's LDS to itself); 4-wave ones (two per CU) reuse
+    // the K/V buffers, one wave per buffer (head_dim 256: two).
+    constexpr bool OWN = D <= 128 && NW == 8;
     __shared__ __align__(16) uint16_t own_stg[OWN ? NW * R * OP : 8];
     static_assert(OWN || ((NW + 3) / 4) * R * OP <= kKeyTile * ROWH, "staging fits the K/V buffers");
     uint16_t *stg;
@@ -558,23 +562,50 @@ __global__ __launch_bounds__(256) void attention_weights_kernel(const __half *q,
     (void)H;
 }
 
-template <int D, int G>
-void launch_dg(const PrefillArgs &a, int grid, bool paged, hipStream_t stream) {
+template <int D, int G, int NW>
+void launch_dgw(const PrefillArgs &a, int grid, bool paged, hipStream_t stream) {
     if (paged)
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true>), dim3(grid), dim3(kPThreads<D>), 0, stream, a);
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, true, NW>), dim3(grid), dim3(NW * 64), 0, stream, a);
     else
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false>), dim3(grid), dim3(kPThreads<D>), 0, stream, a);
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, false, NW>), dim3(grid), dim3(NW * 64), 0, stream, a);
+}
+
+template <int D, int G>
+void launch_dg(const PrefillArgs &a, int grid, int waves, bool paged, hipStream_t stream) {
+    if constexpr (D <= 128) {
+        if (waves == 8) {
+            launch_dgw<D, G, 8>(a, grid, paged, stream);
+            return;
+        }
+    }
+    launch_dgw<D, G, 4>(a, grid, paged, stream);
 }
 
 template <int D>
-void launch_d(const PrefillArgs &a, int grid, int G, bool paged, hipStream_t stream) {
+void launch_d(const PrefillArgs &a, int grid, int G, int waves, bool paged, hipStream_t stream) {
     switch (G) {
-    case 1: launch_dg<D, 1>(a, grid, paged, stream); break;
-    case 2: launch_dg<D, 2>(a, grid, paged, stream); break;
-    case 4: launch_dg<D, 4>(a, grid, paged, stream); break;
-    case 8: launch_dg<D, 8>(a, grid, paged, stream); break;
+    case 1: launch_dg<D, 1>(a, grid, waves, paged, stream); break;
+    case 2: launch_dg<D, 2>(a, grid, waves, paged, stream); break;
+    case 4: launch_dg<D, 4>(a, grid, waves, paged, stream); break;
+    case 8: launch_dg<D, 8>(a, grid, waves, paged, stream); break;
     default: break;
     }
+}
+
+// TL_PREFILL_WAVES ("4" / "8") at first use, else auto; set_prefill_waves
+// overrides it.
+std::atomic<int> g_prefill_waves{-1};
+
+// The rule of prefill_waves over the 8-wave tiling's items (x Hkv) and
+// their attended keys.
+int waves_rule(int D, int64_t items, int64_t keys, int Hkv, int cus) {
+    if (D > 128) return 4;
+    const int setting = prefill_waves_setting();
+    if (setting == 4 || setting == 8) return setting;
+    if (D != 128 || items <= 0) return 8;
+    const bool many = items * Hkv >= (int64_t)kPrefill4wItemsPerCU * std::max(1, cus);
+    const bool short_items = keys <= (int64_t)kPrefill4wMeanKeys * items;
+    return many && short_items ? 4 : 8;
 }
 
 } // namespace
@@ -583,8 +614,41 @@ bool prefill_shape_supported(int D, int G) {
     return (D == 32 || D == 64 || D == 128 || D == 256) && (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
-void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<int32_t> &work) {
-    const int BQ = prefill_block_tokens(D, G);
+void set_prefill_waves(int waves) { g_prefill_waves.store(waves); }
+
+int prefill_waves_setting() {
+    int v = g_prefill_waves.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char *e = std::getenv("TL_PREFILL_WAVES");
+        v = 0;
+        if (e && std::strcmp(e, "4") == 0) v = 4;
+        if (e && std::strcmp(e, "8") == 0) v = 8;
+        g_prefill_waves.store(v);
+    }
+    return v;
+}
+
+int prefill_waves(const PrefillEntry *entries, int n, int D, int G, int Hkv, int cus) {
+    const int BQ = prefill_block_tokens(D, G, 8);
+    int64_t   items = 0, keys = 0;
+    for (int e = 0; e < n; ++e) {
+        const int nqt = (entries[e].n + BQ - 1) / BQ;
+        items += nqt;
+        for (int qt = 0; qt < nqt; ++qt) keys += (int64_t)entries[e].p0 + std::min(entries[e].n, (qt + 1) * BQ);
+    }
+    return waves_rule(D, items, keys, Hkv, cus);
+}
+
+int prefill_waves_uniform(int B, int S, int D, int G, int Hkv, int cus) {
+    const int     BQ = prefill_block_tokens(D, G, 8);
+    const int64_t nqt = (S + BQ - 1) / BQ;
+    int64_t       keys = 0;
+    for (int64_t qt = 0; qt < nqt; ++qt) keys += std::min<int64_t>(S, (qt + 1) * BQ);
+    return waves_rule(D, (int64_t)B * nqt, (int64_t)B * keys, Hkv, cus);
+}
+
+void plan_prefill(const PrefillEntry *entries, int n, int D, int G, int waves, std::vector<int32_t> &work) {
+    const int BQ = prefill_block_tokens(D, G, waves);
     struct It {
         int64_t keys;
         int32_t e, qt;
@@ -613,11 +677,16 @@ void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<
 void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int Hkv, int D,
                          float scale, hipStream_t stream) {
     const int G = Hq / Hkv;
-    int       items;
+    int       items, waves;
     if (p.work) {
         items = p.n_items;
+        waves = p.waves;
+        if (waves != 4 && !(waves == 8 && D <= 128))
+            throw std::invalid_argument("attention_prefill: the work list's waves per workgroup must be 4, or 8 "
+                                        "up to head_dim 128");
     } else {
-        const int BQ = prefill_block_tokens(D, G);
+        waves = prefill_waves_uniform(p.uniform_b, p.uniform_n, D, G, Hkv, device_cus());
+        const int BQ = prefill_block_tokens(D, G, waves);
         items = p.uniform_b * ((p.uniform_n + BQ - 1) / BQ);
     }
     if (items <= 0) return;
@@ -644,10 +713,10 @@ void launch_attn_prefill(const PrefillLaunch &p, const KvView &kv, int Hq, int H
         throw std::invalid_argument("attention_prefill: token offsets exceed 32 bits (keys * row bytes)");
     profile_begin(KernelId::AttnPrefill, stream);
     switch (D) {
-    case 32: launch_d<32>(a, (int)grid, G, paged, stream); break;
-    case 64: launch_d<64>(a, (int)grid, G, paged, stream); break;
-    case 128: launch_d<128>(a, (int)grid, G, paged, stream); break;
-    case 256: launch_d<256>(a, (int)grid, G, paged, stream); break;
+    case 32: launch_d<32>(a, (int)grid, G, waves, paged, stream); break;
+    case 64: launch_d<64>(a, (int)grid, G, waves, paged, stream); break;
+    case 128: launch_d<128>(a, (int)grid, G, waves, paged, stream); break;
+    case 256: launch_d<256>(a, (int)grid, G, waves, paged, stream); break;
     default: break;
     }
     HIP_CHECK(hipGetLastError());

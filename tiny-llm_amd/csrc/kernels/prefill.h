@@ -31,18 +31,45 @@ struct PrefillEntry {
 
 static_assert(sizeof(PrefillEntry) == 24, "six 32-bit words per entry");
 
-// Query rows (token, head) per workgroup: 256 up to head_dim 128 (8 waves x
-// 2 groups of 16), 64 at 256 (4 waves x 1).
-constexpr int prefill_rows(int D) { return D <= 128 ? 256 : 64; }
+// Query rows (token, head) per workgroup of `waves` waves: 16 per query group,
+// two groups per wave up to head_dim 128, one at 256.  Up to head_dim 128 a
+// workgroup has 8 waves (256 rows, one workgroup per CU) or 4 (128 rows, two
+// per CU); head_dim 256 has 4 (64 rows).
+constexpr int prefill_rows(int D, int waves) { return waves * 16 * (D <= 128 ? 2 : 1); }
 // Query tokens per workgroup: G heads of one kv group per token.
-inline int prefill_block_tokens(int D, int G) { return prefill_rows(D) / G; }
+inline int prefill_block_tokens(int D, int G, int waves) { return prefill_rows(D, waves) / G; }
 
-// Work items (entry, query tile), most keys first (LPT order for the
-// hardware dispatcher), each a self-contained record of kPrefillItemWords
-// 32-bit words: {q_off low, q_off high, p0, n, row, query tile, tok0, 0}, so
-// a workgroup needs one dependent load before its Q and K/V loads.
+// Waves per workgroup of a prefill launch over `entries`, with Hkv kv heads
+// (the grid is items x Hkv) on `cus` CUs: the process setting when it forces
+// 4 or 8 (head_dim <= 128; head_dim 256 is always 4); else, at head_dim 128,
+// 4 when the 8-wave tiling gives every CU at least kPrefill4wItemsPerCU
+// items and they attend at most kPrefill4wMeanKeys keys on average (many
+// short items: a workgroup's start-up -- work record, q, first tile -- is a
+// large part of each, and two 4-wave workgroups per CU run one's start-up
+// under the other's tiles), else 8 (longer items pay for the 4-wave form's
+// doubled K/V tile traffic per row; few items leave nothing to overlap).
+// Measured at Llama-3-8B heads (32 / 8, head_dim 128), µs per launch, 8 / 4
+// waves: 16 x 512 prompts 81.1 / 74.2, 32 x 256 66.1 / 60.9, 4 x 1536 99.5 /
+// 96.0, 8 x 1024 96.6 / 94.5; 8 x 512 (two items per CU) 38.4 / 41.6, 4 x
+// 2048 152 / 157, 1 x 8192 518 / 551, 16 x 512 after 1024 cached tokens
+// 193 / 206.
+constexpr int kPrefill4wItemsPerCU = 3;
+constexpr int kPrefill4wMeanKeys = 800;
+int prefill_waves(const PrefillEntry *entries, int n, int D, int G, int Hkv, int cus);
+// The same rule for `B` entries of S new tokens each and no cached prefix.
+int prefill_waves_uniform(int B, int S, int D, int G, int Hkv, int cus);
+// Process setting: 0 = auto (the rule above), 4 or 8; initial value from the
+// environment variable TL_PREFILL_WAVES ("4" / "8"), else 0.
+void set_prefill_waves(int waves);
+int  prefill_waves_setting();
+
+// Work items (entry, query tile of prefill_block_tokens(D, G, waves) tokens),
+// most keys first (LPT order for the hardware dispatcher), each a
+// self-contained record of kPrefillItemWords 32-bit words: {q_off low, q_off
+// high, p0, n, row, query tile, tok0, 0}, so a workgroup needs one dependent
+// load before its Q and K/V loads.  The launch must use the same waves.
 constexpr int kPrefillItemWords = 8;
-void plan_prefill(const PrefillEntry *entries, int n, int D, int G, std::vector<int32_t> &work);
+void plan_prefill(const PrefillEntry *entries, int n, int D, int G, int waves, std::vector<int32_t> &work);
 
 struct PrefillLaunch {
     const __half       *q = nullptr;
@@ -50,11 +77,13 @@ struct PrefillLaunch {
     int64_t             q_tok_stride = 0;
     int64_t             q_head_stride = 0;
     // Either a device work list of n_items records (plan_prefill; 32-byte
-    // aligned) ...
+    // aligned) with the waves per workgroup it was planned for ...
     const int32_t      *work = nullptr;
     int                 n_items = 0;
+    int                 waves = 0;
     // ... or, with work == NULL, `uniform_b` entries b with p0 = 0,
-    // n = uniform_n, row = b and q_off = b * q_entry_stride.
+    // n = uniform_n, row = b and q_off = b * q_entry_stride (waves by
+    // prefill_waves_uniform).
     int                 uniform_b = 0;
     int                 uniform_n = 0;
     int64_t             q_entry_stride = 0;

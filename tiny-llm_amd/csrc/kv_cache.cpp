@@ -824,7 +824,9 @@ Result<void> PrefillBatch::prepare(const int *seq_ids, const int *num_tokens, in
         if (r.isErr()) return r;
         mgr_.syncTable(stream);
     }
-    detail::plan_prefill(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads, work_);
+    waves_ = detail::prefill_waves(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads,
+                                   cfg.num_heads, detail::device_cus());
+    detail::plan_prefill(entries.data(), n, cfg.head_dim, num_q_heads_ / cfg.num_heads, waves_, work_);
     n_items_ = static_cast<int>(work_.size() / detail::kPrefillItemWords);
     slots_ = std::move(slots);
     pos0_.resize(static_cast<size_t>(n));
@@ -891,6 +893,7 @@ Result<void> PrefillBatch::launch(int layer_idx, const half *q, const half *new_
     p.q_head_stride = cfg.head_dim;
     p.work = d_work_;
     p.n_items = n_items_;
+    p.waves = waves_;
     p.max_keys = max_keys_;
     p.new_k = new_k;
     p.new_v = new_v;

@@ -264,6 +264,7 @@ class PrefillBatch {
     int                  n_ = 0;
     int                  tokens_ = 0;
     int                  n_items_ = 0;
+    int                  waves_ = 8; // waves per attention workgroup the work list was planned for
     int                  max_keys_ = 0;
     std::vector<int32_t> ids_, counts_, slots_, pos0_, work_;
     bool                 uploaded_ = false;

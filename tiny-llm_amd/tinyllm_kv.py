@@ -155,6 +155,9 @@ def _declare(L: C.CDLL) -> None:
         "tl_kv_prefill_attention": (i, [vp, i, vp, vp, f, vp]),
         "tl_kv_prefill_run": (i, [vp, i, vp, vp, vp, vp, f, vp]),
         "tl_kv_prefill_commit": (i, [vp]),
+        "tl_prefill_set_waves": (i, [i]),
+        "tl_prefill_get_waves": (i, []),
+        "tl_prefill_plan_waves": (i, [vp, vp, i, i, i, i, i, ip]),
         "tl_attn_set_score_path": (i, [i]),
         "tl_attn_get_score_path": (i, []),
         "tl_attn_set_waves": (i, [i]),
@@ -495,6 +498,31 @@ def set_head_fuse(mode: int):
 
 def get_head_fuse() -> int:
     return load().tl_attn_get_head_fuse()
+
+
+def set_prefill_waves(waves: int):
+    """Waves per prefill-attention workgroup: 0 = auto, 4 or 8."""
+    _check(load().tl_prefill_set_waves(waves))
+
+
+def get_prefill_waves() -> int:
+    return load().tl_prefill_get_waves()
+
+
+def prefill_plan_waves(prefix_lens, num_tokens, num_q_heads, num_kv_heads, head_dim, num_cus=0) -> int:
+    """The waves per workgroup the prefill entry points choose (under the
+    current setting) for sequences with prefix_lens[i] cached and
+    num_tokens[i] new tokens; num_cus 0 = the current device's."""
+    import numpy as np
+    p = np.ascontiguousarray(prefix_lens, dtype=np.int32)
+    t = np.ascontiguousarray(num_tokens, dtype=np.int32)
+    if p.shape != t.shape:
+        raise ValueError("prefix_lens and num_tokens differ in length")
+    out = C.c_int(0)
+    _check(load().tl_prefill_plan_waves(p.ctypes.data if p.size else None, t.ctypes.data if t.size else None,
+                                        int(p.size), num_q_heads,
+                                        num_kv_heads, head_dim, num_cus, C.byref(out)))
+    return out.value
 
 
 _HEAD_FUSE_CODES = {"current": -1, "auto": 0, "off": 1, 2: 2, 4: 4, 8: 8}
