@@ -397,11 +397,23 @@ def fixed_batch(args, tl, torch, workloads, np):
     info = batch.info()
     # kv heads per attention workgroup of the last timed step's plan (1: per
     # head; 2, 4, 8: head-fused), as the library's planner makes it
-    att_last = np.array([mgr.getSeqLen(s) for s in ids], dtype=np.int32)
-    plan = tl.attn_plan(att_last, Hkv, num_cus=torch.cuda.get_device_properties(0).multi_processor_count,
-                        head_fuse="current", head_dim=D)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    att_last = np.array([mgr.getSeqLen(s) + 1 for s in ids], dtype=np.int32)
+    plan = tl.attn_plan(att_last, Hkv, num_cus=cus, head_fuse="current", head_dim=D)
     heads_per_wg = plan["head_fused"] or 1
     fused_items = ("chunks" if plan["fused_chunked"] else "interleaved tiles") if plan["head_fused"] else None
+
+    # The plan of every timed step, for that step's attended lengths (ragged
+    # plans can change as the lengths grow): {plan: steps}.
+    def plan_name(p):
+        return (f"chunk {p['chunk_tokens']}, {p['work_items']} items, "
+                + (f"{p['head_fused']} kv heads per workgroup" if p["head_fused"] else "per head")
+                + (", merge" if p["any_multi"] else ""))
+    step_plans = {}
+    for i in range(K):
+        p_i = tl.attn_plan((lens0 + i + 1).astype(np.int32), Hkv, num_cus=cus, head_fuse="current",
+                           head_dim=D, with_rows=False)
+        step_plans[plan_name(p_i)] = step_plans.get(plan_name(p_i), 0) + 1
 
     # Per-step pass: the same steps (lengths not advanced) with one event
     # between consecutive steps, for the spread of the step time.
@@ -441,6 +453,7 @@ def fixed_batch(args, tl, torch, workloads, np):
             "alloc": "blocks" if blocks else ("permuted blocks" if bt else "full-length slots"),
             "chunk_tokens": info["chunk_tokens"], "work_items": info["work_items"],
             "kv_heads_per_workgroup": heads_per_wg, "head_fused_items": fused_items,
+            "timed_step_plans": step_plans,
             "parallelism": "single GPU"}
     data = (f"synthetic: KV ~ N(0,1)*{cfg.kv_std}, Q ~ N(0,1) ({GEN_NOTE}), prefilled "
             f"via appendKV" + (", 16-token blocks behind a seeded random permutation" if bt else ""))

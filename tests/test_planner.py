@@ -83,11 +83,15 @@ def test_benchmark_config_plans(tl, name):
 # configurations keep their chunk plans; cfg4 and cfg5, whose per-head
 # workgroups would have 4 waves, run them with 2 heads per 8-wave workgroup,
 # cfg4's split sequences in chunks 3/2 as long (3328 * 3/2 = 4992, rounded
-# up to 5120 tokens: 163 items).
+# up to 5120 tokens: 163 items).  cfg2's whole sequences in per-head 8-wave
+# workgroups end at 11 tile rounds; head pairs in chunks of 2560 end at 10
+# (plan_balanced_split): 16 sequences, 5 of them over 2560 tokens, 21 items.
 EXPECTED_FUSED = {
     "cfg3": dict(chunk_tokens=8448, work_items=64, waves=8, any_multi=0, inline_words=321,
                  head_fused=2, fused_chunked=0),
-    **{k: dict(EXPECTED[k], head_fused=0, fused_chunked=0) for k in ("cfg1", "cfg2")},
+    "cfg1": dict(EXPECTED["cfg1"], head_fused=0, fused_chunked=0),
+    "cfg2": dict(EXPECTED["cfg2"], chunk_tokens=2560, work_items=21, any_multi=1, inline_words=91,
+                 head_fused=2, fused_chunked=1),
     "cfg4": dict(EXPECTED["cfg4"], chunk_tokens=5120, work_items=163, inline_words=711, waves=8,
                  head_fused=2, fused_chunked=1),
     "cfg5": dict(EXPECTED["cfg5"], waves=8, head_fused=2, fused_chunked=1),
@@ -105,6 +109,58 @@ def fused_chunk_plan(per_head, lens):
         chunk = min(-(-(chunk * 3 // 2) // 256) * 256, cap)
     per_entry = -(-lens // chunk)
     return chunk, int(per_entry.sum()), int((per_entry > 1).any())
+
+
+def lpt_rounds_py(items_desc, per_item, waves_per_head, cus):
+    """Longest-first list scheduling (a heap of CU loads) of per_item
+    workgroups per item, in whole tile rounds: ceil(ceil(len / 64) /
+    waves_per_head) per workgroup."""
+    h = [0] * cus
+    for L in items_desc:
+        w = -(-(-(-int(L) // 64)) // waves_per_head)
+        for _ in range(per_item):
+            heapq.heapreplace(h, h[0] + w)
+    return max(h)
+
+
+def balanced_split_py(lens, hkv, cus):
+    """plan_balanced_split restated: the chunk c (a multiple of 256 from a
+    CU's share of the head pairs' tokens up to the longest length) whose
+    head-pair plan (hkv / 2 workgroups per item, 4 waves per head) ends at
+    least one tile round before whole sequences in per-head 8-wave
+    workgroups; the longest c among the shortest makespans; else 0."""
+    lens = [int(x) for x in lens]
+    if hkv % 2 or max(lens) <= 1024:
+        return 0
+    r0 = lpt_rounds_py(sorted(lens, reverse=True), hkv, 8, cus)
+    share = -(-(sum(lens) * (hkv // 2)) // cus)
+    best, best_r = 0, r0
+    for c in range(max(256, -(-share // 256) * 256), max(lens), 256):
+        items = sorted((min(c, L - t) for L in lens for t in range(0, L, c)), reverse=True)
+        r = lpt_rounds_py(items, hkv // 2, 4, cus)
+        if r < best_r or (r == best_r and best):
+            best, best_r = c, r
+    return best if best and best_r <= r0 - 1 else 0
+
+
+def test_balanced_split_rounds_examples(tl):
+    """cfg2's lengths (16 MHA sequences): whole sequences take 11 tile rounds,
+    head pairs in chunks of 2048, 2304 or 2816 also 11, of 2560 10 (the
+    kernel measured 88.0 us per layer against 91.6-96.3 for the others), so
+    2560 is the split.  Uniform lengths and short ones never split."""
+    lens, hkv = cases()["cfg2"]
+    ls = [int(x) for x in lens]
+    assert lpt_rounds_py(sorted(ls, reverse=True), 32, 8, CUS) == 11
+    for c, r in ((2048, 11), (2304, 11), (2560, 10), (2816, 11), (3072, 12), (3584, 14)):
+        items = sorted((min(c, L - t) for L in ls for t in range(0, L, c)), reverse=True)
+        assert lpt_rounds_py(items, 16, 4, CUS) == r, c
+    assert balanced_split_py(ls, 32, CUS) == 2560
+    p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="auto")
+    assert (p["chunk_tokens"], p["head_fused"], p["fused_chunked"]) == (2560, 2, 1)
+    # the per-head-only plan (head_fuse off) and a forced chunk keep their chunks
+    assert tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="off")["chunk_tokens"] == 4096
+    assert tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="auto", forced_chunk=3072)["chunk_tokens"] == 3072
+    assert balanced_split_py([1000] * 16, 32, CUS) == 0
 
 
 @pytest.mark.parametrize("name", sorted(EXPECTED_FUSED))
@@ -190,13 +246,19 @@ def test_random_plans_head_fused(tl, seed):
         # the chunk plan, over 2 (auto, where per-head workgroups would have 4
         # waves) or the forced number of heads per workgroup
         per_head = tl.attn_plan(lens, hkv, num_cus=cus, head_fuse="off")
+        split = 0
         if force in (2, 4, 8):
             want = force if hkv % force == 0 else 0
         else:
             want = 2 if hkv % 2 == 0 and per_head["waves"] == 4 else 0
+            if hkv % 2 == 0 and per_head["waves"] == 8 and not per_head["any_multi"]:
+                split = balanced_split_py(lens, hkv, cus)
+                want = 2 if split else want
         assert (p["head_fused"], p["fused_chunked"]) == (want, int(want > 0))
         got = tuple(p[k] for k in ("chunk_tokens", "work_items", "any_multi"))
-        if force == 1 and want == 2:
+        if split:
+            assert got == (split, int((-(-lens.astype(np.int64) // split)).sum()), 1)
+        elif force == 1 and want == 2:
             assert got == fused_chunk_plan(per_head, lens)
         else:
             assert got == tuple(per_head[k] for k in ("chunk_tokens", "work_items", "any_multi"))

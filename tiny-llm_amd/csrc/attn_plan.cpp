@@ -2,6 +2,7 @@
 #include "attn_plan.h"
 
 #include <algorithm>
+#include <functional>
 #include <climits>
 #include <cstdlib>
 #include <cstring>
@@ -150,7 +151,68 @@ void chunk_items(const int32_t *lens, int n, WorkList &out) {
     }
 }
 
+// Longest-first makespan, in whole tile rounds (one 64-token tile per wave),
+// of the workgroups of items with lengths lens_desc (longest first),
+// per_item workgroups each, on `cus` CUs (one workgroup at a time each),
+// where a workgroup of an item of len tokens takes ceil(ceil(len / 64) /
+// waves_per_head) rounds.  The hardware dispatcher hands the next workgroup
+// to the first CU that frees up, which is this greedy assignment to the least
+// loaded CU; loads are small integers, so the CUs are counted per load level.
+int lpt_rounds(const std::vector<int> &lens_desc, int per_item, int waves_per_head, int cus) {
+    std::vector<int> at(1, std::max(1, cus)); // at[l]: CUs with load l
+    int              lo = 0, top = 0;
+    for (const int len : lens_desc) {
+        const int w = ((len + kPlanTile - 1) / kPlanTile + waves_per_head - 1) / waves_per_head;
+        for (int k = 0; k < per_item; ++k) {
+            while (at[(size_t)lo] == 0) ++lo;
+            --at[(size_t)lo];
+            const int l = lo + w;
+            if ((int)at.size() <= l) at.resize((size_t)l + 1, 0);
+            ++at[(size_t)l];
+            top = std::max(top, l);
+        }
+    }
+    return top;
+}
+
+// Items of chunk c over lens: per entry, full chunks of c tokens and the
+// remainder, longest first.
+std::vector<int> chunk_lengths(const int32_t *lens, int n, int c) {
+    std::vector<int> v;
+    for (int i = 0; i < n; ++i) {
+        for (int t = 0; t < lens[i]; t += c) v.push_back(std::min(c, lens[i] - t));
+    }
+    std::sort(v.begin(), v.end(), std::greater<int>());
+    return v;
+}
+
 } // namespace
+
+int plan_balanced_split(const int32_t *lens, int n, int num_kv_heads, int cus) {
+    if (!lens || n <= 0 || cus <= 0 || num_kv_heads % 2 != 0) return 0;
+    int64_t total = 0;
+    int     mx = 0;
+    for (int i = 0; i < n; ++i) {
+        total += std::max(0, (int)lens[i]);
+        mx = std::max(mx, (int)lens[i]);
+    }
+    if (mx <= kPlanShortLen) return 0;
+    std::vector<int> whole(lens, lens + n);
+    std::sort(whole.begin(), whole.end(), std::greater<int>());
+    const int r0 = lpt_rounds(whole, num_kv_heads, 8, cus);
+    // a CU's share of the head-pair workgroups' tokens, rounded up
+    const int64_t share = (total * (num_kv_heads / 2) + cus - 1) / cus;
+    int64_t       lo = (share + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum;
+    int           best = 0, best_r = r0;
+    for (int64_t c = std::max<int64_t>(lo, kPlanQuantum); c < mx; c += kPlanQuantum) {
+        const int r = lpt_rounds(chunk_lengths(lens, n, (int)c), num_kv_heads / 2, 4, cus);
+        if (r < best_r || (r == best_r && best)) { // shortest makespan, the longest chunk on a tie
+            best_r = r;
+            best = (int)c;
+        }
+    }
+    return best && best_r <= r0 - 1 ? best : 0;
+}
 
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
                     int head_fuse, WorkList &out) {
@@ -162,6 +224,20 @@ void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int f
     out.fused_chunked = false;
     out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
     chunk_items(lens, n, out);
+    // Whole sequences in per-head 8-wave workgroups at most two per CU: a
+    // head-pair chunk plan when it ends at least a tile round sooner
+    // (plan_balanced_split).
+    if (forced_chunk == 0 && head_fuse == 1 && !out.any_multi && out.n_work > 0 &&
+        plan_waves((int64_t)out.n_work * num_kv_heads, cus, 0) == 8) {
+        const int c = plan_balanced_split(lens, n, num_kv_heads, cus);
+        if (c) {
+            out.chunk = c;
+            chunk_items(lens, n, out);
+            out.fused_heads = 2;
+            out.fused_chunked = true;
+            return;
+        }
+    }
     // Head-fused over the chunk items: forced heads per workgroup, or (auto)
     // two heads per 8-wave workgroup where the per-head plan takes 4-wave
     // workgroups -- as many waves per head, two heads' pieces of each row

@@ -64,11 +64,30 @@ int plan_chunk(const int32_t *lens, int n, int num_kv_heads, int uniform_len, in
 bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int head_fuse,
                      WorkList &out);
 
+// Ragged lengths that the chunk rule leaves whole, in per-head 8-wave
+// workgroups at most two per CU, can end far from the ideal: longest-first
+// can only pair each CU's two heads of two sequences (B = 16 MHA sequences
+// of 657..3948 tokens: 11 tile rounds against 8.75 of work per CU).  This is
+// the chunk c of a head-pair chunk plan (2 kv heads per 8-wave workgroup, 4
+// waves per head, each sequence in chunks of c and a remainder) that ends at
+// least one whole tile round (one 64-token tile per wave) sooner in the
+// longest-first schedule of lpt_rounds, or 0: c is a multiple of
+// kPlanQuantum from a CU's share of the head pairs' tokens (shorter chunks
+// only add workgroups, partials and merge work) up to the longest length;
+// among the shortest makespans the longest c.  One round (at head_dim 128 on
+// 256 CUs, every CU streaming 8 tiles, ~9.7 us) pays for the merge launch
+// the split needs (~5 us).  (That B = 16 set, 32 layers, kernel µs per
+// layer: whole sequences 94.2 at 11 rounds; chunks of 2560 88.0 at 10; 2048,
+// 2304, 2816 at 11 rounds 91.6-96.3; 1792 and 3072 at 12 95.3-96.6; 3328 at
+// 13 99.0; 3584 at 14 102.5.)
+int plan_balanced_split(const int32_t *lens, int n, int num_kv_heads, int cus);
+
 // The whole ragged plan (chunk, part_base, work list) for lens[0..n): the
 // head-fused plan when it applies and no chunk is forced, else chunks --
 // head-fused over the chunk items (fused_chunked) when head_fuse forces 2, 4
 // or 8 heads per workgroup, or, for head_fuse 1, with 2 heads per 8-wave
-// workgroup where the per-head plan would take 4-wave workgroups.
+// workgroup where the per-head plan would take 4-wave workgroups or where
+// plan_balanced_split finds a chunk (then of that length).
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,
                     int head_fuse, WorkList &out);
 
