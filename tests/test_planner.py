@@ -113,50 +113,57 @@ def fused_chunk_plan(per_head, lens):
 
 def lpt_rounds_py(items_desc, per_item, waves_per_head, cus):
     """Longest-first list scheduling (a heap of CU loads) of per_item
-    workgroups per item, in whole tile rounds: ceil(ceil(len / 64) /
-    waves_per_head) per workgroup."""
+    workgroups per item, in whole tile rounds (ceil(ceil(len / 64) /
+    waves_per_head) per workgroup): (makespan R, CUs busy in round R)."""
     h = [0] * cus
     for L in items_desc:
         w = -(-(-(-int(L) // 64)) // waves_per_head)
         for _ in range(per_item):
             heapq.heapreplace(h, h[0] + w)
-    return max(h)
+    return max(h), h.count(max(h))
 
 
 def balanced_split_py(lens, hkv, cus):
     """plan_balanced_split restated: the chunk c (a multiple of 256 from a
     CU's share of the head pairs' tokens up to the longest length) whose
-    head-pair plan (hkv / 2 workgroups per item, 4 waves per head) ends at
-    least one tile round before whole sequences in per-head 8-wave
-    workgroups; the longest c among the shortest makespans; else 0."""
+    head-pair plan (hkv / 2 workgroups per item, 4 waves per head) ends before
+    whole sequences in per-head 8-wave workgroups -- fewer tile rounds, or as
+    many with fewer CUs in the last -- the longest c among the soonest; else 0."""
     lens = [int(x) for x in lens]
     if hkv % 2 or max(lens) <= 1024:
         return 0
-    r0 = lpt_rounds_py(sorted(lens, reverse=True), hkv, 8, cus)
+    best, best_r = 0, lpt_rounds_py(sorted(lens, reverse=True), hkv, 8, cus)
     share = -(-(sum(lens) * (hkv // 2)) // cus)
-    best, best_r = 0, r0
     for c in range(max(256, -(-share // 256) * 256), max(lens), 256):
         items = sorted((min(c, L - t) for L in lens for t in range(0, L, c)), reverse=True)
         r = lpt_rounds_py(items, hkv // 2, 4, cus)
         if r < best_r or (r == best_r and best):
             best, best_r = c, r
-    return best if best and best_r <= r0 - 1 else 0
+    return best
 
 
 def test_balanced_split_rounds_examples(tl):
-    """cfg2's lengths (16 MHA sequences): whole sequences take 11 tile rounds,
-    head pairs in chunks of 2048, 2304 or 2816 also 11, of 2560 10 (the
-    kernel measured 88.0 us per layer against 91.6-96.3 for the others), so
-    2560 is the split.  Uniform lengths and short ones never split."""
+    """cfg2's lengths (16 MHA sequences), (tile rounds, CUs in the last):
+    whole sequences (11, 32); head pairs in chunks of 2304 (11, 32), 2560
+    (10, 112), 2816 (11, 80) -- the kernel measured 92.6, 88.0 and 91.6 us
+    per layer against 94.2, and only the 2560 split beat whole sequences end
+    to end -- so 2560 is the split.  18 steps later (lengths + 18) whole
+    sequences are (11, 64) and 2560 (11, 16): still the split (measured over
+    40 steps: 2913 us per step with it throughout, 2992 without).  Uniform
+    lengths and short ones never split."""
     lens, hkv = cases()["cfg2"]
     ls = [int(x) for x in lens]
-    assert lpt_rounds_py(sorted(ls, reverse=True), 32, 8, CUS) == 11
-    for c, r in ((2048, 11), (2304, 11), (2560, 10), (2816, 11), (3072, 12), (3584, 14)):
+    assert lpt_rounds_py(sorted(ls, reverse=True), 32, 8, CUS) == (11, 32)
+    for c, r in ((2304, (11, 32)), (2560, (10, 112)), (2816, (11, 80)), (3072, (12, 80))):
         items = sorted((min(c, L - t) for L in ls for t in range(0, L, c)), reverse=True)
         assert lpt_rounds_py(items, 16, 4, CUS) == r, c
     assert balanced_split_py(ls, 32, CUS) == 2560
-    p = tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="auto")
-    assert (p["chunk_tokens"], p["head_fused"], p["fused_chunked"]) == (2560, 2, 1)
+    later = [L + 18 for L in ls]
+    assert lpt_rounds_py(sorted(later, reverse=True), 32, 8, CUS) == (11, 64)
+    assert balanced_split_py(later, 32, CUS) == 2560
+    for grow in (0, 18, 39):
+        p = tl.attn_plan(lens + grow, hkv, num_cus=CUS, head_fuse="auto")
+        assert (p["chunk_tokens"], p["head_fused"], p["fused_chunked"]) == (2560, 2, 1), grow
     # the per-head-only plan (head_fuse off) and a forced chunk keep their chunks
     assert tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="off")["chunk_tokens"] == 4096
     assert tl.attn_plan(lens, hkv, num_cus=CUS, head_fuse="auto", forced_chunk=3072)["chunk_tokens"] == 3072

@@ -151,15 +151,19 @@ void chunk_items(const int32_t *lens, int n, WorkList &out) {
     }
 }
 
-// Longest-first makespan, in whole tile rounds (one 64-token tile per wave),
+// Longest-first schedule, in whole tile rounds (one 64-token tile per wave),
 // of the workgroups of items with lengths lens_desc (longest first),
 // per_item workgroups each, on `cus` CUs (one workgroup at a time each),
 // where a workgroup of an item of len tokens takes ceil(ceil(len / 64) /
-// waves_per_head) rounds.  The hardware dispatcher hands the next workgroup
-// to the first CU that frees up, which is this greedy assignment to the least
-// loaded CU; loads are small integers, so the CUs are counted per load level.
-int lpt_rounds(const std::vector<int> &lens_desc, int per_item, int waves_per_head, int cus) {
-    std::vector<int> at(1, std::max(1, cus)); // at[l]: CUs with load l
+// waves_per_head) rounds: its makespan R and the number of CUs still busy in
+// round R, as the key R * (cus + 1) + busy (smaller: ends sooner; with as
+// many rounds, fewer CUs share the last one).  The hardware dispatcher hands
+// the next workgroup to the first CU that frees up, which is this greedy
+// assignment to the least loaded CU; loads are small integers, so the CUs are
+// counted per load level.
+int64_t lpt_rounds(const std::vector<int> &lens_desc, int per_item, int waves_per_head, int cus) {
+    cus = std::max(1, cus);
+    std::vector<int> at(1, cus); // at[l]: CUs with load l
     int              lo = 0, top = 0;
     for (const int len : lens_desc) {
         const int w = ((len + kPlanTile - 1) / kPlanTile + waves_per_head - 1) / waves_per_head;
@@ -172,7 +176,7 @@ int lpt_rounds(const std::vector<int> &lens_desc, int per_item, int waves_per_he
             top = std::max(top, l);
         }
     }
-    return top;
+    return (int64_t)top * (cus + 1) + at[(size_t)top];
 }
 
 // Items of chunk c over lens: per entry, full chunks of c tokens and the
@@ -199,19 +203,20 @@ int plan_balanced_split(const int32_t *lens, int n, int num_kv_heads, int cus) {
     if (mx <= kPlanShortLen) return 0;
     std::vector<int> whole(lens, lens + n);
     std::sort(whole.begin(), whole.end(), std::greater<int>());
-    const int r0 = lpt_rounds(whole, num_kv_heads, 8, cus);
-    // a CU's share of the head-pair workgroups' tokens, rounded up
+    const int64_t r0 = lpt_rounds(whole, num_kv_heads, 8, cus);
+    // a CU's share of the head pairs' tokens, rounded up
     const int64_t share = (total * (num_kv_heads / 2) + cus - 1) / cus;
     int64_t       lo = (share + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum;
-    int           best = 0, best_r = r0;
+    int           best = 0;
+    int64_t       best_r = r0;
     for (int64_t c = std::max<int64_t>(lo, kPlanQuantum); c < mx; c += kPlanQuantum) {
-        const int r = lpt_rounds(chunk_lengths(lens, n, (int)c), num_kv_heads / 2, 4, cus);
-        if (r < best_r || (r == best_r && best)) { // shortest makespan, the longest chunk on a tie
+        const int64_t r = lpt_rounds(chunk_lengths(lens, n, (int)c), num_kv_heads / 2, 4, cus);
+        if (r < best_r || (r == best_r && best)) { // ends soonest; the longest chunk on a tie
             best_r = r;
             best = (int)c;
         }
     }
-    return best && best_r <= r0 - 1 ? best : 0;
+    return best; // nonzero only when it ends before the whole sequences
 }
 
 void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int forced_chunk,

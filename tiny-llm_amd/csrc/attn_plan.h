@@ -67,19 +67,21 @@ bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int 
 // Ragged lengths that the chunk rule leaves whole, in per-head 8-wave
 // workgroups at most two per CU, can end far from the ideal: longest-first
 // can only pair each CU's two heads of two sequences (B = 16 MHA sequences
-// of 657..3948 tokens: 11 tile rounds against 8.75 of work per CU).  This is
+// of 657..3948 tokens: 11 tile rounds against 8.35 of work per CU).  This is
 // the chunk c of a head-pair chunk plan (2 kv heads per 8-wave workgroup, 4
-// waves per head, each sequence in chunks of c and a remainder) that ends at
-// least one whole tile round (one 64-token tile per wave) sooner in the
-// longest-first schedule of lpt_rounds, or 0: c is a multiple of
-// kPlanQuantum from a CU's share of the head pairs' tokens (shorter chunks
-// only add workgroups, partials and merge work) up to the longest length;
-// among the shortest makespans the longest c.  One round (at head_dim 128 on
-// 256 CUs, every CU streaming 8 tiles, ~9.7 us) pays for the merge launch
-// the split needs (~5 us).  (That B = 16 set, 32 layers, kernel µs per
-// layer: whole sequences 94.2 at 11 rounds; chunks of 2560 88.0 at 10; 2048,
-// 2304, 2816 at 11 rounds 91.6-96.3; 1792 and 3072 at 12 95.3-96.6; 3328 at
-// 13 99.0; 3584 at 14 102.5.)
+// waves per head, each sequence in chunks of c and a remainder) that ends
+// sooner in the longest-first schedule of lpt_rounds -- in fewer whole tile
+// rounds (one 64-token tile per wave), or in as many with fewer CUs busy in
+// the last one -- or 0: c is a multiple of kPlanQuantum from a CU's share of
+// the head pairs' tokens (shorter chunks only add workgroups, partials and
+// merge work) up to the longest length; among the soonest the longest c.
+// At head_dim 128 on 256 CUs a round (every CU streaming 8 tiles) takes
+// ~9.7 us, the merge launch the split needs ~5 us.  (That B = 16 set, 32
+// layers, kernel us per layer, (rounds, CUs in the last): whole sequences
+// 94.2 (11, 32); chunks of 2560 88.0 (10, 112); 2304 92.6 (11, 32); 2816
+// 91.6 (11, 80); 3072 95.3 (12, 80); 3328 99.0; 3584 102.5; end to end the
+// 2560 split is the one ahead of whole sequences, also 18 steps later, when
+// it is (11, 16) against (11, 64).)
 int plan_balanced_split(const int32_t *lens, int n, int num_kv_heads, int cus);
 
 // The whole ragged plan (chunk, part_base, work list) for lens[0..n): the
