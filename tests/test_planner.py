@@ -125,7 +125,8 @@ def lpt_rounds_py(items_desc, per_item, waves_per_head, cus):
 
 def balanced_split_py(lens, hkv, cus):
     """plan_balanced_split restated: the chunk c (a multiple of 256 from a
-    CU's share of the head pairs' tokens up to the longest length) whose
+    CU's share of the head pairs' tokens up to the longest length, at most 32
+    of them, evenly strided) whose
     head-pair plan (hkv / 2 workgroups per item, 4 waves per head) ends before
     whole sequences in per-head 8-wave workgroups -- fewer tile rounds, or as
     many with fewer CUs in the last -- the longest c among the soonest; else 0."""
@@ -134,7 +135,9 @@ def balanced_split_py(lens, hkv, cus):
         return 0
     best, best_r = 0, lpt_rounds_py(sorted(lens, reverse=True), hkv, 8, cus)
     share = -(-(sum(lens) * (hkv // 2)) // cus)
-    for c in range(max(256, -(-share // 256) * 256), max(lens), 256):
+    lo = max(256, -(-share // 256) * 256)
+    stride = max(256, -(-((max(lens) - lo) // 32) // 256) * 256)  # at most 32 candidates
+    for c in range(lo, max(lens), stride):
         items = sorted((min(c, L - t) for L in lens for t in range(0, L, c)), reverse=True)
         r = lpt_rounds_py(items, hkv // 2, 4, cus)
         if r < best_r or (r == best_r and best):

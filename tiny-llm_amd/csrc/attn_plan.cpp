@@ -207,9 +207,13 @@ int plan_balanced_split(const int32_t *lens, int n, int num_kv_heads, int cus) {
     // a CU's share of the head pairs' tokens, rounded up
     const int64_t share = (total * (num_kv_heads / 2) + cus - 1) / cus;
     int64_t       lo = (share + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum;
+    lo = std::max<int64_t>(lo, kPlanQuantum);
+    // at most kPlanSplitCandidates chunk lengths, evenly strided (host cost)
+    const int64_t stride = std::max<int64_t>(
+        kPlanQuantum, ((mx - lo) / kPlanSplitCandidates + kPlanQuantum - 1) / kPlanQuantum * kPlanQuantum);
     int           best = 0;
     int64_t       best_r = r0;
-    for (int64_t c = std::max<int64_t>(lo, kPlanQuantum); c < mx; c += kPlanQuantum) {
+    for (int64_t c = lo; c < mx; c += stride) {
         const int64_t r = lpt_rounds(chunk_lengths(lens, n, (int)c), num_kv_heads / 2, 4, cus);
         if (r < best_r || (r == best_r && best)) { // ends soonest; the longest chunk on a tie
             best_r = r;
@@ -230,7 +234,7 @@ void plan_work_list(const int32_t *lens, int n, int num_kv_heads, int cus, int f
     out.chunk = plan_chunk(lens, n, num_kv_heads, 0, cus, forced_chunk);
     chunk_items(lens, n, out);
     // Whole sequences in per-head 8-wave workgroups at most two per CU: a
-    // head-pair chunk plan when it ends at least a tile round sooner
+    // head-pair chunk plan when its longest-first schedule ends sooner
     // (plan_balanced_split).
     if (forced_chunk == 0 && head_fuse == 1 && !out.any_multi && out.n_work > 0 &&
         plan_waves((int64_t)out.n_work * num_kv_heads, cus, 0) == 8) {

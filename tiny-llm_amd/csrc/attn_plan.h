@@ -18,6 +18,7 @@ constexpr int kPlanShortLen = 2 * 8 * kPlanTile; // never split lengths up to th
 constexpr int kPlanFusedWaves = 8;             // waves of a head-fused workgroup
 constexpr int kPlanFusedMaxItems = 8;          // head-fused items per entry, at most
 constexpr int kFusedChunkNum = 3, kFusedChunkDen = 2; // chunk scale of head-fused chunk items
+constexpr int kPlanSplitCandidates = 32;       // chunk lengths plan_balanced_split tries, at most
 
 // Host side of a ragged plan: chunk length, per-entry partial-row bases and
 // the (entry, chunk) work list in longest-first order, so the hardware
@@ -74,7 +75,9 @@ bool plan_head_fused(const int32_t *lens, int n, int num_kv_heads, int cus, int 
 // rounds (one 64-token tile per wave), or in as many with fewer CUs busy in
 // the last one -- or 0: c is a multiple of kPlanQuantum from a CU's share of
 // the head pairs' tokens (shorter chunks only add workgroups, partials and
-// merge work) up to the longest length; among the soonest the longest c.
+// merge work) up to the longest length, at most kPlanSplitCandidates of them
+// (evenly strided by a multiple of kPlanQuantum); among the soonest the
+// longest c.
 // At head_dim 128 on 256 CUs a round (every CU streaming 8 tiles) takes
 // ~9.7 us, the merge launch the split needs ~5 us.  (That B = 16 set, 32
 // layers, kernel us per layer, (rounds, CUs in the last): whole sequences
