@@ -95,6 +95,25 @@ def test_noalloc_head_fused_twice_then_smaller(tl, orc):
         run_pair(tl, orc, rng, lens, Hq, Hkv, D)
 
 
+def test_noalloc_balanced_split_then_smaller(tl, orc):
+    """Ragged MHA lengths whose whole sequences would run in per-head 8-wave
+    workgroups two per CU take the planner's balanced split (head pairs in
+    chunks, partials in the scratch, the merge launch); then a smaller call
+    whose sequences stay whole."""
+    rng = np.random.default_rng(20261205)
+    Hq, Hkv, D = 16, 16, 128
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    lens1 = rng.integers(300, 2000, 32).astype(np.int32)
+    p1 = tl.attn_plan(lens1, Hkv, num_cus=ncu, with_rows=False, head_fuse="current")
+    assert (p1["chunk_tokens"], p1["head_fused"], p1["fused_chunked"], p1["any_multi"]) == (1280, 2, 1, 1) \
+        or ncu != 256
+    run_pair(tl, orc, rng, lens1, Hq, Hkv, D)
+    lens2 = np.array([700, 650, 600, 500], dtype=np.int32)
+    p2 = tl.attn_plan(lens2, Hkv, num_cus=ncu, with_rows=False, head_fuse="current")
+    assert p2["any_multi"] == 0
+    run_pair(tl, orc, rng, lens2, Hq, Hkv, D)
+
+
 def test_noalloc_rejects_calls_beyond_the_scratch(tl, monkeypatch):
     """400 split items of 64 heads x (256 + 2) fp32 need 26 MB of partials,
     more than the 16 MiB array: rejected with a clear error, nothing runs."""
