@@ -6,7 +6,8 @@
 //
 // MFMA path (K % 32 == 0, gs in {32, 64, 128, 256, 512}, every segment's
 // N % 16 == 0), two kernels, each for both weight layouts (packed: the
-// launch_w8a16_pack layout, B fragments of 8 bytes per lane; reference:
+// launch_w8a16_pack layout, B fragments of 8 bytes per lane, two k steps per
+// 16-byte lane load; reference:
 // [K][N] row-major, staged in LDS and read as B fragments by the transposing
 // ds_read_b64_tr_b8).  Both layouts give the same fragments and the same
 // summation order, hence the same bits.  The int8 weights become fp16
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(256, ACC ? 2 : 3) void w8a16_sk_kernel(GemmArgs a) 
 // rows, two MFMA row blocks).  K is cut into 128-row chunks (4 k steps); wave
 // w takes chunks w, w + 8, w + 16, w + 24 through a two-deep register ring:
 // x in whole 128-byte lines (4 rows x 256 bytes per load) and packed W
-// fragments (8 bytes per lane) load into registers, so the compiler's own
+// fragments (16 bytes per lane: two k steps) load into registers, so the compiler's own
 // load counters order each use after exactly the data it needs, and the next
 // chunks' loads are in flight while one is multiplied.  (The LDS DMA load
 // would not do: this compiler waits for every outstanding load before the

@@ -30,7 +30,9 @@ void w8a16_matmul_residual(const half *input, const int8_t *weight, const half *
 
 // One-time repack of weight [K][N] int8 (K % 32 == 0, N % 16 == 0) into the
 // MFMA-fragment layout the packed entry points read (K*N bytes, device to
-// device): each 16-column x 32-row fragment is 512 contiguous bytes.
+// device): the B fragments of 16 columns x 32 rows, 8 bytes per lane, two k
+// steps' fragments interleaved in 1024 contiguous bytes (16 per lane), as
+// offset-binary bytes (w ^ 0x80).
 void w8a16_pack(const int8_t *weight, int K, int N, int8_t *packed, hipStream_t stream = 0);
 
 } // namespace kernels
