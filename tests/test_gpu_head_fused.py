@@ -5,7 +5,9 @@ pieces of each token row at once, and a sequence's work items interleave its
 
 Ragged lengths keep the chunk plan's items (longest first), with 2 heads per
 workgroup where per-head workgroups would have 4 waves, split sequences in
-chunks 3/2 as long.
+chunks 3/2 as long; where per-head workgroups would have 8 waves, at most two
+per CU, with whole sequences, the planner's balanced split (2 heads per
+workgroup, the longest sequences in chunks).
 
 Checked for H = 2, 4 and 8 and the planner's own choice, every group size,
 contiguous and paged caches, one to eight interleaved items per sequence and
@@ -106,6 +108,30 @@ def test_head_fused_chunk_items_decode_step(tl, orc, head_fuse, run):
         assert plan["chunk_tokens"] >= per_head["chunk_tokens"]
         assert plan["work_items"] <= per_head["work_items"]
     decode_step_checks(tl, orc, head_fuse, rng, setting, Hkv, G, paged, ctx, plan)
+
+
+# Ragged lengths whose whole sequences would run in per-head 8-wave
+# workgroups at most two per CU: the planner's balanced split (head pairs in
+# chunks, split sequences merged).  (kv heads, batch, context range, group,
+# paged)
+BALANCED = [(16, 32, (300, 2000), 1, False), (16, 32, (300, 2000), 2, True),
+            (32, 16, (512, 4096), 1, True), (8, 60, (300, 2000), 8, True)]
+
+
+@pytest.mark.parametrize("run", BALANCED, ids=[
+    "hkv{}-b{}-g{}-{}".format(r[0], r[1], r[3], "paged" if r[4] else "slots") for r in BALANCED])
+def test_balanced_split_decode_step(tl, orc, head_fuse, run):
+    Hkv, B, (lo, hi), G, paged = run
+    rng = np.random.default_rng(zlib.crc32(repr(run).encode()))
+    ctx = rng.integers(lo, hi + 1, B)
+    lens = (ctx + 1).astype(np.int32)
+    per_head = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse="off")
+    plan = tl.attn_plan(lens, Hkv, num_cus=cus(), with_rows=True, head_fuse="auto")
+    if cus() == 256:
+        assert (per_head["waves"], per_head["any_multi"]) == (8, 0)
+        assert (plan["head_fused"], plan["fused_chunked"], plan["any_multi"]) == (2, 1, 1)
+        assert plan["chunk_tokens"] < per_head["chunk_tokens"]
+    decode_step_checks(tl, orc, head_fuse, rng, 0, Hkv, G, paged, ctx, plan)
 
 
 def decode_step_checks(tl, orc, head_fuse, rng, setting, Hkv, G, paged, ctx, plan):
