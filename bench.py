@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="prefill: new tokens per prompt")
     ap.add_argument("--prefill-prefix", type=int, default=0,
                     help="prefill: tokens already cached per prompt (chunked continuation)")
+    ap.add_argument("--prefill-heads", default="32,8,128",
+                    help="prefill: q heads, kv heads, head_dim (default Llama-3-8B's)")
     ap.add_argument("--settle-ms", type=float, default=100.0,
                     help="prefill, project, oproj: untimed back-to-back calls for about this "
                          "long before the timed ones, so the kernels are timed at the clock the "
@@ -585,7 +587,7 @@ def churn(args, tl, torch, workloads, np):
 
 def prefill_bench(args, tl, torch, np):
     """Prefill into the cache at Llama-3-8B attention shapes (32 q / 8 kv
-    heads, head_dim 128): --prefill-seqs prompts of --prefill-tokens new tokens
+    heads, head_dim 128; --prefill-heads for others): --prefill-seqs prompts of --prefill-tokens new tokens
     on top of --prefill-prefix cached ones, one layer.  A step is
     PrefillBatch.prepare + run: one launch that attends every new token
     causally over its sequence's cache (keys at or past the write position
@@ -594,8 +596,9 @@ def prefill_bench(args, tl, torch, np):
     rewound after each step (lengths are not committed), so every step
     repeats the same work."""
     import workloads
-    Hq, Hkv, D = 32, 8, 128
+    Hq, Hkv, D = (int(x) for x in args.prefill_heads.split(","))
     nseq, n, p0 = args.prefill_seqs, args.prefill_tokens, args.prefill_prefix
+    heads_tag = "" if (Hq, Hkv, D) == (32, 8, 128) else f"_h{Hq}x{Hkv}d{D}"
     K = args.steps or 20
     dev = torch.device("cuda", 0)
     stream = torch.cuda.current_stream().cuda_stream
@@ -669,13 +672,13 @@ def prefill_bench(args, tl, torch, np):
                           "follows the shader clock, which ramps under sustained load"},
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": f"synthetic: Q/K/V ~ N(0,1) ({GEN_NOTE})",
-        "config": {"workload": f"llama3_8b_prefill_{nseq}x{n}" + (f"_prefix{p0}" if p0 else ""),
+        "config": {"workload": f"llama3_8b_prefill_{nseq}x{n}" + (f"_prefix{p0}" if p0 else "") + heads_tag,
                    "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "prompts": nseq,
                    "new_tokens": n, "cached_prefix": p0, "attended_keys": keys,
                    "workgroup_waves": waves},
         "kernels_us": {"attn_prefill": round(a_avg * 1e3, 2), "kv_append": round(c_avg * 1e3, 2)},
         "host_wall_us_per_step": round(t_wall / K * 1e6, 2),
-        "roofline": {"kernel": f"attn_prefill_kernel<128,4,contiguous,{waves} waves>", "bound": "mfma",
+        "roofline": {"kernel": f"attn_prefill_kernel<{D},{Hq // Hkv},contiguous,{waves} waves>", "bound": "mfma",
                      "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": None},
         "cpu_baseline": None,

@@ -298,7 +298,8 @@ int  tl_kv_prefill_commit(tl_kv_prefill *p);
 
 /* Waves per prefill-attention workgroup, process-wide: 0 = auto, 4 or 8
  * (8: one 256-row workgroup per CU; 4: two 128-row workgroups per CU, one's
- * start-up under the other's tiles).  Auto takes 4 at head_dim 128 when the
+ * start-up under the other's tiles).  Auto takes 4 at head_dim 64 (three
+ * workgroups per CU), 8 at head_dim 32, and at head_dim 128 4 when the
  * 8-wave tiling gives every CU at least 3 work items ((entry, query tile) x
  * kv heads) that attend at most 800 keys on average, else 8; head_dim 256 is
  * always 4.  Initial value from the environment variable TL_PREFILL_WAVES

@@ -513,8 +513,11 @@ def test_prefill_waves_rule_boundaries_and_settings(tl):
         assert tl.prefill_plan_waves([0] * 4, [1536] * 4, 32, 8, 128, CUS + 1) == 8
         # a cached prefix long enough to lift the mean past 800 keys
         assert tl.prefill_plan_waves([64] * 4, [1536] * 4, 32, 8, 128, CUS) == 8
-        # auto is measured at head_dim 128 only; 256 has the 4-wave form only
-        assert tl.prefill_plan_waves([0] * 16, [512] * 16, 32, 8, 64, CUS) == 8
+        # head_dim 64: always 4 (three workgroups per CU); 32: 8; 256 has the
+        # 4-wave form only
+        for n, p0 in ((512, 0), (8192, 0), (512, 1024)):
+            assert tl.prefill_plan_waves([p0] * 16, [n] * 16, 32, 8, 64, CUS) == 4
+            assert tl.prefill_plan_waves([p0] * 16, [n] * 16, 32, 8, 32, CUS) == 8
         assert tl.prefill_plan_waves([0] * 16, [512] * 16, 32, 8, 256, CUS) == 4
         for forced in (4, 8):
             tl.set_prefill_waves(forced)

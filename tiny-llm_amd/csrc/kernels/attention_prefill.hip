@@ -602,6 +602,7 @@ int waves_rule(int D, int64_t items, int64_t keys, int Hkv, int cus) {
     if (D > 128) return 4;
     const int setting = prefill_waves_setting();
     if (setting == 4 || setting == 8) return setting;
+    if (D == 64) return 4; // three 4-wave workgroups per CU against one 8-wave one
     if (D != 128 || items <= 0) return 8;
     const bool many = items * Hkv >= (int64_t)kPrefill4wItemsPerCU * std::max(1, cus);
     const bool short_items = keys <= (int64_t)kPrefill4wMeanKeys * items;

@@ -41,7 +41,11 @@ inline int prefill_block_tokens(int D, int G, int waves) { return prefill_rows(D
 
 // Waves per workgroup of a prefill launch over `entries`, with Hkv kv heads
 // (the grid is items x Hkv) on `cus` CUs: the process setting when it forces
-// 4 or 8 (head_dim <= 128; head_dim 256 is always 4); else, at head_dim 128,
+// 4 or 8 (head_dim <= 128; head_dim 256 is always 4); else 4 at head_dim 64
+// (its ~144 VGPRs per wave let a CU run three 4-wave workgroups but only one
+// 8-wave one: 4 waves measured 6-24% faster on every shape tried, 32 / 8 and
+// 32 / 4 heads, prompts of 256 to 8192 tokens, with and without a cached
+// prefix), 8 at head_dim 32 (mixed: -16% to +28%); at head_dim 128,
 // 4 when the 8-wave tiling gives every CU at least kPrefill4wItemsPerCU
 // items and they attend at most kPrefill4wMeanKeys keys on average (many
 // short items: a workgroup's start-up -- work record, q, first tile -- is a
