@@ -236,10 +236,21 @@ struct RowAddr {
     }
 };
 
+// A global-memory pointer that is the same in every lane, moved to scalar
+// registers (its arithmetic then runs on the scalar unit); typed as global so
+// that the loads through it stay global loads, not flat ones.
+typedef const __attribute__((address_space(1))) char *gptr;
+__device__ __forceinline__ gptr uniform_ptr(const char *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<gptr>(((uint64_t)hi << 32) | lo);
+}
+
 // Streaming load of cache bytes that are read once per call: the
 // non-temporal hint keeps them from displacing reusable lines in L2 / MALL.
-__device__ __forceinline__ uint4 ld16nt(const char *p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+__device__ __forceinline__ uint4 ld16nt(gptr p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
@@ -707,6 +718,16 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     const int g = HF ? hb * HPW + wave % H1 : blockIdx.x - item * a.Hkv;
     int       b, c, S, nch, widx, row;
     ATTN_WORK_ITEM(a, item, b, c, S, nch, widx, row);
+    // One value per workgroup; the device-array path reads them with vector
+    // loads (the kernel's stores could alias them, which rules out scalar
+    // loads), so they are moved to scalar registers here: the tile loop and
+    // the token addresses then run on the scalar unit.
+    b = __builtin_amdgcn_readfirstlane(b);
+    c = __builtin_amdgcn_readfirstlane(c);
+    S = __builtin_amdgcn_readfirstlane(S);
+    nch = __builtin_amdgcn_readfirstlane(nch);
+    widx = __builtin_amdgcn_readfirstlane(widx);
+    row = __builtin_amdgcn_readfirstlane(row);
     // HF: the nch items of an entry interleave its tiles in slices: slice s
     // of item c takes tiles u, u + nch * NS, ... with u = c * NS + s, instead
     // of contiguous chunks.
@@ -787,27 +808,40 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
     // quarter, known at compile time; tokens past the end are clamped to the
     // last valid one, which lies in the same quarter or in the block of the
     // tile's last token, the block that quarters past the end name.
+    // The clamp runs on the scalar unit: a step's TPI tokens from ss (a
+    // multiple of TPI) lie in one block, so with ssc = min(ss, lim) the row
+    // of token min(ss + r, lim) sits min(r * tok_bytes, (lim - ssc) *
+    // tok_bytes) bytes past row ssc -- one vector min and add per load over
+    // a wave-uniform base (the work item's values are scalar, see above).
     using Quarters = typename RowAddr<PAGED>::Quarters;
+    const uint32_t rtb = (uint32_t)r * ra.tok_bytes, p16 = 16u * (uint32_t)p;
+    const gptr     kbu = uniform_ptr(ra.kbase), vbu = uniform_ptr(ra.vbase);
+    auto step_ptr = [&](gptr base, int64_t qo, int ss, int lim) __attribute__((always_inline)) {
+        const int      ssc = min(ss, lim);
+        const uint32_t lim_off = (uint32_t)(lim - ssc) * ra.tok_bytes;
+        return base + qo + ra.in_block(ssc) + (min(rtb, lim_off) + p16);
+    };
+    // (Tile starts and ends are wave-uniform; readfirstlane keeps them in
+    // scalar registers where register pressure would move them to vector
+    // ones.)
     auto kload = [&](int ts, int tend, int bi, uint4(&buf)[KB], const Quarters &q) {
+        const int tb = __builtin_amdgcn_readfirstlane(t0 + ts);
+        const int lim = __builtin_amdgcn_readfirstlane(t0 + tend - 1);
 #pragma unroll
         for (int u = 0; u < KB; ++u) {
-            const int   ss = t0 + ts + (bi * KB + u) * TPI; // step start (global token)
-            const int   lim = t0 + tend - 1;
-            const int   t = ss + r < lim ? ss + r : lim;
-            const char *base = ra.kbase + q.o[(bi * KB + u) * TPI / 16];
-            buf[u] = ld16nt(base + ra.in_block(t) + 16 * p);
+            const int ss = tb + (bi * KB + u) * TPI; // step start (global token)
+            buf[u] = ld16nt(step_ptr(kbu, q.o[(bi * KB + u) * TPI / 16], ss, lim));
         }
     };
     auto vload = [&](int ts, int tend, int bj, uint4(&bufa)[VB], uint4(&bufb)[VB], const Quarters &q) {
+        const int tb = __builtin_amdgcn_readfirstlane(t0 + ts);
+        const int lim = __builtin_amdgcn_readfirstlane(t0 + tend - 1);
 #pragma unroll
         for (int u = 0; u < VB; ++u) {
             const int ob = (bj * VB + u) * 2 * TPI; // pair block start in the tile
-            const int bs = t0 + ts + ob;
-            const int lim = t0 + tend - 1;
-            const int ta = bs + r < lim ? bs + r : lim;
-            const int tb = bs + TPI + r < lim ? bs + TPI + r : lim;
-            bufa[u] = ld16nt(ra.vbase + q.o[ob / 16] + ra.in_block(ta) + 16 * p);
-            bufb[u] = ld16nt(ra.vbase + q.o[(ob + TPI) / 16] + ra.in_block(tb) + 16 * p);
+            const int bs = tb + ob;
+            bufa[u] = ld16nt(step_ptr(vbu, q.o[ob / 16], bs, lim));
+            bufb[u] = ld16nt(step_ptr(vbu, q.o[(ob + TPI) / 16], bs + TPI, lim));
         }
     };
     // Quarter block ids of the wave's tile ti (paged views only).
@@ -1379,17 +1413,32 @@ void launch_mma_d(const AttnArgs &args, int n_work, int Hkv, int G, bool paged, 
     }
 }
 
+// Dynamic LDS of a decode launch: the kernel's own, raised for 8-wave
+// workgroups past half of a CU's 160 KB, so that a CU holds one of them at a
+// time -- the planner's model (plan_waves, plan_balanced_split: 8-wave
+// workgroups one per CU, in turn).  Otherwise the occupancy would follow the
+// register count: a kernel under 128 VGPRs fits two 8-wave workgroups on a CU,
+// and a ragged plan then shares one CU's bandwidth between two items that its
+// schedule runs one after the other (head_dim 128, group 1, 127 VGPRs: cfg2's
+// balanced split 92 -> 108 us per layer).
+constexpr int kCuLdsBytes = 160 * 1024;
+template <int NW, int OWN>
+constexpr int decode_lds_bytes() {
+    return NW == 8 && OWN <= kCuLdsBytes / 2 ? kCuLdsBytes / 2 + 4096 : OWN;
+}
+
 template <int D, int G, bool PAGED, bool MFMA, int NW, int HPW = 0, int VBO = 0>
 void launch_one(const AttnArgs &args, int n_work, int Hkv, hipStream_t stream) {
     using SM = Smem<D, G, MFMA, NW>;
+    constexpr int         lds = decode_lds_bytes<NW, SM::kBytes>();
     auto                 *fn = attn_decode_kernel<D, G, PAGED, MFMA, NW, HPW, VBO>;
     static std::once_flag once;
     std::call_once(once, [&] {
         HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, SM::kBytes));
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     });
     const unsigned per = (unsigned)(Hkv / (HPW ? HPW : 1));
-    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * per), dim3(NW * 64), SM::kBytes, stream, args);
+    hipLaunchKernelGGL(fn, dim3((unsigned)n_work * per), dim3(NW * 64), lds, stream, args);
 }
 
 // Chunk items of 2 heads per workgroup (ragged plans) load V 16 tokens a
