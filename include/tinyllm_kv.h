@@ -387,6 +387,18 @@ int tl_attn_get_waves(void);
 int tl_attn_set_head_fuse(int mode);
 int tl_attn_get_head_fuse(void);
 
+/* Where a multi-chunk decode plan merges its chunks' partials, process-wide:
+ * 0 = in a second launch (attn_merge_kernel; default), 1 = inside the
+ * attention launch (the workgroup that completes a sequence's last chunk of
+ * a kv-head block merges them, after device-scope fences; measured slower
+ * than the second launch on every plan timed).  Both give the same bits.
+ * Plans with an empty sequence, and tl_attn_decode_gqa_noalloc, always take
+ * the second launch.  Initial value from the environment variable
+ * TL_ATTN_MERGE ("fused" = 1).  No reference counterpart (the reference's
+ * decode kernel is one workgroup per (sequence, head), attention.cu:114-128). */
+int tl_attn_set_fused_merge(int on);
+int tl_attn_get_fused_merge(void);
+
 /* The launch plan of the decode attention entry points (tl_kv_batch_attention,
  * tl_kv_batch_decode, tl_attn_decode_gqa) for attended lengths
  * seq_lens[0..n) at head_dim (32, 64, 128 or 256) on a device of num_cus

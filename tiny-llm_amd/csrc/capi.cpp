@@ -552,6 +552,15 @@ int tl_attn_set_head_fuse(int mode) {
 
 int tl_attn_get_head_fuse(void) { return tiny_llm::detail::head_fuse(); }
 
+int tl_attn_set_fused_merge(int on) {
+    if (on != 0 && on != 1)
+        return fail(TL_ERR_INVALID, "tl_attn_set_fused_merge: on must be 0 (second launch) or 1 (in the launch)");
+    tiny_llm::detail::set_fused_merge(on != 0);
+    return TL_OK;
+}
+
+int tl_attn_get_fused_merge(void) { return tiny_llm::detail::fused_merge_enabled() ? 1 : 0; }
+
 int tl_attn_plan(const int32_t *seq_lens, int n, int num_kv_heads, int head_dim, int num_cus,
                  int forced_chunk, int waves_setting, int head_fuse, int with_rows,
                  tl_attn_plan_info *info, int32_t *part_base, int32_t *work) {

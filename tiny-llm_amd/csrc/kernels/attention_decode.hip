@@ -129,7 +129,12 @@ struct AttnArgs {
     int           Hkv;
     float         scale_log2; // scale * log2(e)
     InlineMeta    meta;       // used when meta.n > 0
+    // Merge in the launch: one counter per (entry, kv head), zero between
+    // launches; the workgroup that completes an entry's last chunk of a head
+    // block merges its partials (fused_merge).  Null: attn_merge_kernel does.
+    int          *counters;
 };
+static_assert(sizeof(AttnArgs) <= 4096, "kernel arguments");
 
 // Work item `item` of the launch: entry b, chunk c of nch, attended length
 // S, partial row widx and cache row (slot) row, from the inline metadata
@@ -668,6 +673,64 @@ struct MfmaScorer {
     }
 };
 
+// Merge of an entry's chunk partials inside the attention launch, for the R
+// query heads row0 .. row0 + R - 1 (the kv heads of one workgroup).  Every
+// chunk's workgroup calls this after writing its partials.  Each wave waits
+// for its own stores; after the workgroup barrier one thread releases them at
+// device scope (the chunks run on any XCD, whose L2s are not coherent with
+// each other: the fence writes this XCD's L2 back) and counts the chunk in
+// *counter.  The thread that counts the last one acquires (invalidating this
+// CU's and XCD's caches) before the barrier that lets its workgroup read the
+// other chunks' partials and write the output rows; it resets the counter,
+// so it is zero again for the next launch.  One device-scope fence per
+// workgroup, two for the merging one (a fence in every wave made the launch
+// 1.7x longer).  No workgroup waits for another.  Off by default
+// (fused_merge_enabled): even so the launch's tail grows by more than the
+// merge launch costs.  The
+// arithmetic is attn_merge_kernel's, term for term (same bits):
+//   m* = max m_c, l = sum l_c 2^(m_c-m*) (in blocks of kMergeMaxChunks,
+//   rescaled between blocks), o = sum o_c 2^(m_c-m*) / (l + 1e-6).
+// flag: an LDS word no thread reads or writes at the call.
+constexpr int kMergeMaxChunks = 64;
+
+template <int D, int R, int NT>
+__device__ __forceinline__ void fused_merge(int *counter, int *flag, const float *part_o,
+                                            const float *part_ml, __half *out, int Hq, int b,
+                                            int row0, int pb0, int nch) {
+    __builtin_amdgcn_s_waitcnt(kVmcntAll); // this wave's partial stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const bool last =
+            __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    const int64_t cs_ml = (int64_t)Hq * 2, cs_o = (int64_t)Hq * D; // chunk strides
+    for (int idx = threadIdx.x; idx < R * D; idx += NT) {
+        const int    h = idx / D, d = idx - h * D;
+        const float *ml = part_ml + ((int64_t)pb0 * Hq + row0 + h) * 2;
+        const float *po = part_o + ((int64_t)pb0 * Hq + row0 + h) * D + d;
+        float        mx = -INFINITY, l = 0.0f;
+        for (int c0 = 0; c0 < nch; c0 += kMergeMaxChunks) {
+            const int cn = min(kMergeMaxChunks, nch - c0);
+            float     mnew = mx;
+            for (int c = c0; c < c0 + cn; ++c) mnew = fmaxf(mnew, ml[c * cs_ml]);
+            l = c0 ? l * __builtin_amdgcn_exp2f(mx - mnew) : 0.0f;
+            for (int c = c0; c < c0 + cn; ++c)
+                l = fmaf(__builtin_amdgcn_exp2f(ml[c * cs_ml] - mnew), ml[c * cs_ml + 1], l);
+            mx = mnew;
+        }
+        float o = 0.0f;
+#pragma unroll 8
+        for (int c = 0; c < nch; ++c) o = fmaf(__builtin_amdgcn_exp2f(ml[c * cs_ml] - mx), po[c * cs_o], o);
+        out[((int64_t)b * Hq + row0 + h) * D + d] = __float2half(o * (1.0f / (l + 1e-6f)));
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------------ kernel
 template <int D, int G, bool PAGED, bool MFMA, int kNW, int HPW, int VBO = 0>
 __global__ __launch_bounds__(kNW * 64)
@@ -1052,6 +1115,11 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU))) void attn_decode_kernel(AttnAr
             }
         }
     }
+    if (a.counters && nch > 1) { // the workgroup's kv heads: g (per head), hb * HPW .. + HPW - 1
+        const int gh0 = HF ? hb * HPW : g;
+        fused_merge<D, H1 * G, kThreads>(a.counters + (int64_t)b * a.Hkv + gh0, reinterpret_cast<int *>(sm),
+                                         a.part_o, a.part_ml, a.out, a.Hq, b, gh0 * G, widx - c, nch);
+    }
 }
 
 // ----------------------------------------------------------------- MMA path
@@ -1274,6 +1342,9 @@ __global__ __launch_bounds__(kNW * 64) void attn_decode_mma_kernel(AttnArgs a) {
             }
         }
     }
+    if (a.counters && nch > 1)
+        fused_merge<D, G, kThreads>(a.counters + (int64_t)b * a.Hkv + g, reinterpret_cast<int *>(sm_m), a.part_o,
+                                    a.part_ml, a.out, a.Hq, b, g * G, widx - c, nch);
 }
 
 struct MergeArgs {
@@ -1286,8 +1357,6 @@ struct MergeArgs {
     int            Hkv;
     InlineMeta     meta; // part_base from here when meta.n > 0
 };
-
-constexpr int kMergeMaxChunks = 64;
 
 // One workgroup per (entry b, kv head g): log-sum-exp merge of the chunk
 // partials of the G query heads,
@@ -1618,10 +1687,29 @@ void plan_work(const int32_t *lens, int n, int num_kv_heads, int head_dim, WorkL
                    planner_head_fuse(head_dim), out);
 }
 
+// Merge placement: -1 until first use, then 1 (in the attention launch) or
+// 0 (attn_merge_kernel, the default: the merging workgroups' device-scope
+// fences and partial reads at the end of the launch cost more than the
+// second launch, 99.2 against 92.2 + 4.7 us per cfg2 layer);
+// TL_ATTN_MERGE=fused gives 1 at first use.
+std::atomic<int> g_fused_merge{-1};
+
+bool fused_merge_enabled() {
+    int v = g_fused_merge.load(std::memory_order_relaxed);
+    if (v < 0) {
+        const char *e = std::getenv("TL_ATTN_MERGE");
+        v = e && std::strcmp(e, "fused") == 0 ? 1 : 0;
+        g_fused_merge.store(v);
+    }
+    return v != 0;
+}
+
+void set_fused_merge(bool on) { g_fused_merge.store(on ? 1 : 0); }
+
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
                         int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
                         const __half *new_v, hipStream_t stream, const InlineMeta *inl,
-                        bool hooks) {
+                        bool hooks, int *counters) {
     const int G = Hq / Hkv;
     if (plan.n_work <= 0 && !plan.any_empty) return;
     const bool paged = kv.block_table != nullptr;
@@ -1663,6 +1751,10 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
     args.scale_log2 = scale * 1.4426950408889634f;
     if (inl) std::memcpy(&args.meta, inl, sizeof(InlineMeta));
     else args.meta.n = 0;
+    // Merge inside the attention launch when every entry has work items (an
+    // entry with none gets its zero rows from attn_merge_kernel).
+    const bool fuse = counters && plan.any_multi && !plan.any_empty && fused_merge_enabled();
+    args.counters = fuse ? counters : nullptr;
 
     if (plan.n_work > 0 && !hf && use_mma_path(D, G)) {
         const int nw = waves_for((int64_t)plan.n_work * Hkv);
@@ -1687,7 +1779,7 @@ void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan,
         if (hooks) profile_end(KernelId::AttnChunk, stream);
     }
 
-    if (plan.any_multi || plan.any_empty) {
+    if ((plan.any_multi || plan.any_empty) && !fuse) {
         MergeArgs m;
         m.part_o = args.part_o;
         m.part_ml = args.part_ml;

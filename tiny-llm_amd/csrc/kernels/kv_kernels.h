@@ -81,10 +81,17 @@ bool attn_shape_supported(int D, int G);
 // seq_lens / work / part_base pointers of plan and kv.seq_row are not read.
 // hooks = false: no tl_profile_* event hooks around the launches (the
 // no-allocation entry point).
+// counters (optional): attn_counters_ints() ints, zero before the call (and
+// left zero by it): with fused_merge_enabled(), a multi-chunk plan without
+// empty entries then merges the partials inside the attention launch instead
+// of a second launch.
 void launch_attn_decode(const __half *q, const KvView &kv, const AttnPlan &plan, int B, int Hq,
                         int Hkv, int D, float scale, __half *out, float *part, const __half *new_k,
                         const __half *new_v, hipStream_t stream, const InlineMeta *inl = nullptr,
-                        bool hooks = true);
+                        bool hooks = true, int *counters = nullptr);
+
+// Merge counters (ints) launch_attn_decode uses for B entries of Hkv kv heads.
+inline size_t attn_counters_ints(int B, int Hkv) { return (size_t)B * (size_t)Hkv; }
 
 // Argument checks shared by the view-based decode entry points: "" when the
 // call is valid, else the reason, prefixed by `who`.
@@ -147,6 +154,11 @@ int  waves();
 // heads per workgroup where a plan with it applies.
 void set_head_fuse(int mode);
 int  head_fuse();
+// Merge of multi-chunk plans inside the attention launch (true) or by
+// attn_merge_kernel (false, the default); initial value from TL_ATTN_MERGE
+// ("fused": true).
+void set_fused_merge(bool on);
+bool fused_merge_enabled();
 // The head_fuse argument plan_work passes to plan_work_list for this
 // head_dim under the current settings (head-fuse mode, waves, score path):
 // 0 = per-head plans only, 1 = auto, 2 / 4 / 8 = forced heads per workgroup.

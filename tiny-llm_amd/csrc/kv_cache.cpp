@@ -659,11 +659,14 @@ Result<void> DecodeBatch::run_attention(int layer_idx, const half *q, const half
     plan.fused_heads = fused_heads_;
     plan.fused_chunked = fused_chunked_;
     float *part = nullptr;
-    if (any_multi_)
+    int   *cnt = nullptr;
+    if (any_multi_) {
         part = work_->get(detail::attn_workspace_floats(n_work_, num_q_heads_, cfg.head_dim));
+        cnt = work_->counters(detail::attn_counters_ints(n_, cfg.num_heads), stream);
+    }
     detail::launch_attn_decode(q, mgr_.layerView(layer_idx, d_slot_), plan, n_, num_q_heads_,
                                cfg.num_heads, cfg.head_dim, scale, out, part, new_k, new_v, stream,
-                               inline_ok_ ? inl_.get() : nullptr);
+                               inline_ok_ ? inl_.get() : nullptr, true, cnt);
     return Result<void>::ok();
 }
 

@@ -151,9 +151,25 @@ void *MetaRing::commit(hipStream_t stream) {
 
 // --------------------------------------------------------------- Workspace
 Workspace::~Workspace() {
-    if (!retired_.empty()) (void)hipDeviceSynchronize();
+    if (!retired_.empty() || !retired_cnt_.empty()) (void)hipDeviceSynchronize();
     for (float *p : retired_) (void)hipFree(p);
     if (ptr_) (void)hipFree(ptr_);
+    for (int *p : retired_cnt_) (void)hipFree(p);
+    if (cnt_) (void)hipFree(cnt_);
+}
+
+int *Workspace::counters(size_t n, hipStream_t stream) {
+    if (n > cnt_cap_) {
+        size_t cap = 1024;
+        while (cap < n) cap <<= 1;
+        int *p = nullptr;
+        HIP_CHECK(hipMalloc(&p, cap * sizeof(int)));
+        HIP_CHECK(hipMemsetAsync(p, 0, cap * sizeof(int), stream));
+        if (cnt_) retired_cnt_.push_back(cnt_); // may still be counted in by queued kernels
+        cnt_ = p;
+        cnt_cap_ = cap;
+    }
+    return cnt_;
 }
 
 float *Workspace::get(size_t floats) {

@@ -58,11 +58,19 @@ class Workspace {
     Workspace(const Workspace &) = delete;
     Workspace &operator=(const Workspace &) = delete;
     float *get(size_t floats);
+    // Grow-only ints that are zero between uses (the attention merge
+    // counters: the kernels that count in them leave them zero).  A new
+    // buffer is cleared on `stream`, ahead of whatever is queued there after
+    // this call.
+    int *counters(size_t n, hipStream_t stream);
 
   private:
     float              *ptr_ = nullptr;
     size_t              cap_ = 0;
     std::vector<float *> retired_; // replaced buffers, freed with the workspace
+    int                *cnt_ = nullptr;
+    size_t              cnt_cap_ = 0;
+    std::vector<int *>  retired_cnt_;
 };
 
 // Staging + workspace of the stateless entry points, one per device.

@@ -164,6 +164,8 @@ def _declare(L: C.CDLL) -> None:
         "tl_attn_get_waves": (i, []),
         "tl_attn_set_head_fuse": (i, [i]),
         "tl_attn_get_head_fuse": (i, []),
+        "tl_attn_set_fused_merge": (i, [i]),
+        "tl_attn_get_fused_merge": (i, []),
         "tl_fill_normal_f16": (i, [C.c_uint64, C.c_uint64, C.c_float, vp, sz, vp]),
         "tl_attn_plan": (i, [vp, i, i, i, i, i, i, i, i, C.POINTER(AttnPlanInfo), vp, vp]),
         "tl_profile_enable": (None, [i]),
@@ -498,6 +500,16 @@ def set_head_fuse(mode: int):
 
 def get_head_fuse() -> int:
     return load().tl_attn_get_head_fuse()
+
+
+def set_fused_merge(on: bool):
+    """Multi-chunk decode plans merge their partials in a second launch
+    (False, the default) or inside the attention launch (True); same bits."""
+    _check(load().tl_attn_set_fused_merge(1 if on else 0))
+
+
+def get_fused_merge() -> bool:
+    return bool(load().tl_attn_get_fused_merge())
 
 
 def set_prefill_waves(waves: int):
