@@ -1358,10 +1358,15 @@ struct MergeArgs {
     InlineMeta     meta; // part_base from here when meta.n > 0
 };
 
+// Entries of at most this many chunks take the single-round-trip merge.
+constexpr int kMergeFast = 8;
+
 // One workgroup per (entry b, kv head g): log-sum-exp merge of the chunk
 // partials of the G query heads,
 //   m* = max m_c, l = sum l_c 2^(m_c-m*), o = sum o_c 2^(m_c-m*) / (l+1e-6).
-// The chunk weights go through LDS; every thread then issues the o loads of
+// Up to kMergeFast chunks, each thread loads every chunk's (m, l) and o at
+// once and weighs them itself (one memory round trip); more chunks go
+// through LDS: the weights first, then every thread issues the o loads of
 // all chunks back to back.  Entries with no tokens get a zero row.
 template <int D, int G>
 __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
@@ -1385,6 +1390,38 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeArgs a) {
     if (nch == 1) return; // written by attn_decode_kernel
     if (nch == 0) {
         for (int i = threadIdx.x; i < G * D; i += 256) dst[i] = __float2half(0.0f);
+        return;
+    }
+    if (nch <= kMergeFast) {
+        // One memory round trip: every thread loads its head's (m, l) pairs
+        // and its o values of all chunks at once (indices clamped, unused
+        // terms dropped by selects) and computes the chunk weights itself --
+        // no LDS stage and no barrier.  The same terms in the same order as
+        // below, so the same bits.
+        for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+            const int    h = idx / D;
+            const float *ml = a.part_ml + ((int64_t)pb0 * a.Hq + (int64_t)g * G + h) * 2;
+            const float *po = a.part_o + ((int64_t)pb0 * a.Hq + (int64_t)g * G) * D + idx;
+            float2       mlc[kMergeFast];
+            float        pv[kMergeFast];
+#pragma unroll
+            for (int c = 0; c < kMergeFast; ++c) {
+                const int64_t cc = min(c, nch - 1);
+                mlc[c] = *reinterpret_cast<const float2 *>(ml + cc * a.Hq * 2);
+                pv[c] = po[cc * a.Hq * D];
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < kMergeFast; ++c) mx = c < nch ? fmaxf(mx, mlc[c].x) : mx;
+            float l = 0.0f, o = 0.0f;
+#pragma unroll
+            for (int c = 0; c < kMergeFast; ++c) {
+                const float wgt = __builtin_amdgcn_exp2f(mlc[c].x - mx);
+                l = c < nch ? fmaf(wgt, mlc[c].y, l) : l;
+                o = c < nch ? fmaf(wgt, pv[c], o) : o;
+            }
+            dst[idx] = __float2half(o * (1.0f / (l + 1e-6f)));
+        }
         return;
     }
     const int w0 = pb0;
