@@ -69,7 +69,9 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
             plan.fused_heads = wl.fused_heads;
             plan.fused_chunked = wl.fused_chunked;
             float *part = wl.any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
-            int   *cnt = wl.any_multi ? ctx.ws.counters(attn_counters_ints(B, Hkv), stream) : nullptr;
+            int   *cnt = wl.any_multi && fused_merge_enabled()
+                                 ? ctx.ws.counters(attn_counters_ints(B, Hkv), stream)
+                                 : nullptr;
             launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, nullptr, nullptr, stream,
                                &inl, true, cnt);
             return "";
@@ -97,7 +99,9 @@ std::string attn_decode_view(const __half *q, const KvView &kv, const int32_t *s
     plan.fused_heads = wl.fused_heads;
     plan.fused_chunked = wl.fused_chunked;
     float *part = wl.any_multi ? ctx.ws.get(attn_workspace_floats(n_work, Hq, D)) : nullptr;
-    int   *cnt = wl.any_multi ? ctx.ws.counters(attn_counters_ints(B, Hkv), stream) : nullptr;
+    int   *cnt = wl.any_multi && fused_merge_enabled()
+                         ? ctx.ws.counters(attn_counters_ints(B, Hkv), stream)
+                         : nullptr;
     launch_attn_decode(q, kv, plan, B, Hq, Hkv, D, scale, out, part, nullptr, nullptr, stream, nullptr,
                        true, cnt);
     return "";
@@ -129,7 +133,8 @@ std::string attn_decode_compact(const __half *q, const __half *k, const __half *
     std::lock_guard<std::mutex> lk(ctx.mu);
     ctx.claim(stream);
     float *part = plan.any_multi ? ctx.ws.get(attn_workspace_floats(plan.n_work, H, D)) : nullptr;
-    int   *cnt = plan.any_multi ? ctx.ws.counters(attn_counters_ints(B, H), stream) : nullptr;
+    int   *cnt = plan.any_multi && fused_merge_enabled() ? ctx.ws.counters(attn_counters_ints(B, H), stream)
+                                                        : nullptr;
     launch_attn_decode(q, kv, plan, B, H, H, D, scale, out, part, nullptr, nullptr, stream, nullptr, true,
                        cnt);
     return "";

@@ -662,7 +662,8 @@ Result<void> DecodeBatch::run_attention(int layer_idx, const half *q, const half
     int   *cnt = nullptr;
     if (any_multi_) {
         part = work_->get(detail::attn_workspace_floats(n_work_, num_q_heads_, cfg.head_dim));
-        cnt = work_->counters(detail::attn_counters_ints(n_, cfg.num_heads), stream);
+        if (detail::fused_merge_enabled()) // only the in-launch merge counts in them
+            cnt = work_->counters(detail::attn_counters_ints(n_, cfg.num_heads), stream);
     }
     detail::launch_attn_decode(q, mgr_.layerView(layer_idx, d_slot_), plan, n_, num_q_heads_,
                                cfg.num_heads, cfg.head_dim, scale, out, part, new_k, new_v, stream,
